@@ -1,0 +1,48 @@
+// cm_internal.h -- shared declarations of the gfx950 kernel library (not public).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/cormorant_amd.h"   // error codes, pool types
+
+// VectorOP opcodes (kernels/vectorop/include/VectorOP.h:50-57); any other value copies a.
+enum {
+    CM_OP_ADD = 0,
+    CM_OP_SUB = 1,
+    CM_OP_MUL = 2,
+    CM_OP_DIV = 3,
+    CM_OP_RELU = 4,
+    CM_OP_RELU6 = 5,
+    CM_OP_COPY = 6,
+};
+
+
+int cm_set_error(int code, const char* fmt, ...);
+int cm_check_launch(const char* what);
+
+inline uint64_t cm_grid_blocks(uint64_t work, uint32_t threads, uint64_t cap = 1u << 20) {
+    uint64_t b = (work + threads - 1) / threads;
+    if (b == 0) b = 1;
+    return b > cap ? cap : b;
+}
+
+int cm_vectorop_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t size,
+                       uint32_t op, uint32_t outer, uint32_t a_inc, uint32_t b_inc,
+                       hipStream_t s);
+int cm_div_sweep_launch(uint32_t b_lo, uint32_t b_count, unsigned long long* out,
+                        hipStream_t s);
+int cm_pool_launch(const int16_t* x, int16_t* y, uint32_t batch, uint32_t ch, uint32_t in_h,
+                   uint32_t in_w, uint32_t out_h, uint32_t out_w, uint32_t ph, uint32_t pw,
+                   uint32_t sh, uint32_t sw, uint32_t pad_top, uint32_t pad_left, uint32_t dh,
+                   uint32_t dw, uint32_t pool_type, uint32_t lp_order, uint32_t cip,
+                   hipStream_t s);
+int cm_finalize_sweep_launch(uint32_t mode, uint32_t lo, uint32_t count, uint32_t d,
+                             unsigned long long* checksum, hipStream_t s);
+int cm_matmul_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
+                     uint32_t m, uint32_t batch, uint32_t a_bs, uint32_t b_bs, uint32_t c_bs,
+                     hipStream_t s);
+int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
+                   uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                   uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
+                   uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
+                   uint32_t pad_left, uint32_t has_bias, uint32_t is_dw, hipStream_t s);

@@ -1,0 +1,491 @@
+// gemm.hip -- exact Q8.8 GEMM and implicit-GEMM convolution on gfx950 int8 MFMA.
+//
+// Reference arithmetic (kernels/matmul/kernel/MatmulKernel.cpp:196-218,
+// kernels/conv/kernel/ConvKernel.cpp:160-169, 231-249, 333):
+//     acc = wrap32( [bias << 8] + sum_k a_k * b_k ),   out = sat16(acc >> 8)
+// with int16 operands and an ap_fixed<32,16> accumulator that wraps mod 2^32.
+//
+// Limb decomposition.  Every int16 v splits into a signed high byte and an
+// offset low byte, both int8:
+//     vh = v >> 8,   vl = (v & 255) - 128,   v = 256*vh + vl + 128.
+// With A' = a - 128 = 256*ah + al and B' = b - 128 = 256*bh + bl,
+//     sum a*b = 65536*S_hh + 256*S_mid + S_ll + 128*(sum_k a + sum_k b) - 16384*Kp
+// where S_hh = sum ah*bh, S_mid = sum (ah*bl + al*bh), S_ll = sum al*bl are
+// int8 x int8 -> int32 MFMA sums over the Kp (zero-padded) k positions, and
+// the row sums of A / column sums of B are gathered while tiles are loaded.
+// Every term is taken modulo 2^32, which is exactly the accumulator's wrap,
+// so the result is bit-identical to the reference for any inputs.  |S_mid|
+// grows by at most 2^15 per k, so MFMA partials are folded into a uint32
+// total every 32768 k when K is larger than that (never overflow int32).
+//
+// Tiling: 256 threads (4 waves, 2x2), block tile 128 rows x 128 cols x 64 k,
+// wave tile 64x64 = 4x4 MFMA 16x16x64 tiles, 3 accumulator sets (hh, mid, ll).
+// Tiles are split into limbs while being stored to LDS (rows of 64 int8 k
+// values, padded to 80 B so the 16 lanes of a fragment read hit distinct
+// banks).  The next tile's global loads are issued before the MFMA phase.
+#include <type_traits>
+
+#include "cm_internal.h"
+#include "q88.h"
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int BM = 128, BN = 128, BK = 64;
+constexpr int kThreads = 256;
+constexpr int kStride = 80;          // LDS bytes per row of 64 int8 (k) values
+constexpr int kFoldIters = 512;      // fold MFMA partials every 512*64 = 32768 k
+
+struct GemmArgs {
+    const int16_t* a;     // [rows][k], row stride lda (weights for conv)
+    const int16_t* b;     // dense: [k][cols], row stride ldb; conv: x (NCHW)
+    int16_t* c;           // dense: [rows][cols], row stride ldc; conv: y (NCHW)
+    const int16_t* bias;  // [rows] or null
+    uint32_t rows, cols, k;
+    uint64_t lda, ldb, ldc;
+    uint64_t a_bs, b_bs, c_bs;   // per blockIdx.z (dense only)
+    uint32_t a_vec, b_vec;       // 16-byte loads allowed
+    // implicit GEMM: column = n*P + p, k = (c*kh + khi)*kw + kwi
+    uint32_t C, H, W, OW, P, kh, kw, sh, sw, dh, dw, pt, pl;
+    uint64_t x_img, y_img;
+};
+
+// Split four int16 values held in two words into a word of high bytes and a
+// word of offset low bytes (value order preserved, low byte first).
+__device__ __forceinline__ void split4(uint32_t w0, uint32_t w1, uint32_t& hi, uint32_t& lo) {
+    hi = ((w0 >> 8) & 0xFFu) | ((w0 >> 16) & 0xFF00u) | ((w1 << 8) & 0xFF0000u) |
+         (w1 & 0xFF000000u);
+    lo = ((w0 & 0xFFu) | ((w0 >> 8) & 0xFF00u) | ((w1 << 16) & 0xFF0000u) |
+          ((w1 << 8) & 0xFF000000u)) ^ 0x80808080u;
+}
+
+__device__ __forceinline__ int32_t wsum(uint32_t w) {
+    return (int32_t)(int16_t)(w & 0xFFFFu) + (int32_t)(int16_t)(w >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack2(int16_t lo, int16_t hi) {
+    return (uint32_t)(uint16_t)lo | ((uint32_t)(uint16_t)hi << 16);
+}
+
+struct Smem {
+    uint8_t a_hi[BM * kStride];
+    uint8_t a_lo[BM * kStride];
+    uint8_t b_hi[BN * kStride];
+    uint8_t b_lo[BN * kStride];
+    uint32_t row_sum[BM];
+    uint32_t col_sum[BN];
+};
+
+// ---------------------------------------------------------------- A tile --
+// Thread t owns row t/2 and k values [32*(t&1), +32) of the 64-k slice.
+struct ATile {
+    uint32_t w[16];
+    __device__ __forceinline__ void load(const GemmArgs& g, const int16_t* abase, uint32_t row0,
+                                         uint32_t k0) {
+        const uint32_t r = row0 + (threadIdx.x >> 1);
+        const uint32_t ks = k0 + (threadIdx.x & 1) * 32;
+        if (g.a_vec) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                v4i v = {0, 0, 0, 0};
+                if (r < g.rows && ks + q * 8 < g.k)
+                    v = *reinterpret_cast<const v4i*>(abase + (uint64_t)r * g.lda + ks + q * 8);
+                w[4 * q + 0] = v[0]; w[4 * q + 1] = v[1]; w[4 * q + 2] = v[2]; w[4 * q + 3] = v[3];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                int16_t v0 = 0, v1 = 0;
+                if (r < g.rows) {
+                    const int16_t* p = abase + (uint64_t)r * g.lda;
+                    if (ks + 2 * j < g.k) v0 = p[ks + 2 * j];
+                    if (ks + 2 * j + 1 < g.k) v1 = p[ks + 2 * j + 1];
+                }
+                w[j] = pack2(v0, v1);
+            }
+        }
+    }
+    __device__ __forceinline__ void store(Smem& s, uint32_t& row_sum) const {
+        const uint32_t off = (threadIdx.x >> 1) * kStride + (threadIdx.x & 1) * 32;
+        uint32_t hi[8], lo[8];
+        int32_t sum = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            split4(w[2 * j], w[2 * j + 1], hi[j], lo[j]);
+            sum += wsum(w[2 * j]) + wsum(w[2 * j + 1]);
+        }
+        row_sum += (uint32_t)sum;
+        v4i* dh = reinterpret_cast<v4i*>(s.a_hi + off);
+        v4i* dl = reinterpret_cast<v4i*>(s.a_lo + off);
+        dh[0] = v4i{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        dh[1] = v4i{(int)hi[4], (int)hi[5], (int)hi[6], (int)hi[7]};
+        dl[0] = v4i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
+        dl[1] = v4i{(int)lo[4], (int)lo[5], (int)lo[6], (int)lo[7]};
+    }
+};
+
+// ---------------------------------------------------------- dense B tile --
+// Thread t owns columns [8*(t&15), +8) and k rows [4*(t>>4), +4).
+struct DenseBTile {
+    uint32_t w[4][4];   // [k row][word of 2 columns]
+    uint32_t col_sum[8];
+
+    __device__ __forceinline__ void init() {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) col_sum[j] = 0;
+    }
+    __device__ __forceinline__ void load(const GemmArgs& g, const int16_t* bbase, uint32_t col0,
+                                         uint32_t k0) {
+        const uint32_t cb = col0 + (threadIdx.x & 15) * 8;
+        const uint32_t kb = k0 + (threadIdx.x >> 4) * 4;
+        if (g.b_vec) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                v4i v = {0, 0, 0, 0};
+                if (kb + i < g.k && cb < g.cols)
+                    v = *reinterpret_cast<const v4i*>(bbase + (uint64_t)(kb + i) * g.ldb + cb);
+                w[i][0] = v[0]; w[i][1] = v[1]; w[i][2] = v[2]; w[i][3] = v[3];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bool kok = kb + i < g.k;
+                const int16_t* p = bbase + (uint64_t)(kb + i) * g.ldb;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    int16_t v0 = 0, v1 = 0;
+                    if (kok && cb + 2 * q < g.cols) v0 = p[cb + 2 * q];
+                    if (kok && cb + 2 * q + 1 < g.cols) v1 = p[cb + 2 * q + 1];
+                    w[i][q] = pack2(v0, v1);
+                }
+            }
+        }
+    }
+    __device__ __forceinline__ void store(Smem& s) {
+        const uint32_t cl = (threadIdx.x & 15) * 8;
+        const uint32_t kbyte = (threadIdx.x >> 4) * 4;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int sh = (j & 1) * 16;
+            const int16_t v0 = (int16_t)(w[0][j >> 1] >> sh), v1 = (int16_t)(w[1][j >> 1] >> sh);
+            const int16_t v2 = (int16_t)(w[2][j >> 1] >> sh), v3 = (int16_t)(w[3][j >> 1] >> sh);
+            uint32_t hi, lo;
+            split4(pack2(v0, v1), pack2(v2, v3), hi, lo);
+            col_sum[j] += (uint32_t)((int32_t)v0 + v1 + v2 + v3);
+            *reinterpret_cast<uint32_t*>(s.b_hi + (cl + j) * kStride + kbyte) = hi;
+            *reinterpret_cast<uint32_t*>(s.b_lo + (cl + j) * kStride + kbyte) = lo;
+        }
+    }
+    __device__ __forceinline__ void publish_sums(Smem& s) const {
+        const uint32_t cl = (threadIdx.x & 15) * 8;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) atomicAdd(&s.col_sum[cl + j], col_sum[j]);
+    }
+};
+
+// ------------------------------------------------------- im2col B tile --
+// Thread t owns column (pixel) t&127 and k values [32*(t>>7), +32).
+struct ConvBTile {
+    uint32_t w[16];
+    uint32_t col_sum;
+    const int16_t* xb;   // image base of this thread's column
+    int32_t ih0, iw0;
+    bool col_ok;
+
+    __device__ __forceinline__ void init(const GemmArgs& g, uint32_t col0) {
+        col_sum = 0;
+        const uint32_t col = col0 + (threadIdx.x & 127);
+        col_ok = col < g.cols;
+        const uint32_t n = col_ok ? col / g.P : 0;
+        const uint32_t p = col_ok ? col - n * g.P : 0;
+        const uint32_t oh = p / g.OW, ow = p - (p / g.OW) * g.OW;
+        ih0 = (int32_t)(oh * g.sh) - (int32_t)g.pt;
+        iw0 = (int32_t)(ow * g.sw) - (int32_t)g.pl;
+        xb = g.b + (uint64_t)n * g.x_img;
+    }
+    __device__ __forceinline__ void load(const GemmArgs& g, uint32_t k0) {
+        const uint32_t ks = k0 + (threadIdx.x >> 7) * 32;
+        const uint32_t kk = g.kh * g.kw;
+        uint32_t c = ks / kk;
+        uint32_t r = ks - c * kk;
+        uint32_t khi = r / g.kw;
+        uint32_t kwi = r - khi * g.kw;
+        const uint32_t hw = g.H * g.W;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            int16_t v[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                v[e] = 0;
+                const int32_t ih = ih0 + (int32_t)(khi * g.dh);
+                const int32_t iw = iw0 + (int32_t)(kwi * g.dw);
+                if (col_ok && ks + 2 * j + e < g.k && ih >= 0 && ih < (int32_t)g.H && iw >= 0 &&
+                    iw < (int32_t)g.W)
+                    v[e] = xb[c * hw + (uint32_t)ih * g.W + (uint32_t)iw];
+                if (++kwi == g.kw) {
+                    kwi = 0;
+                    if (++khi == g.kh) { khi = 0; ++c; }
+                }
+            }
+            w[j] = pack2(v[0], v[1]);
+        }
+    }
+    __device__ __forceinline__ void store(Smem& s) {
+        const uint32_t off = (threadIdx.x & 127) * kStride + (threadIdx.x >> 7) * 32;
+        uint32_t hi[8], lo[8];
+        int32_t sum = 0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            split4(w[2 * j], w[2 * j + 1], hi[j], lo[j]);
+            sum += wsum(w[2 * j]) + wsum(w[2 * j + 1]);
+        }
+        col_sum += (uint32_t)sum;
+        v4i* dh = reinterpret_cast<v4i*>(s.b_hi + off);
+        v4i* dl = reinterpret_cast<v4i*>(s.b_lo + off);
+        dh[0] = v4i{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+        dh[1] = v4i{(int)hi[4], (int)hi[5], (int)hi[6], (int)hi[7]};
+        dl[0] = v4i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
+        dl[1] = v4i{(int)lo[4], (int)lo[5], (int)lo[6], (int)lo[7]};
+    }
+    __device__ __forceinline__ void publish_sums(Smem& s) const {
+        atomicAdd(&s.col_sum[threadIdx.x & 127], col_sum);
+    }
+};
+
+template <bool CONV, bool HAS_BIAS, bool FOLD>
+__global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
+    __shared__ __align__(16) Smem s;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t row0 = blockIdx.y * BM;
+    const uint32_t col0 = blockIdx.x * BN;
+    const uint32_t wrow = (wave >> 1) * 64, wcol = (wave & 1) * 64;
+
+    const int16_t* abase = g.a + (CONV ? 0 : (uint64_t)blockIdx.z * g.a_bs);
+    const int16_t* bbase = g.b + (CONV ? 0 : (uint64_t)blockIdx.z * g.b_bs);
+
+    if (threadIdx.x < BN) s.col_sum[threadIdx.x] = 0;   // published with atomics at the end
+    __syncthreads();
+
+    ATile at;
+    typename std::conditional<CONV, ConvBTile, DenseBTile>::type bt;
+    uint32_t row_sum = 0;
+    if constexpr (CONV) bt.init(g, col0); else bt.init();
+
+    v4i hh[4][4], mid[4][4], ll[4][4], tot[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            hh[i][j] = v4i{0, 0, 0, 0}; mid[i][j] = v4i{0, 0, 0, 0}; ll[i][j] = v4i{0, 0, 0, 0};
+            if constexpr (FOLD) tot[i][j] = v4i{0, 0, 0, 0};
+        }
+
+    const uint32_t nk = (g.k + BK - 1) / BK;
+    at.load(g, abase, row0, 0);
+    if constexpr (CONV) bt.load(g, 0); else bt.load(g, bbase, col0, 0);
+
+    for (uint32_t it = 0; it < nk; ++it) {
+        __syncthreads();                 // previous tile fully consumed
+        at.store(s, row_sum);
+        bt.store(s);
+        __syncthreads();
+        if (it + 1 < nk) {               // next tile's loads overlap the MFMAs below
+            at.load(g, abase, row0, (it + 1) * BK);
+            if constexpr (CONV) bt.load(g, (it + 1) * BK); else bt.load(g, bbase, col0, (it + 1) * BK);
+        }
+        v4i ah[4], al[4], bh[4], bl[4];
+        const uint32_t koff = (lane >> 4) * 16;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t r = (wrow + i * 16 + (lane & 15)) * kStride + koff;
+            ah[i] = *reinterpret_cast<const v4i*>(s.a_hi + r);
+            al[i] = *reinterpret_cast<const v4i*>(s.a_lo + r);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t cidx = (wcol + j * 16 + (lane & 15)) * kStride + koff;
+            bh[j] = *reinterpret_cast<const v4i*>(s.b_hi + cidx);
+            bl[j] = *reinterpret_cast<const v4i*>(s.b_lo + cidx);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                hh[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bh[j], hh[i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                mid[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bl[j], mid[i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                mid[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], bh[j], mid[i][j], 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                ll[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], bl[j], ll[i][j], 0, 0, 0);
+
+        if constexpr (FOLD) {
+            if ((it + 1) % kFoldIters == 0) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            tot[i][j][e] = (int)((uint32_t)tot[i][j][e] + ((uint32_t)hh[i][j][e] << 16) +
+                                                 ((uint32_t)mid[i][j][e] << 8) + (uint32_t)ll[i][j][e]);
+                        hh[i][j] = v4i{0, 0, 0, 0}; mid[i][j] = v4i{0, 0, 0, 0}; ll[i][j] = v4i{0, 0, 0, 0};
+                    }
+            }
+        }
+    }
+
+    // row sums: the two threads of a row are adjacent lanes
+    row_sum += (uint32_t)__shfl_xor((int)row_sum, 1, 64);
+    if ((threadIdx.x & 1) == 0) s.row_sum[threadIdx.x >> 1] = row_sum;
+    bt.publish_sums(s);
+    __syncthreads();
+
+    const uint32_t kp_term = 16384u * (nk * (uint32_t)BK);
+    int16_t* cptr = g.c + (CONV ? 0 : (uint64_t)blockIdx.z * g.c_bs);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t cl = wcol + j * 16 + (lane & 15);
+        const uint32_t col = col0 + cl;
+        if (col >= g.cols) continue;
+        uint64_t coff;
+        uint64_t rstride;
+        if constexpr (CONV) {
+            const uint32_t n = col / g.P;
+            coff = (uint64_t)n * g.y_img + (col - n * g.P);
+            rstride = g.P;
+        } else {
+            coff = col;
+            rstride = g.ldc;
+        }
+        const uint32_t csum = s.col_sum[cl];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t rl = wrow + i * 16 + (lane >> 4) * 4 + e;
+                const uint32_t row = row0 + rl;
+                if (row >= g.rows) continue;
+                uint32_t v = ((uint32_t)hh[i][j][e] << 16) + ((uint32_t)mid[i][j][e] << 8) +
+                             (uint32_t)ll[i][j][e];
+                if constexpr (FOLD) v += (uint32_t)tot[i][j][e];
+                v += 128u * (s.row_sum[rl] + csum) - kp_term;
+                if constexpr (HAS_BIAS) v += (uint32_t)(int32_t)g.bias[row] << 8;
+                cptr[coff + (uint64_t)row * rstride] = q88::acc_to_data(v);
+            }
+        }
+    }
+}
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+template <bool CONV>
+int launch_gemm(GemmArgs& g, uint32_t zdim, hipStream_t s, const char* name) {
+    const dim3 grid((g.cols + BN - 1) / BN, (g.rows + BM - 1) / BM, zdim);
+    if (grid.y > 65535u || grid.z > 65535u || grid.x > 0x7FFFFFFFu)
+        return cm_set_error(CM_ERR_RANGE, "%s: grid too large", name);
+    const bool fold = g.k > (uint32_t)(kFoldIters * BK);
+    const bool bias = g.bias != nullptr;
+#define CM_GEMM_LAUNCH(B, F) \
+    hipLaunchKernelGGL((q88_gemm<CONV, B, F>), grid, dim3(kThreads), 0, s, g)
+    if (bias) { if (fold) CM_GEMM_LAUNCH(true, true); else CM_GEMM_LAUNCH(true, false); }
+    else { if (fold) CM_GEMM_LAUNCH(false, true); else CM_GEMM_LAUNCH(false, false); }
+#undef CM_GEMM_LAUNCH
+    return cm_check_launch(name);
+}
+
+}  // namespace
+
+int cm_matmul_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
+                     uint32_t m, uint32_t batch, uint32_t a_bs, uint32_t b_bs, uint32_t c_bs,
+                     hipStream_t s) {
+    if (batch == 0 || n == 0 || m == 0) return CM_OK;
+    GemmArgs g{};
+    g.a = a; g.b = b; g.c = c; g.bias = nullptr;
+    g.rows = n; g.cols = m; g.k = k;
+    g.lda = k; g.ldb = m; g.ldc = m;
+    g.a_bs = a_bs; g.b_bs = b_bs; g.c_bs = c_bs;
+    g.a_vec = aligned16(a) && k % 8 == 0 && a_bs % 8 == 0;
+    g.b_vec = aligned16(b) && m % 8 == 0 && b_bs % 8 == 0;
+    if (c_bs == 0 && batch > 1) {
+        // every batch step overwrites the same C; the sequential reference leaves the last one
+        g.a = a + (uint64_t)(batch - 1) * a_bs;
+        g.b = b + (uint64_t)(batch - 1) * b_bs;
+        g.a_vec = aligned16(g.a) && k % 8 == 0;
+        g.b_vec = aligned16(g.b) && m % 8 == 0;
+        batch = 1;
+    }
+    uint32_t done = 0;
+    while (done < batch) {   // grid.z is limited to 65535 batches per launch
+        const uint32_t z = (batch - done) > 65535u ? 65535u : (batch - done);
+        GemmArgs gz = g;
+        gz.a = g.a + (uint64_t)done * a_bs;
+        gz.b = g.b + (uint64_t)done * b_bs;
+        gz.c = g.c + (uint64_t)done * c_bs;
+        const int rc = launch_gemm<false>(gz, z, s, "matmul");
+        if (rc) return rc;
+        done += z;
+    }
+    return CM_OK;
+}
+
+int cm_conv_gemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
+                        uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                        uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
+                        uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
+                        uint32_t pad_left, hipStream_t s) {
+    const uint64_t P = (uint64_t)out_h * out_w;
+    const uint64_t K = (uint64_t)in_ch * kh * kw;
+    const uint64_t cols = P * batch;
+    const uint64_t x_img = (uint64_t)in_ch * in_h * in_w;
+    if (cols == 0 || out_ch == 0) return CM_OK;
+    if (cols > 0x7FFFFFFFull || K > 0x7FFFFFFFull || x_img > 0x7FFFFFFFull || P > 0x7FFFFFFFull)
+        return cm_set_error(CM_ERR_RANGE, "conv: shape exceeds 32-bit indexing");
+    GemmArgs g{};
+    g.a = w; g.b = x; g.c = y; g.bias = bias;
+    g.rows = out_ch; g.cols = (uint32_t)cols; g.k = (uint32_t)K;
+    g.lda = K;
+    g.a_vec = aligned16(w) && K % 8 == 0;
+    g.b_vec = 0;
+    g.C = in_ch; g.H = in_h; g.W = in_w; g.OW = out_w; g.P = (uint32_t)P;
+    g.kh = kh; g.kw = kw; g.sh = sh; g.sw = sw; g.dh = dh; g.dw = dw; g.pt = pad_top; g.pl = pad_left;
+    g.x_img = x_img;
+    g.y_img = (uint64_t)out_ch * P;
+    return launch_gemm<true>(g, 1, s, "conv_gemm");
+}
+
+int cm_conv_pointwise_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
+                             uint32_t batch, uint32_t in_ch, uint32_t out_ch, uint32_t hw,
+                             hipStream_t s) {
+    // 1x1, stride 1, no padding: y[n] = W[out_ch][in_ch] x X[n][in_ch][hw] (+ bias)
+    if (batch == 0 || out_ch == 0 || hw == 0) return CM_OK;
+    GemmArgs g{};
+    g.a = w; g.b = x; g.c = y; g.bias = bias;
+    g.rows = out_ch; g.cols = hw; g.k = in_ch;
+    g.lda = in_ch; g.ldb = hw; g.ldc = hw;
+    g.a_bs = 0; g.b_bs = (uint64_t)in_ch * hw; g.c_bs = (uint64_t)out_ch * hw;
+    g.a_vec = aligned16(w) && in_ch % 8 == 0;
+    g.b_vec = aligned16(x) && hw % 8 == 0 && g.b_bs % 8 == 0;
+    uint32_t done = 0;
+    while (done < batch) {
+        const uint32_t z = (batch - done) > 65535u ? 65535u : (batch - done);
+        GemmArgs gz = g;
+        gz.b = x + (uint64_t)done * g.b_bs;
+        gz.c = y + (uint64_t)done * g.c_bs;
+        const int rc = launch_gemm<false>(gz, z, s, "conv_pointwise");
+        if (rc) return rc;
+        done += z;
+    }
+    return CM_OK;
+}

@@ -1,0 +1,104 @@
+// q88.h -- exact ap_fixed<16,8> / ap_fixed<32,16> arithmetic for gfx950 kernels.
+//
+// Data:        int16 raw r, value r/256 (kernels/*/CMakeLists.txt Data_t default).
+// Accumulator: ap_fixed<32,16> raw bits carried in uint32 so that every "+="
+//              wraps modulo 2^32 (AP_WRAP), value raw/65536.
+// Output rule: saturate_cast<ap_fixed<16,8>> = AP_TRN floor (arithmetic >> 8
+//              of the accumulator raw) then AP_SAT clamp to [-32768, 32767]
+//              (kernels/vectorop/include/VectorOP.h:30-39).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace q88 {
+
+// IEEE binary32 round-to-nearest-even primitives.  The library is compiled
+// with -ffp-contract=off, so a product is never fused into an FMA; division
+// and square root lower to LLVM's correctly rounded fdiv / llvm.sqrt.f32
+// expansions (no approximate-math flags).  The parity tests sweep every
+// accumulator value of both finalisers against the host's float32 results.
+__device__ __forceinline__ float mul_rn(float x, float y) { return x * y; }
+__device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
+__device__ __forceinline__ float div_rn(float x, float y) { return x / y; }
+
+// PoolingKernel.cpp:137: inv_denom = denom > 0 ? 1.0f / (float)denom : 0.0f
+__device__ __forceinline__ float inv_denom(uint32_t d) {
+    return d > 0u ? div_rn(1.0f, (float)d) : 0.0f;
+}
+
+__device__ __forceinline__ int32_t sat16(int32_t v) {
+    return __builtin_elementwise_min(__builtin_elementwise_max(v, -32768), 32767);
+}
+
+// saturate_cast<Data_t>(AccData_t acc)
+__device__ __forceinline__ int16_t acc_to_data(uint32_t acc) {
+    return (int16_t)sat16(((int32_t)acc) >> 8);
+}
+
+// Data_t -> AccData_t (raw << 8)
+__device__ __forceinline__ uint32_t data_to_acc(int32_t x) { return (uint32_t)x << 8; }
+
+// VectorOP.cpp:8-14: sat16(a + b), sat16(a - b)
+__device__ __forceinline__ int32_t add(int32_t a, int32_t b) { return sat16(a + b); }
+__device__ __forceinline__ int32_t sub(int32_t a, int32_t b) { return sat16(a - b); }
+
+// VectorOP.cpp:17-19: full-precision product, AP_TRN floor of 8 bits, AP_SAT.
+__device__ __forceinline__ int32_t mul(int32_t a, int32_t b) { return sat16((a * b) >> 8); }
+
+// VectorOP.cpp:22-25: b == 0 -> 0, else sat16(trunc((a * 256) / b)).
+// The quotient estimate comes from v_rcp_f32 (relative error ~2^-23) and is
+// clamped to +-40000 (saturation is decided well outside that band); inside
+// the band the estimate is within 0.01 of the exact quotient, so one integer
+// remainder check moves it onto trunc(A/b) exactly.  Verified exhaustively
+// over all 2^32 (a, b) pairs against integer division.
+__device__ __forceinline__ int32_t div(int32_t a, int32_t b) {
+    if (b == 0) return 0;
+    const int32_t A = a * 256;
+    float qf = (float)A * __builtin_amdgcn_rcpf((float)b);
+    qf = __builtin_fminf(__builtin_fmaxf(qf, -40000.0f), 40000.0f);
+    int32_t q = (int32_t)qf;                      // truncation toward zero
+    const int32_t r = A - q * b;                  // |q * b| < 2^31
+    const int32_t s = ((A ^ b) < 0) ? -1 : 1;     // sign of the true quotient
+    if (r != 0 && ((r ^ A) < 0)) q -= s;          // overshot past trunc(A/b)
+    else if (__builtin_abs(r) >= __builtin_abs(b)) q += s;   // undershot
+    return sat16(q);
+}
+
+// VectorOP.cpp:27-35
+__device__ __forceinline__ int32_t relu(int32_t a) { return a < 0 ? 0 : a; }
+__device__ __forceinline__ int32_t relu6(int32_t a) {
+    return a < 0 ? 0 : (a > 1536 ? 1536 : a);
+}
+
+// (float)AccData_t: nearest-even rounding of raw, then exact scale by 2^-16.
+__device__ __forceinline__ float acc_to_float(uint32_t acc) {
+    return mul_rn((float)(int32_t)acc, 1.0f / 65536.0f);   // v_cvt_f32_i32 rounds to nearest even
+}
+
+// saturate_cast<Data_t>(AccData_t(f)): AccData_t(f) floors f to 2^-16 and wraps;
+// the >> 8 then floors to 2^-8.  For |f| < 32768 this is sat16(floor(f * 256)).
+// NaN / Inf (only reachable from a wrapped LP p=2 accumulator) give 0.
+__device__ __forceinline__ int16_t float_to_data(float f) {
+    if (!__builtin_isfinite(f)) return 0;
+    if (!(__builtin_fabsf(f) < 32768.0f)) {
+        // AP_WRAP of floor(f * 65536): keep the low 32 bits of the exact value.
+        const double s = __builtin_floor((double)f * 65536.0);
+        if (!(__builtin_fabs(s) < 9.2e18)) return 0;
+        return acc_to_data((uint32_t)(uint64_t)(int64_t)s);
+    }
+    const float s = __builtin_floorf(mul_rn(f, 256.0f));  // exact scale
+    return (int16_t)sat16((int32_t)s);
+}
+
+// PoolingKernel.cpp:137, 259, 265: AccData_t((float)acc * (1.0f / denom)).
+__device__ __forceinline__ int16_t avg_finalize(uint32_t acc, float inv_denom) {
+    return float_to_data(mul_rn(acc_to_float(acc), inv_denom));
+}
+
+// PoolingKernel.cpp:263, 265: AccData_t(sqrtf((float)acc)).
+__device__ __forceinline__ int16_t lp2_finalize(uint32_t acc) {
+    if ((int32_t)acc < 0) return 0;   // sqrt of a negative (wrapped) sum: NaN -> 0
+    return float_to_data(sqrt_rn(acc_to_float(acc)));
+}
+
+}  // namespace q88

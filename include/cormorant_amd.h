@@ -1,0 +1,175 @@
+/*
+ * cormorant_amd.h -- C ABI of the MI355X (gfx950) implementation of Cormorant's
+ * four Q8.8 inference kernels: VectorOPKernel, MatmulKernel, ConvKernel and
+ * PoolingKernel.
+ *
+ * Data: every tensor is int16 two's complement holding ap_fixed<16,8>
+ * (value = raw / 256), NCHW for conv/pool, row-major for matmul.  Results are
+ * bit-identical to the reference C-simulation kernels, including the 32-bit
+ * wrapping accumulator and the truncate-then-saturate output rule.
+ *
+ * Conventions
+ *   - Kernel entry points take DEVICE pointers and enqueue work on `stream`
+ *     (NULL = the library stream set by cm_set_stream, default stream 0); they
+ *     return as soon as the work is queued.  Results are visible after
+ *     cm_sync() or cm_buf_sync_from_device().  One in-order stream gives the
+ *     reference's strictly sequential node order.
+ *   - Every function returning int returns 0 on success and a negative CM_ERR_*
+ *     code otherwise; cm_last_error() describes the last failure of the
+ *     calling thread.  Where the reference has undefined behaviour (shapes
+ *     beyond its compile-time kMax* limits) this library computes the exact
+ *     result instead, or returns CM_ERR_RANGE if a size exceeds its indexing.
+ *   - The caller owns every buffer; kernels never allocate.
+ *
+ * Reference interfaces replaced (paths relative to the reference root):
+ *   kernels/vectorop/include/VectorOP.h:86-95        VectorOPKernel
+ *   kernels/matmul/include/MatmulKernel.h:68-79      MatmulKernel
+ *   kernels/conv/include/ConvKernel.h:79-101         ConvKernel
+ *   kernels/pool/include/PoolingKernel.h:63-83       PoolingKernel
+ *   inference-scheduler/src/codegen/_source.py:198-421  run_op / run_matmul /
+ *       run_matmul_at / run_conv / run_pool (generated C helpers)
+ *   inference-scheduler/bench_src/inference.h:12-38  inference_buf_* (DMA buffers)
+ */
+#ifndef CORMORANT_AMD_H
+#define CORMORANT_AMD_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Return codes. */
+#define CM_OK          0
+#define CM_ERR_INVALID (-1)  /* null pointer or inconsistent arguments */
+#define CM_ERR_HIP     (-2)  /* HIP runtime / launch failure */
+#define CM_ERR_RANGE   (-3)  /* size beyond the library's indexing */
+#define CM_ERR_NOMEM   (-4)  /* allocation failed */
+
+/* VectorOP opcodes: kernels/vectorop/include/VectorOP.h:50-57.
+ * Any other opcode copies a (kernels/vectorop/kernel/VectorOP.cpp:112). */
+#define CM_VECTOROP_ADD   0u
+#define CM_VECTOROP_SUB   1u
+#define CM_VECTOROP_MUL   2u
+#define CM_VECTOROP_DIV   3u
+#define CM_VECTOROP_RELU  4u
+#define CM_VECTOROP_RELU6 5u
+
+/* Pool types: kernels/pool/include/Config.h.in:40-42.  Any other value is Lp. */
+#define CM_POOL_MAX 0u
+#define CM_POOL_AVG 1u
+#define CM_POOL_LP  2u
+
+/* ------------------------------------------------------------------ kernels */
+
+/* VectorOPKernel (VectorOP.h:86-95):
+ *   c[o*(a_inc+b_inc) + i] = op(a[o*a_inc + i], b[o*b_inc + i]),
+ *   o < outer, i < size.  b may be NULL for op RELU/RELU6 (never read).
+ * Overlapping outputs of different outer steps keep the last step's value. */
+int cm_vectorop(const int16_t *a, const int16_t *b, int16_t *c, uint32_t size, uint32_t op,
+                uint32_t outer, uint32_t a_inc, uint32_t b_inc, hipStream_t stream);
+
+/* MatmulKernel (MatmulKernel.h:68-79): for bi < batch,
+ *   C_bi[n][m] = sat16(wrap32(sum_k A_bi[n][k] * B_bi[k][m]) >> 8)
+ * with A_bi = a + bi*a_stride, B_bi = b + bi*b_stride, C_bi = c + bi*c_stride
+ * (element strides; 0 broadcasts).  No limit on k (the reference's kMaxK=2048
+ * static buffer is not needed). */
+int cm_matmul(const int16_t *a, const int16_t *b, int16_t *c, uint32_t n, uint32_t k,
+              uint32_t m, uint32_t batch, uint32_t a_stride, uint32_t b_stride,
+              uint32_t c_stride, hipStream_t stream);
+
+/* run_matmul_at (_source.py:275-300): cm_matmul on a+a_off, b+b_off, c+c_off. */
+int cm_matmul_at(const int16_t *a, uint32_t a_off, const int16_t *b, uint32_t b_off,
+                 int16_t *c, uint32_t c_off, uint32_t n, uint32_t k, uint32_t m,
+                 uint32_t batch, uint32_t a_stride, uint32_t b_stride, uint32_t c_stride,
+                 hipStream_t stream);
+
+/* ConvKernel (ConvKernel.h:79-101): NCHW, weights [out_ch][in_ch][kh][kw]
+ * (depthwise: [out_ch][1][kh][kw], output channel m reads input channel m),
+ * bias [out_ch] (NULL allowed when has_bias == 0), pad_bottom/right implicit.
+ * Depthwise requires out_ch <= in_ch. */
+int cm_conv(const int16_t *x, const int16_t *weight, const int16_t *bias, int16_t *y,
+            uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
+            uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
+            uint32_t stride_w, uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
+            uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise, hipStream_t stream);
+
+/* PoolingKernel (PoolingKernel.h:63-83): MAX / AVG / LP(lp_order 1, else 2),
+ * Global variants by passing the whole plane as the window. */
+int cm_pool(const int16_t *x, int16_t *y, uint32_t batch, uint32_t channels, uint32_t in_h,
+            uint32_t in_w, uint32_t out_h, uint32_t out_w, uint32_t pool_h, uint32_t pool_w,
+            uint32_t stride_h, uint32_t stride_w, uint32_t pad_top, uint32_t pad_left,
+            uint32_t dil_h, uint32_t dil_w, uint32_t pool_type, uint32_t lp_order,
+            uint32_t count_include_pad, hipStream_t stream);
+
+/* ------------------------------------------------------------------ buffers */
+
+/* Mirrors inference_buf_t (bench_src/inference.h:12-21): an owning allocation
+ * or a non-owning view at an element offset.  `host` is the CPU-side mirror
+ * (pinned; the reference's `virt`), `dev` the device address (the reference's
+ * `phys`).  Transfers happen only in the two sync calls. */
+typedef struct cm_buf {
+    int16_t *host;
+    int16_t *dev;
+    uint32_t count;
+    uint8_t is_owner;
+} cm_buf_t;
+
+int cm_buf_pool_init(void);                       /* inference_buf_pool_init */
+void cm_buf_pool_deinit(void);                    /* inference_buf_pool_deinit */
+cm_buf_t *cm_buf_alloc(uint32_t n_elem);          /* inference_buf_alloc; NULL on failure */
+void cm_buf_free(cm_buf_t *buf);                  /* inference_buf_free (views: no-op) */
+int16_t *cm_buf_ptr(cm_buf_t *buf);               /* inference_buf_ptr: host mirror */
+int16_t *cm_buf_dev(cm_buf_t *buf);               /* inference_buf_phys: device address */
+uint32_t cm_buf_count(const cm_buf_t *buf);       /* inference_buf_count */
+void cm_buf_init_view(cm_buf_t *view, cm_buf_t *base, uint32_t offset_elems,
+                      uint32_t count_elems);      /* inference_buf_init_view */
+int cm_buf_sync_to_device(cm_buf_t *buf);         /* host -> device, stream-ordered */
+int cm_buf_sync_from_device(cm_buf_t *buf);       /* device -> host, then waits */
+
+/* Buffer-level helpers with the generated run_* signatures (_source.py:198-421). */
+int cm_run_op(cm_buf_t *a, cm_buf_t *b, cm_buf_t *c, uint32_t size, uint32_t op,
+              uint32_t outer, uint32_t a_inc, uint32_t b_inc);
+int cm_run_matmul(cm_buf_t *a, cm_buf_t *b, cm_buf_t *c, uint32_t n, uint32_t k, uint32_t m,
+                  uint32_t batch, uint32_t a_stride, uint32_t b_stride, uint32_t c_stride);
+int cm_run_matmul_at(cm_buf_t *a, uint32_t a_off, cm_buf_t *b, uint32_t b_off, cm_buf_t *c,
+                     uint32_t c_off, uint32_t n, uint32_t k, uint32_t m, uint32_t batch,
+                     uint32_t a_stride, uint32_t b_stride, uint32_t c_stride);
+int cm_run_conv(cm_buf_t *x, cm_buf_t *weight, cm_buf_t *bias, cm_buf_t *y, uint32_t batch,
+                uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch, uint32_t out_h,
+                uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h, uint32_t stride_w,
+                uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top, uint32_t pad_left,
+                uint32_t has_bias, uint32_t is_depthwise);
+int cm_run_pool(cm_buf_t *x, cm_buf_t *y, uint32_t batch, uint32_t channels, uint32_t in_h,
+                uint32_t in_w, uint32_t out_h, uint32_t out_w, uint32_t pool_h, uint32_t pool_w,
+                uint32_t stride_h, uint32_t stride_w, uint32_t pad_top, uint32_t pad_left,
+                uint32_t dil_h, uint32_t dil_w, uint32_t pool_type, uint32_t lp_order,
+                uint32_t count_include_pad);
+
+/* ------------------------------------------------------------------ runtime */
+
+int cm_set_stream(hipStream_t stream);   /* stream used when a call passes NULL */
+hipStream_t cm_get_stream(void);
+int cm_sync(hipStream_t stream);         /* wait for all work queued on stream */
+const char *cm_last_error(void);
+const char *cm_version(void);
+
+/* Self-checks of the two scalar paths that use float arithmetic (no reference
+ * counterpart; used by the parity tests).  All run on `stream` and wait.
+ *   cm_selftest_div: compares the VectorOP DIV path with exact integer
+ *     division for every a and every b in [b_lo, b_lo + b_count) (b as uint16
+ *     bit patterns); *mismatches receives the count and *example (may be NULL)
+ *     one failing case packed as a<<48 | b<<32 | got<<16 | want (16-bit raw).
+ *   cm_selftest_finalize: mode 0 = LP p=2 finaliser over accumulators
+ *     lo .. lo+count-1; mode 1 = AVG finaliser over accumulators (lo+i) << 8
+ *     with denominator d; *checksum = sum (uint16)out * ((lo+i) | 1) mod 2^64. */
+int cm_selftest_div(uint32_t b_lo, uint32_t b_count, uint64_t *mismatches, uint64_t *example,
+                    hipStream_t stream);
+int cm_selftest_finalize(uint32_t mode, uint32_t lo, uint32_t count, uint32_t d,
+                         uint64_t *checksum, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CORMORANT_AMD_H */

@@ -1,0 +1,91 @@
+"""GPU parity: ConvKernel (implicit GEMM / pointwise GEMM on MFMA, direct depthwise)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from cormorant_amd import kernels as K
+from cormorant_amd import workloads as wl
+from tests import refcases as rc
+from tests.gpu_util import dev, empty_dev, host, oracle_threads, say
+
+pytestmark = pytest.mark.gpu
+
+
+def conv_both(x, w, b, N, C, H, W, M, OH, OW, kh, kw, sh, sw, dh, dw, pt, pl, bias, dwise):
+    y = empty_dev(N * M * OH * OW)
+    K.ConvKernel(dev(x), dev(w), dev(b), y, N, C, H, W, M, OH, OW, kh, kw, sh, sw, dh, dw, pt, pl,
+                 bias, dwise)
+    want = np.zeros(N * M * OH * OW, np.int16)
+    oracle.set_threads(oracle_threads())
+    oracle.conv(np.ascontiguousarray(x.reshape(-1)), np.ascontiguousarray(w.reshape(-1)),
+                np.ascontiguousarray(b.reshape(-1)), want, N, C, H, W, M, OH, OW, kh, kw, sh, sw,
+                dh, dw, pt, pl, bias, dwise, threads=True)
+    return host(y), want
+
+
+@pytest.mark.parametrize("i", range(len(rc.CONV_GEOMS)), ids=[g[0] for g in rc.CONV_GEOMS])
+def test_reference_geometries(i):
+    geom = rc.CONV_GEOMS[i]
+    (name, N, C, H, W, M, kh, kw, sh, sw, dh, dw, pt, pl, pb, pr, bias, dwise, xs, ws, bs) = geom
+    say(f"conv reference geometry {name}")
+    g = wl.rng(830, i)
+    x = wl.uniform_q88(g, (N, C, H, W), -xs, xs)
+    w = wl.uniform_q88(g, (M, 1 if dwise else C, kh, kw), -ws, ws)
+    b = wl.uniform_q88(g, (M,), -bs, bs)
+    OH = rc.conv_out_size(H, kh, sh, dh, pt, pb)
+    OW = rc.conv_out_size(W, kw, sw, dw, pl, pr)
+    got, want = conv_both(x, w, b, N, C, H, W, M, OH, OW, kh, kw, sh, sw, dh, dw, pt, pl, bias, dwise)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("case", rc.CONV_SAT, ids=[c[0] for c in rc.CONV_SAT])
+def test_saturation_kats(case):
+    name, wv, bv, expect = case
+    say(f"conv saturation {name}")
+    x = np.full((1, 1, 3, 3), 32767, np.int16)
+    w = np.full((1, 1, 1, 1), int(wv * 256), np.int16)
+    b = np.full((1,), int(bv * 256), np.int16)
+    got, want = conv_both(x, w, b, 1, 1, 3, 3, 1, 3, 3, 1, 1, 1, 1, 1, 1, 0, 0, 1, 0)
+    np.testing.assert_array_equal(got, want)
+    assert np.all(got / 256.0 == expect)
+
+
+GEOMS = [
+    # N, C, H, W, M, kh, kw, sh, sw, dh, dw, pt, pl, bias, dw
+    (2, 3, 33, 31, 32, 3, 3, 2, 2, 1, 1, 1, 1, 1, 0),     # stem-like, K = 27
+    (2, 16, 14, 14, 24, 1, 1, 1, 1, 1, 1, 0, 0, 1, 0),    # pointwise, aligned plane? 196 % 8 != 0
+    (2, 32, 16, 16, 40, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0),    # pointwise, 16-byte loads
+    (1, 24, 7, 7, 200, 1, 1, 1, 1, 1, 1, 0, 0, 1, 0),     # pointwise on a 7x7 plane
+    (1, 8, 10, 10, 8, 1, 1, 2, 2, 1, 1, 0, 0, 1, 0),      # 1x1 strided -> implicit GEMM
+    (2, 20, 12, 9, 150, 3, 5, 1, 2, 2, 1, 2, 1, 1, 0),
+    (1, 130, 9, 9, 7, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0),      # K = 1170 (many k tiles)
+    (2, 12, 10, 10, 12, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1),    # depthwise
+    (1, 6, 9, 9, 4, 5, 5, 2, 2, 1, 1, 2, 2, 0, 1),        # depthwise, out_ch < in_ch
+]
+
+
+@pytest.mark.parametrize("geom", GEOMS, ids=[str(g) for g in GEOMS])
+def test_geometries_full_range(geom):
+    N, C, H, W, M, kh, kw, sh, sw, dh, dw, pt, pl, bias, dwise = geom
+    OH = (H + 2 * pt - dh * (kh - 1) - 1) // sh + 1
+    OW = (W + 2 * pl - dw * (kw - 1) - 1) // sw + 1
+    say(f"conv geometry {geom}")
+    g = wl.rng(831, *geom)
+    x = g.integers(-32768, 32768, (N, C, H, W), dtype=np.int16)
+    w = g.integers(-32768, 32768, (M, 1 if dwise else C, kh, kw), dtype=np.int16)
+    b = g.integers(-32768, 32768, (M,), dtype=np.int16)
+    got, want = conv_both(x, w, b, N, C, H, W, M, OH, OW, kh, kw, sh, sw, dh, dw, pt, pl, bias, dwise)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("case", wl.CONV_CASES, ids=[c.name for c in wl.CONV_CASES])
+def test_config4_full_size(case):
+    say(f"conv full-size {case.name}")
+    x, w, b = wl.conv_operands(case)
+    o = case.out_hw
+    got, want = conv_both(x, w, b, case.batch, case.in_ch, case.hw, case.hw, case.out_ch, o, o,
+                          case.k, case.k, case.stride, case.stride, case.dil, case.dil, case.pad,
+                          case.pad, 1, 0)
+    np.testing.assert_array_equal(got, want)

@@ -1,0 +1,91 @@
+"""GPU parity: PoolingKernel through the C ABI vs the CPU oracle (bit-exact)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from cormorant_amd import kernels as K
+from cormorant_amd import workloads as wl
+from tests import refcases as rc
+from tests.gpu_util import dev, empty_dev, host, oracle_threads, say
+
+pytestmark = pytest.mark.gpu
+
+
+def pool_both(x, N, C, H, W, OH, OW, ph, pw, sh, sw, pt, pl, dh, dw, ptype, lp, cip):
+    y = empty_dev(N * C * OH * OW)
+    K.PoolingKernel(dev(x), y, N, C, H, W, OH, OW, ph, pw, sh, sw, pt, pl, dh, dw, ptype, lp, cip)
+    want = np.zeros(N * C * OH * OW, np.int16)
+    oracle.set_threads(oracle_threads())
+    oracle.pool(np.ascontiguousarray(x.reshape(-1)), want, N, C, H, W, OH, OW, ph, pw, sh, sw, pt,
+                pl, dh, dw, ptype, lp, cip, threads=True)
+    return host(y), want
+
+
+@pytest.mark.parametrize("case", rc.POOL_TESTS, ids=[c[0] for c in rc.POOL_TESTS])
+def test_reference_cases(case):
+    name, N, C, H, W, OH, OW, ph, pw, sh, sw, pt, pl, dh, dw, ptype, lp, cip = case
+    say(f"pool reference case: {name}")
+    x = rc.pool_test_fill(N * C * H * W)
+    got, want = pool_both(x, N, C, H, W, OH, OW, ph, pw, sh, sw, pt, pl, dh, dw, ptype, lp, cip)
+    np.testing.assert_array_equal(got, want)
+
+
+EDGE_CASES = [
+    # N, C, H, W, ph, pw, sh, sw, pt, pl, dh, dw  (out size computed with symmetric pads)
+    (2, 3, 9, 11, 3, 3, 2, 2, 1, 1, 1, 1),
+    (1, 5, 17, 13, 2, 3, 1, 2, 0, 1, 2, 1),
+    (1, 2, 7, 7, 5, 5, 3, 3, 2, 2, 1, 1),
+    (1, 1, 3, 3, 3, 3, 1, 1, 3, 3, 1, 1),       # windows entirely in padding at the corners
+    (1, 2, 5, 20000, 3, 3, 1, 1, 1, 1, 1, 1),   # rows too wide for LDS -> direct path
+    (2, 4, 56, 56, 56, 56, 1, 1, 0, 0, 1, 1),   # global (wave reduction path)
+    (1, 3, 7, 9, 7, 9, 1, 1, 0, 0, 1, 1),       # global, plane not a multiple of 8
+    (3, 2, 33, 31, 4, 4, 4, 4, 0, 0, 1, 1),
+]
+
+
+@pytest.mark.parametrize("ptype,lp,cip", [(0, 0, 0), (1, 0, 0), (1, 0, 1), (2, 1, 0), (2, 2, 0)])
+@pytest.mark.parametrize("geom", EDGE_CASES, ids=[str(g) for g in EDGE_CASES])
+def test_geometries_full_range_values(ptype, lp, cip, geom):
+    N, C, H, W, ph, pw, sh, sw, pt, pl, dh, dw = geom
+    OH = (H + 2 * pt - dh * (ph - 1) - 1) // sh + 1
+    OW = (W + 2 * pl - dw * (pw - 1) - 1) // sw + 1
+    say(f"pool geometry {geom} type={ptype} lp={lp} cip={cip}")
+    g = wl.rng(810, ptype, lp, cip, *geom)
+    x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)   # full range: sums wrap
+    got, want = pool_both(x, N, C, H, W, OH, OW, ph, pw, sh, sw, pt, pl, dh, dw, ptype, lp, cip)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("case", wl.POOL_CASES, ids=[c.name for c in wl.POOL_CASES])
+def test_config4_pools_full_size(case):
+    """Pools of the benchmark block on a [32, 128, 56, 56] activation."""
+    say(f"pool full-size {case.name}")
+    x = wl.uniform_q88(wl.rng(811), (32, 128, 56, 56), -4.0, 4.0)
+    a = wl.pool_args(case, 32, 128, 56)
+    got, want = pool_both(x, a["batch"], a["channels"], a["in_h"], a["in_w"], a["out_h"],
+                          a["out_w"], a["pool_h"], a["pool_w"], a["stride_h"], a["stride_w"],
+                          a["pad_top"], a["pad_left"], a["dil_h"], a["dil_w"], a["pool_type"],
+                          a["lp_order"], a["count_include_pad"])
+    np.testing.assert_array_equal(got, want)
+
+
+def test_lp2_finalizer_all_accumulators():
+    """LP p=2 finaliser (float32 convert + sqrt) for every A in [0, 2^31): checksums
+    of GPU and host float32 paths agree, chunk by chunk."""
+    oracle.set_threads(oracle_threads())
+    step = 1 << 27
+    for lo in range(0, 1 << 31, step):
+        say(f"lp2 sweep chunk {lo >> 27}")
+        assert K.selftest_finalize(0, lo, step) == oracle.lp2_checksum(lo, lo + step), lo
+    # negative (wrapped) accumulators map to 0 on both sides
+    assert K.selftest_finalize(0, 0x80000000, 1 << 20) == oracle.lp2_checksum(0x80000000, 0x80100000)
+
+
+@pytest.mark.parametrize("d", [0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 12, 16, 25, 49, 196, 784, 3136, 50176])
+def test_avg_finalizer_all_accumulators(d):
+    """AVG finaliser for every accumulator state (v << 8, v < 2^24) and denominator d."""
+    say(f"avg sweep d={d}")
+    oracle.set_threads(oracle_threads())
+    assert K.selftest_finalize(1, 0, 1 << 24, d) == oracle.avg_checksum(0, 1 << 24, d)
