@@ -1,0 +1,387 @@
+"""Benchmark of the MI355X Q8.8 kernels (one JSON line on stdout).
+
+Headline workload (the BASELINE metric's vector-op configuration): one step is
+the six-op VectorOP sweep -- Add, Sub, Mul, Div, Relu, Clip(0,6) -- over
+67,108,864-element int16 Q8.8 tensors (70% uniform over [-8, 8), 30% pinned at
+the saturation edges), every op with its own operand buffers (2.3 GB touched
+per step, far beyond the 256 MB Infinity Cache).  `value` is the aggregate
+GB/s of the step with the reference formula ports * elements * 2 B / time,
+ports = 3 for binary and 2 for unary ops (bench_src/bench_vectorop.c:93-95).
+
+The same run also reports (under "results") the GEMM, convolution and pooling
+configurations: Q8.8 GOP/s = 2*MAC / t (bench_matmul.c:95, bench_conv.c:129-132)
+with the int8-MFMA utilisation of the four limb products, and pool GB/s =
+(x + y) * 2 B / t (bench_pool.c:116-117) with rotating input buffers.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "Q8.8 GOP/s (conv/GEMM), GB/s (vecop/pool); images/s MobileNet-like b16"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
+INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA, 5.0 POP/s
+LIMB_PRODUCTS = 4              # int8 MFMA products per exact Q8.8 product
+
+
+def log(msg: str) -> None:
+    sys.stderr.write(f"[bench] {msg}\n")
+    sys.stderr.flush()
+
+
+class LaunchTimer:
+    """HIP events around each launch on torch's current stream (the stream the
+    C ABI wrappers launch on)."""
+
+    def __init__(self):
+        import torch
+        self.torch = torch
+        self.pairs: dict[str, list] = {}
+
+    def run(self, name: str, fn) -> None:
+        e0 = self.torch.cuda.Event(enable_timing=True)
+        e1 = self.torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fn()
+        e1.record()
+        self.pairs.setdefault(name, []).append((e0, e1))
+
+    def mean_ms(self, name: str) -> float:
+        v = [a.elapsed_time(b) for a, b in self.pairs[name]]
+        return float(np.mean(v))
+
+    def reset(self) -> None:
+        self.pairs.clear()
+
+
+def dev(a):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda")
+
+
+# ------------------------------------------------------------------ vecop --
+def setup_vecop():
+    from cormorant_amd import workloads as wl
+    import torch
+    bufs = []
+    for name, op in wl.VECOP_OPS:
+        a = wl.vecop_operand(wl.VECOP_N, op, 0)
+        b = wl.vecop_operand(wl.VECOP_N, op, 1) if op < 4 else None
+        bufs.append(dict(name=name, op=op, a=dev(a), b=dev(b) if b is not None else None,
+                         c=torch.empty(wl.VECOP_N, dtype=torch.int16, device="cuda"),
+                         a_host=a, b_host=b))
+    return bufs
+
+
+def vecop_bytes(op: int, n: int) -> int:
+    return (3 if op < 4 else 2) * n * 2
+
+
+def run_vecop_step(bufs, timer: LaunchTimer | None):
+    from cormorant_amd import kernels as K
+    for bf in bufs:
+        fn = lambda bf=bf: K.VectorOPKernel(bf["a"], bf["b"], bf["c"], bf["a"].numel(), bf["op"])
+        if timer is None:
+            fn()
+        else:
+            timer.run(bf["name"], fn)
+
+
+# ------------------------------------------------------------------- gemm --
+def bench_gemm(steps: int, warmup: int):
+    import torch
+    from cormorant_amd import kernels as K
+    from cormorant_amd import workloads as wl
+    out = {}
+    for cid, case in enumerate(wl.GEMM_CASES):
+        a, b = wl.gemm_operands(case, cid)
+        da, db = dev(a), dev(b)
+        dc = torch.empty(case.batch * case.n * case.m, dtype=torch.int16, device="cuda")
+        fn = lambda: K.MatmulKernel(da, db, dc, case.n, case.k, case.m, case.batch,
+                                    case.n * case.k, case.k * case.m, case.n * case.m)
+        for _ in range(warmup):
+            fn()
+        timer = LaunchTimer()
+        torch.cuda.synchronize()
+        for _ in range(steps):
+            timer.run(case.name, fn)
+        torch.cuda.synchronize()
+        ms = timer.mean_ms(case.name)
+        gops = 2.0 * case.macs / (ms * 1e-3) / 1e9
+        out[case.name] = dict(
+            shape=f"batch {case.batch}, {case.n}x{case.k}x{case.m}, U[{case.lo},{case.hi})",
+            ms=round(ms, 5), gops=round(gops, 1),
+            mfma_int8_tops=round(LIMB_PRODUCTS * gops / 1e3, 2),
+            mfma_frac=round(LIMB_PRODUCTS * gops / 1e3 / INT8_PEAK_TOPS, 4),
+            kernel="q88_gemm (dense)")
+        out[case.name]["_dev"] = (da, db, dc, a, b)
+    return out
+
+
+# ------------------------------------------------------------------- conv --
+def bench_conv(steps: int, warmup: int):
+    import torch
+    from cormorant_amd import kernels as K
+    from cormorant_amd import workloads as wl
+    out = {}
+    x, w, b = wl.conv_operands(wl.CONV_CASES[0])
+    dx, dw_, db = dev(x), dev(w), dev(b)
+    for case in wl.CONV_CASES:
+        o = case.out_hw
+        dy = torch.empty(case.batch * case.out_ch * o * o, dtype=torch.int16, device="cuda")
+        fn = lambda case=case, o=o, dy=dy: K.ConvKernel(
+            dx, dw_, db, dy, case.batch, case.in_ch, case.hw, case.hw, case.out_ch, o, o, case.k,
+            case.k, case.stride, case.stride, case.dil, case.dil, case.pad, case.pad, 1, 0)
+        for _ in range(warmup):
+            fn()
+        timer = LaunchTimer()
+        torch.cuda.synchronize()
+        for _ in range(steps):
+            timer.run(case.name, fn)
+        torch.cuda.synchronize()
+        ms = timer.mean_ms(case.name)
+        gops = 2.0 * case.macs / (ms * 1e-3) / 1e9
+        out[case.name] = dict(
+            shape=f"N={case.batch} C {case.in_ch}->{case.out_ch} {case.hw}x{case.hw} {case.k}x{case.k} "
+                  f"s{case.stride} d{case.dil} p{case.pad} bias -> {o}x{o}",
+            ms=round(ms, 5), gops=round(gops, 1),
+            mfma_int8_tops=round(LIMB_PRODUCTS * gops / 1e3, 2),
+            mfma_frac=round(LIMB_PRODUCTS * gops / 1e3 / INT8_PEAK_TOPS, 4),
+            kernel="q88_gemm (implicit GEMM)")
+        out[case.name]["_dev"] = (dx, dw_, db, dy, x, w, b)
+    return out
+
+
+# ------------------------------------------------------------------- pool --
+POOL_ROTATE = 12     # 12 x 25.7 MB inputs > 256 MB Infinity Cache
+
+
+def bench_pool(steps: int, warmup: int):
+    import torch
+    from cormorant_amd import kernels as K
+    from cormorant_amd import workloads as wl
+    n, c, hw = 32, 128, 56
+    xs = [dev(wl.uniform_q88(wl.rng(5, i), (n, c, hw, hw), -4.0, 4.0)) for i in range(POOL_ROTATE)]
+    out = {}
+    for case in wl.POOL_CASES:
+        a = wl.pool_args(case, n, c, hw)
+        ny = n * c * a["out_h"] * a["out_w"]
+        ys = [torch.empty(ny, dtype=torch.int16, device="cuda") for _ in range(POOL_ROTATE)]
+        calls = [lambda i=i: K.PoolingKernel(xs[i], ys[i], **a) for i in range(POOL_ROTATE)]
+        for i in range(warmup):
+            calls[i % POOL_ROTATE]()
+        timer = LaunchTimer()
+        torch.cuda.synchronize()
+        for s in range(max(steps, POOL_ROTATE)):
+            timer.run(case.name, calls[s % POOL_ROTATE])
+        torch.cuda.synchronize()
+        ms = timer.mean_ms(case.name)
+        nbytes = (n * c * hw * hw + ny) * 2
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[case.name] = dict(ms=round(ms, 5), gbs=round(gbs, 1),
+                              hbm_frac=round(gbs / HBM_PEAK_GBS, 4), bytes=nbytes,
+                              rotating_inputs=POOL_ROTATE)
+        out[case.name]["_dev"] = (xs[0], ys[0], a)
+    return out
+
+
+# ------------------------------------------------------------ cpu baseline --
+def cpu_baseline(vec_bufs, extras: dict):
+    """The oracle (C restatement of the reference C-simulation loops, -O2) timed
+    on this host: single thread, on a bounded sample.  The same run checks the
+    GPU outputs of that sample bit-for-bit."""
+    import oracle
+    oracle.set_threads(1)
+    res = {}
+    # VectorOP: the whole 64Mi sweep, one thread
+    t_total, bytes_total = 0.0, 0
+    for bf in vec_bufs:
+        want = np.empty(bf["a_host"].size, np.int16)
+        b = bf["b_host"] if bf["b_host"] is not None else np.zeros(1, np.int16)
+        t0 = time.perf_counter()
+        oracle.vectorop(bf["a_host"], b, want, want.size, bf["op"])
+        t_total += time.perf_counter() - t0
+        bytes_total += vecop_bytes(bf["op"], want.size)
+        got = bf["c"].cpu().numpy()
+        if not np.array_equal(got, want):
+            raise SystemExit(f"bench: GPU {bf['name']} output differs from the oracle")
+    res["vecop"] = dict(gbs=bytes_total / t_total / 1e9, seconds=t_total)
+    # GEMM 3a: one of the 32 batches (1024^3); GEMM 3b: 16 rows
+    if "gemm_b32_1024" in extras:
+        da, db, dc, a, b = extras["gemm_b32_1024"].pop("_dev")
+        n = k = m = 1024
+        want = np.empty(n * m, np.int16)
+        t0 = time.perf_counter()
+        oracle.matmul(np.ascontiguousarray(a[0]).reshape(-1), np.ascontiguousarray(b[0]).reshape(-1),
+                      want, n, k, m)
+        dt = time.perf_counter() - t0
+        if not np.array_equal(dc[: n * m].cpu().numpy(), want):
+            raise SystemExit("bench: GPU gemm batch 0 differs from the oracle")
+        res["gemm_b32_1024"] = dict(gops=2.0 * n * k * m / dt / 1e9, seconds=dt,
+                                    sample="batch 0 of 32 (1024^3)")
+    if "gemm_b1_4096" in extras:
+        da, db, dc, a, b = extras["gemm_b1_4096"].pop("_dev")
+        n = k = m = 4096
+        a2, b2 = a.reshape(n, k), b.reshape(k, m)
+        got = dc.cpu().numpy().reshape(n, m)
+        rows = list(range(0, n, n // 16))
+        t0 = time.perf_counter()
+        for r in rows:
+            if not np.array_equal(got[r], oracle.matmul_row(a2[r], b2, k, m)):
+                raise SystemExit(f"bench: GPU gemm 4096 row {r} differs from the oracle")
+        dt = time.perf_counter() - t0
+        res["gemm_b1_4096"] = dict(gops=2.0 * len(rows) * k * m / dt / 1e9, seconds=dt,
+                                   sample=f"{len(rows)} of 4096 rows")
+    for name in ("conv_a_3x3_s1_p1", "conv_b_3x3_s2_d2_p2"):
+        if name not in extras:
+            continue
+        from cormorant_amd import workloads as wl
+        case = [c for c in wl.CONV_CASES if c.name == name][0]
+        dx, dw_, db_, dy, x, w, b = extras[name].pop("_dev")
+        o = case.out_hw
+        want = np.empty(case.out_ch * o * o, np.int16)
+        t0 = time.perf_counter()
+        oracle.conv(np.ascontiguousarray(x[0]).reshape(-1), w.reshape(-1), b, want, 1, case.in_ch,
+                    case.hw, case.hw, case.out_ch, o, o, case.k, case.k, case.stride, case.stride,
+                    case.dil, case.dil, case.pad, case.pad, 1, 0)
+        dt = time.perf_counter() - t0
+        if not np.array_equal(dy[: want.size].cpu().numpy(), want):
+            raise SystemExit(f"bench: GPU {name} image 0 differs from the oracle")
+        res[name] = dict(gops=2.0 * case.macs / case.batch / dt / 1e9, seconds=dt,
+                         sample="image 0 of 32")
+    for name, e in list(extras.items()):
+        if not name.startswith(("maxpool", "avgpool", "lppool", "globalavgpool")):
+            continue
+        x, y, a = e.pop("_dev")
+        xh = x.cpu().numpy()
+        want = np.empty(y.numel(), np.int16)
+        t0 = time.perf_counter()
+        oracle.pool(xh, want, a["batch"], a["channels"], a["in_h"], a["in_w"], a["out_h"],
+                    a["out_w"], a["pool_h"], a["pool_w"], a["stride_h"], a["stride_w"],
+                    a["pad_top"], a["pad_left"], a["dil_h"], a["dil_w"], a["pool_type"],
+                    a["lp_order"], a["count_include_pad"])
+        dt = time.perf_counter() - t0
+        if not np.array_equal(y.cpu().numpy(), want):
+            raise SystemExit(f"bench: GPU {name} differs from the oracle")
+        res[name] = dict(gbs=(xh.size + want.size) * 2 / dt / 1e9, seconds=dt, sample="full tensor")
+    return res
+
+
+def load_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary, if any."""
+    p = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    try:
+        with open(p) as f:
+            return json.load(f).get(kernel)
+    except (OSError, ValueError):
+        return None
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--quick", action="store_true", help="headline workload only, no CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one MI355X; multi-GPU runs are not part of it "
+              "(--gpus must be 1).", file=sys.stderr)
+        return 2
+
+    import torch
+    from cormorant_amd import _native
+    _native.load()
+    torch.cuda.set_device(0)
+
+    log("generating the 64Mi-element VectorOP operands")
+    bufs = setup_vecop()
+    for _ in range(args.warmup):
+        run_vecop_step(bufs, None)
+    torch.cuda.synchronize()
+    timer = LaunchTimer()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        run_vecop_step(bufs, timer)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    from cormorant_amd import workloads as wl
+    step_bytes = sum(vecop_bytes(op, wl.VECOP_N) for _, op in wl.VECOP_OPS)
+    per_op = {}
+    for bf in bufs:
+        ms = timer.mean_ms(bf["name"])
+        gbs = vecop_bytes(bf["op"], wl.VECOP_N) / (ms * 1e-3) / 1e9
+        per_op[bf["name"]] = dict(ms=round(ms, 5), gbs=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
+    kernel_ms = sum(v["ms"] for v in per_op.values())
+    ms_per_step = wall * 1e3 / args.steps
+    value = step_bytes / (ms_per_step * 1e-3) / 1e9
+    dom_name = max(per_op, key=lambda k: per_op[k]["ms"])
+    dom_op = dict(wl.VECOP_OPS)[dom_name]
+    dom_kernel = f"vecop_flat<{dom_op}>"
+    traffic = load_traffic(dom_kernel)
+    roofline = dict(bound="hbm", achieved=per_op[dom_name]["gbs"], peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=per_op[dom_name]["hbm_frac"], traffic=traffic,
+                    kernel=dom_kernel, op=dom_name,
+                    bytes_per_launch=vecop_bytes(dom_op, wl.VECOP_N))
+
+    results = dict(vecop_ops=per_op, vecop_kernel_ms_per_step=round(kernel_ms, 5))
+    cpu = None
+    if not args.quick:
+        log("GEMM / conv / pool configurations")
+        extras = {}
+        extras.update(bench_gemm(max(5, args.steps // 2), 2))
+        extras.update(bench_conv(max(5, args.steps // 2), 2))
+        extras.update(bench_pool(max(args.steps, POOL_ROTATE), 2))
+        log("CPU baseline (oracle, 1 thread) and sample check")
+        cpu_res = cpu_baseline(bufs, extras)
+        for name, e in extras.items():
+            e.pop("_dev", None)
+            if name in cpu_res:
+                e["cpu_1t"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                               for k, v in cpu_res[name].items()}
+            results[name] = e
+        cpu = dict(value=round(cpu_res["vecop"]["gbs"], 3), unit="GB/s", cores=1, kind="port",
+                   sample="the full six-op 64Mi-element sweep, oracle C restatement -O2, one thread",
+                   seconds=round(cpu_res["vecop"]["seconds"], 3))
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int16",
+        "data": "synthetic",
+        "config": {
+            "workload": "vecop_sweep_64Mi: Add, Sub, Mul, Div, Relu, Clip(0,6) on 67108864-element "
+                        "int16 Q8.8 tensors, 70% U[-8,8) + 30% saturation edges, own buffers per op",
+            "elements": wl.VECOP_N,
+            "bytes_per_step": step_bytes,
+            "parallelism": "single GPU",
+        },
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "results": results,
+    }
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

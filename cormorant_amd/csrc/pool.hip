@@ -10,10 +10,13 @@
 //
 // Three launch shapes, all HBM streaming (each input byte read once):
 //   * global: window == whole plane (Global*Pool): one wavefront per plane,
-//     16-byte loads, cross-lane reduction;
+//     8 independent 16-byte loads in flight per lane, cross-lane reduction;
 //   * band:   a block stages the input rows that a band of output rows needs
-//     in LDS (16-byte loads), then computes the band from LDS;
+//     in LDS (16-byte loads, all issued before any is consumed), then
+//     computes the band from LDS;
 //   * direct: rows too wide for LDS -- each thread reads its window from HBM.
+// The reduction kind is a template parameter, so the inner loops carry no
+// per-element type dispatch.
 #include "cm_internal.h"
 #include "q88.h"
 
@@ -29,149 +32,171 @@ struct PoolGeom {
     uint32_t pool_type, lp_order, cip;
 };
 
-// Accumulator state for one output: uint32 wrap sums, int32 max.
-struct PoolAcc {
-    uint32_t acc;
-    __device__ __forceinline__ void init(uint32_t type) { acc = type == CM_POOL_MAX ? 0x80000000u : 0u; }
-    __device__ __forceinline__ void add(uint32_t type, uint32_t lp, int32_t x) {
-        if (type == CM_POOL_MAX) {
-            const int32_t v = x << 8;
-            acc = (uint32_t)__builtin_elementwise_max((int32_t)acc, v);
-        } else if (type == CM_POOL_AVG) {
-            acc += (uint32_t)x << 8;
-        } else if (lp == 1u) {
-            acc += (uint32_t)__builtin_abs(x) << 8;
-        } else {
-            acc += (uint32_t)(x * x);
-        }
+// Reduction kinds: pool_type MAX, AVG, or Lp with p = 1 / 2.
+enum Kind { K_MAX = 0, K_AVG = 1, K_LP1 = 2, K_LP2 = 3 };
+
+// Accumulator for one output: uint32 wrapping sum (AVG, LP) or int32 max,
+// initialised like PoolingKernel.cpp:185-190 (kAccMin = raw -2^31 for MAX).
+template <int KIND>
+struct Acc {
+    uint32_t v;
+    __device__ __forceinline__ Acc() : v(KIND == K_MAX ? 0x80000000u : 0u) {}
+    __device__ __forceinline__ void add(int32_t x) {
+        if constexpr (KIND == K_MAX) v = (uint32_t)__builtin_elementwise_max((int32_t)v, x << 8);
+        else if constexpr (KIND == K_AVG) v += (uint32_t)x << 8;
+        else if constexpr (KIND == K_LP1) v += (uint32_t)__builtin_abs(x) << 8;
+        else v += (uint32_t)(x * x);
+    }
+    __device__ __forceinline__ void merge(uint32_t o) {
+        if constexpr (KIND == K_MAX) v = (uint32_t)__builtin_elementwise_max((int32_t)v, (int32_t)o);
+        else v += o;
+    }
+    // PoolingKernel.cpp:253-266
+    __device__ __forceinline__ int16_t finish(float inv) const {
+        if constexpr (KIND == K_AVG) return q88::avg_finalize(v, inv);
+        else if constexpr (KIND == K_LP2) return q88::lp2_finalize(v);
+        else return q88::acc_to_data(v);
     }
 };
 
-__device__ __forceinline__ int16_t pool_finish(uint32_t type, uint32_t lp, uint32_t acc,
-                                               uint32_t denom) {
-    if (type == CM_POOL_MAX) return q88::acc_to_data(acc);
-    if (type == CM_POOL_AVG) return q88::avg_finalize(acc, q88::inv_denom(denom));
-    if (lp == 1u) return q88::acc_to_data(acc);
-    return q88::lp2_finalize(acc);
-}
-
-// Number of window taps t < k with 0 <= base + t*d < lim.
-__device__ __forceinline__ uint32_t valid_taps(int64_t base, uint32_t k, uint32_t d, uint32_t lim) {
-    uint32_t n = 0;
-    for (uint32_t t = 0; t < k; ++t) {
-        const int64_t p = base + (int64_t)t * d;
-        n += (p >= 0 && p < (int64_t)lim) ? 1u : 0u;
-    }
+// Number of taps t < k with 0 <= base + t*d < lim.
+__device__ __forceinline__ int32_t valid_taps(int32_t base, int32_t k, int32_t d, int32_t lim) {
+    int32_t n = 0;
+    for (int32_t t = 0; t < k; ++t) n += ((uint32_t)(base + t * d) < (uint32_t)lim) ? 1 : 0;
     return n;
 }
 
 // ---------------------------------------------------------------- global --
-// One wavefront reduces one plane of `hw` elements.
+constexpr int kBatch = 8;   // 16-byte loads in flight per lane
+
+template <int KIND>
 __global__ __launch_bounds__(kThreads) void pool_global(const int16_t* __restrict__ x,
                                                         int16_t* __restrict__ y, uint64_t planes,
-                                                        uint32_t hw, uint32_t type, uint32_t lp,
-                                                        uint32_t denom, uint32_t vec_ok) {
+                                                        uint32_t hw, float inv, uint32_t vec_ok) {
     const uint32_t lane = threadIdx.x & 63;
     const uint64_t plane = (uint64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
     if (plane >= planes) return;
     const int16_t* xp = x + plane * hw;
-    PoolAcc a;
-    a.init(type);
+    Acc<KIND> a;
     uint32_t done = 0;
     if (vec_ok) {
         const v8s* xv = reinterpret_cast<const v8s*>(xp);
         const uint32_t nv = hw / 8;
-        for (uint32_t v = lane; v < nv; v += 64) {
-            const v8s t = __builtin_nontemporal_load(xv + v);
+        for (uint32_t base = 0; base < nv; base += 64 * kBatch) {
+            v8s t[kBatch];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) a.add(type, lp, t[j]);
+            for (int u = 0; u < kBatch; ++u) {
+                const uint32_t v = base + u * 64 + lane;
+                if (v < nv) t[u] = __builtin_nontemporal_load(xv + v);
+            }
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                if (base + u * 64 + lane < nv) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) a.add(t[u][j]);
+                }
+            }
         }
         done = nv * 8;
     }
-    for (uint32_t i = done + lane; i < hw; i += 64) a.add(type, lp, xp[i]);
-    // cross-lane reduction: max for MAX, wrapping add otherwise
+    for (uint32_t i = done + lane; i < hw; i += 64) a.add(xp[i]);
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-        const uint32_t o = (uint32_t)__shfl_xor((int)a.acc, off, 64);
-        a.acc = type == CM_POOL_MAX ? (uint32_t)__builtin_elementwise_max((int32_t)a.acc, (int32_t)o)
-                                    : a.acc + o;
-    }
-    if (lane == 0) y[plane] = pool_finish(type, lp, a.acc, denom);
+    for (int off = 32; off > 0; off >>= 1) a.merge((uint32_t)__shfl_xor((int)a.v, off, 64));
+    if (lane == 0) y[plane] = a.finish(inv);
 }
 
 // ------------------------------------------------------------------ band --
-// Block = (plane, band of `band_h` output rows).  Stages input rows
-// [r_lo, r_hi) (full width) in LDS, then each thread produces outputs.
+// Block = (plane, band of `band_h` output rows).  Stages the input rows the
+// band needs (full width) in LDS, then computes the band.  Padded taps are
+// skipped: they add 0 to sums, and for MAX the initial accumulator (kAccMin)
+// already gives -32768 when no tap is valid, as padding with kDataMin does.
+template <int KIND>
 __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict__ x,
                                                       int16_t* __restrict__ y, PoolGeom g,
-                                                      uint32_t band_h, uint32_t n_bands) {
+                                                      uint32_t band_h, uint32_t n_bands,
+                                                      float inv_full) {
     extern __shared__ __align__(16) int16_t lds[];
     const uint64_t plane = blockIdx.x / n_bands;
     const uint32_t band = blockIdx.x - (uint32_t)(plane * n_bands);
     const uint32_t oh0 = band * band_h;
     const uint32_t oh1 = min(oh0 + band_h, g.out_h);
+    const int32_t in_h = (int32_t)g.in_h, in_w = (int32_t)g.in_w;
 
     // input rows touched by output rows [oh0, oh1)
-    const int64_t lo = (int64_t)oh0 * g.sh - g.pt;
-    const int64_t hi = (int64_t)(oh1 - 1) * g.sh - g.pt + (int64_t)(g.ph - 1) * g.dh + 1;
-    const int64_t r_lo = lo < 0 ? 0 : lo;
-    const int64_t r_hi = hi > (int64_t)g.in_h ? (int64_t)g.in_h : hi;
-    const uint64_t plane_elems = (uint64_t)g.in_h * g.in_w;
-    const int16_t* xp = x + plane * plane_elems;
+    const int32_t lo = (int32_t)(oh0 * g.sh) - (int32_t)g.pt;
+    const int32_t hi = (int32_t)((oh1 - 1) * g.sh) - (int32_t)g.pt + (int32_t)((g.ph - 1) * g.dh) + 1;
+    const int32_t r_lo = lo < 0 ? 0 : lo;
+    const int32_t r_hi = hi > in_h ? in_h : hi;
+    const int16_t* xp = x + plane * (uint64_t)g.in_h * g.in_w;
+    const int16_t* src = xp + (int64_t)r_lo * in_w;
+    const uint32_t shift = (uint32_t)(((uintptr_t)src >> 1) & 7u);
 
     if (r_hi > r_lo) {
-        // copy elements [e0, e1) of the plane to lds[shift + (e - e0)], where
-        // shift aligns the 16-byte body of the copy in LDS with global memory.
-        const uint64_t e0 = (uint64_t)r_lo * g.in_w, e1 = (uint64_t)r_hi * g.in_w;
-        const int16_t* src = xp + e0;
-        const uint32_t shift = (uint32_t)(((uintptr_t)src >> 1) & 7u);
-        const uint32_t n = (uint32_t)(e1 - e0);
+        // Copy elements [0, n) of src to lds[shift + i]; the 16-byte body of
+        // the copy is aligned identically in global memory and in LDS.  Each
+        // thread issues the loads of a round before it stores any of them.
+        const uint32_t n = (uint32_t)(r_hi - r_lo) * (uint32_t)in_w;
         const uint32_t head = min((8u - shift) & 7u, n);
         const uint32_t nv = (n - head) / 8;
-        const uint32_t body_end = head + nv * 8;
         int16_t* dst = lds + shift;
         if (threadIdx.x < head) dst[threadIdx.x] = src[threadIdx.x];
         const v8s* sv = reinterpret_cast<const v8s*>(src + head);
         v8s* dv = reinterpret_cast<v8s*>(dst + head);
-        for (uint32_t v = threadIdx.x; v < nv; v += kThreads) dv[v] = __builtin_nontemporal_load(sv + v);
-        for (uint32_t i = body_end + threadIdx.x; i < n; i += kThreads) dst[i] = src[i];
+        constexpr int kRound = 4;
+        for (uint32_t base = 0; base < nv; base += kThreads * kRound) {
+            v8s t[kRound];
+#pragma unroll
+            for (int u = 0; u < kRound; ++u) {
+                const uint32_t v = base + u * kThreads + threadIdx.x;
+                if (v < nv) t[u] = __builtin_nontemporal_load(sv + v);
+            }
+#pragma unroll
+            for (int u = 0; u < kRound; ++u) {
+                const uint32_t v = base + u * kThreads + threadIdx.x;
+                if (v < nv) dv[v] = t[u];
+            }
+        }
+        for (uint32_t i = head + nv * 8 + threadIdx.x; i < n; i += kThreads) dst[i] = src[i];
     }
     __syncthreads();
 
-    const int16_t* rows = lds + (uint32_t)(((uintptr_t)(xp + (uint64_t)r_lo * g.in_w) >> 1) & 7u);
+    // staged element (ih, iw), ih in [r_lo, r_hi): lds[shift + (ih - r_lo) * in_w + iw]
+    const int16_t* rows = lds + shift;
     const uint32_t count = (oh1 - oh0) * g.out_w;
     int16_t* yp = y + plane * (uint64_t)g.out_h * g.out_w + (uint64_t)oh0 * g.out_w;
-    const int16_t pad = g.pool_type == CM_POOL_MAX ? (int16_t)-32768 : (int16_t)0;
+    const int32_t ph = (int32_t)g.ph, pw = (int32_t)g.pw, dh = (int32_t)g.dh, dw = (int32_t)g.dw;
     for (uint32_t idx = threadIdx.x; idx < count; idx += kThreads) {
         const uint32_t r = idx / g.out_w;
         const uint32_t ow = idx - r * g.out_w;
-        const int64_t ih0 = (int64_t)(oh0 + r) * g.sh - g.pt;
-        const int64_t iw0 = (int64_t)ow * g.sw - g.pl;
-        PoolAcc a;
-        a.init(g.pool_type);
-        for (uint32_t khi = 0; khi < g.ph; ++khi) {
-            const int64_t ih = ih0 + (int64_t)khi * g.dh;
-            const bool ih_ok = ih >= 0 && ih < (int64_t)g.in_h;
-            const int16_t* row = rows + (ih_ok ? (uint64_t)(ih - r_lo) * g.in_w : 0);
-            for (uint32_t kwi = 0; kwi < g.pw; ++kwi) {
-                const int64_t iw = iw0 + (int64_t)kwi * g.dw;
-                const bool ok = ih_ok && iw >= 0 && iw < (int64_t)g.in_w;
-                a.add(g.pool_type, g.lp_order, ok ? row[iw] : pad);
+        const int32_t ih0 = (int32_t)((oh0 + r) * g.sh) - (int32_t)g.pt;
+        const int32_t iw0 = (int32_t)(ow * g.sw) - (int32_t)g.pl;
+        Acc<KIND> a;
+        for (int32_t khi = 0; khi < ph; ++khi) {
+            const int32_t ih = ih0 + khi * dh;
+            if ((uint32_t)ih >= (uint32_t)in_h) continue;
+            const int16_t* row = rows + (ih - r_lo) * in_w;
+            for (int32_t kwi = 0; kwi < pw; ++kwi) {
+                const int32_t iw = iw0 + kwi * dw;
+                if ((uint32_t)iw < (uint32_t)in_w) a.add(row[iw]);
             }
         }
-        uint32_t denom = g.ph * g.pw;
-        if (!g.cip) denom = valid_taps(ih0, g.ph, g.dh, g.in_h) * valid_taps(iw0, g.pw, g.dw, g.in_w);
-        yp[idx] = pool_finish(g.pool_type, g.lp_order, a.acc, denom);
+        float inv = inv_full;
+        if constexpr (KIND == K_AVG) {
+            if (!g.cip)
+                inv = q88::inv_denom((uint32_t)(valid_taps(ih0, ph, dh, in_h) *
+                                                valid_taps(iw0, pw, dw, in_w)));
+        }
+        yp[idx] = a.finish(inv);
     }
 }
 
 // ---------------------------------------------------------------- direct --
+template <int KIND>
 __global__ __launch_bounds__(kThreads) void pool_direct(const int16_t* __restrict__ x,
                                                         int16_t* __restrict__ y, PoolGeom g,
-                                                        uint64_t total) {
+                                                        uint64_t total, float inv_full) {
     const uint64_t stride = (uint64_t)gridDim.x * kThreads;
     const uint64_t ohw = (uint64_t)g.out_h * g.out_w;
-    const int16_t pad = g.pool_type == CM_POOL_MAX ? (int16_t)-32768 : (int16_t)0;
     for (uint64_t o = (uint64_t)blockIdx.x * kThreads + threadIdx.x; o < total; o += stride) {
         const uint64_t plane = o / ohw;
         const uint32_t rem = (uint32_t)(o - plane * ohw);
@@ -179,26 +204,97 @@ __global__ __launch_bounds__(kThreads) void pool_direct(const int16_t* __restric
         const int16_t* xp = x + plane * (uint64_t)g.in_h * g.in_w;
         const int64_t ih0 = (int64_t)oh * g.sh - g.pt;
         const int64_t iw0 = (int64_t)ow * g.sw - g.pl;
-        PoolAcc a;
-        a.init(g.pool_type);
+        Acc<KIND> a;
+        uint32_t vh = 0, vw = 0;
         for (uint32_t khi = 0; khi < g.ph; ++khi) {
             const int64_t ih = ih0 + (int64_t)khi * g.dh;
-            const bool ih_ok = ih >= 0 && ih < (int64_t)g.in_h;
+            if (ih < 0 || ih >= (int64_t)g.in_h) continue;
+            ++vh;
             for (uint32_t kwi = 0; kwi < g.pw; ++kwi) {
                 const int64_t iw = iw0 + (int64_t)kwi * g.dw;
-                const bool ok = ih_ok && iw >= 0 && iw < (int64_t)g.in_w;
-                a.add(g.pool_type, g.lp_order, ok ? xp[(uint64_t)ih * g.in_w + iw] : pad);
+                if (iw >= 0 && iw < (int64_t)g.in_w) a.add(xp[(uint64_t)ih * g.in_w + iw]);
             }
         }
-        uint32_t denom = g.ph * g.pw;
-        if (!g.cip) denom = valid_taps(ih0, g.ph, g.dh, g.in_h) * valid_taps(iw0, g.pw, g.dw, g.in_w);
-        y[o] = pool_finish(g.pool_type, g.lp_order, a.acc, denom);
+        float inv = inv_full;
+        if constexpr (KIND == K_AVG) {
+            if (!g.cip) {
+                for (uint32_t t = 0; t < g.pw; ++t) {
+                    const int64_t p = iw0 + (int64_t)t * g.dw;
+                    vw += (p >= 0 && p < (int64_t)g.in_w) ? 1u : 0u;
+                }
+                inv = q88::inv_denom(vh * vw);
+            }
+        }
+        y[o] = a.finish(inv);
     }
 }
 
 // Input rows needed by `bh` consecutive output rows.
 uint64_t rows_needed(const PoolGeom& g, uint32_t bh) {
     return (uint64_t)(bh - 1) * g.sh + (uint64_t)(g.ph - 1) * g.dh + 1;
+}
+
+// 1.0f / (float)d on the host: IEEE round-to-nearest-even, like the device path.
+float host_inv_denom(uint64_t d) { return d ? 1.0f / (float)d : 0.0f; }
+
+template <int KIND>
+int pool_launch(const int16_t* x, int16_t* y, uint64_t planes, const PoolGeom& g, hipStream_t s) {
+    const uint64_t full = (uint64_t)g.ph * g.pw;   // count_include_pad denominator
+    const float inv_full = host_inv_denom(full > 0xFFFFFFFFull ? 0 : full);
+    const uint64_t total = planes * g.out_h * g.out_w;
+    if (g.ph == 0 || g.pw == 0 || g.in_h == 0 || g.in_w == 0) {
+        // empty window or input: every output is the finaliser of the initial accumulator
+        hipLaunchKernelGGL(pool_direct<KIND>, dim3((uint32_t)cm_grid_blocks(total, kThreads)),
+                           dim3(kThreads), 0, s, x, y, g, total, inv_full);
+        return cm_check_launch("pool_direct");
+    }
+    const bool global = g.out_h == 1 && g.out_w == 1 && g.ph == g.in_h && g.pw == g.in_w &&
+                        g.pt == 0 && g.pl == 0 && g.dh == 1 && g.dw == 1;
+    if (global) {
+        const uint64_t hw = (uint64_t)g.in_h * g.in_w;
+        if (hw > 0xFFFFFFFFull) return cm_set_error(CM_ERR_RANGE, "pool: plane too large");
+        const uint32_t vec_ok = (hw % 8 == 0) && (((uintptr_t)x & 15u) == 0);
+        const uint64_t blocks = (planes + 3) / 4;
+        if (blocks > 0x7FFFFFFFull) return cm_set_error(CM_ERR_RANGE, "pool: too many planes");
+        // no padding: the valid count equals the window size for either cip
+        hipLaunchKernelGGL(pool_global<KIND>, dim3((uint32_t)blocks), dim3(kThreads), 0, s, x, y,
+                           planes, (uint32_t)hw, host_inv_denom(hw), vec_ok);
+        return cm_check_launch("pool_global");
+    }
+    // The band kernel indexes with 32-bit arithmetic: only shapes well inside
+    // that range take it.  Band height: as many output rows as fit the LDS
+    // budget (+16 B alignment slack).
+    const bool small = g.in_h < (1u << 20) && g.in_w < (1u << 20) && g.sh < (1u << 10) &&
+                       g.sw < (1u << 10) && g.dh < (1u << 10) && g.dw < (1u << 10) &&
+                       g.pt < (1u << 20) && g.pl < (1u << 20) && g.ph < (1u << 10) &&
+                       g.pw < (1u << 10) && (uint64_t)g.out_w * g.sw < (1u << 30) &&
+                       (uint64_t)g.out_h * g.sh < (1u << 30) &&
+                       (uint64_t)g.in_h * g.in_w < (1u << 30);
+    uint32_t band_h = 0;
+    const uint64_t row_bytes = (uint64_t)g.in_w * 2;
+    if (small && rows_needed(g, 1) * row_bytes + 16 <= kLdsBytes) {
+        uint32_t lo = 1, hi = g.out_h;
+        while (lo < hi) {
+            const uint32_t mid = lo + (hi - lo + 1) / 2;
+            if (rows_needed(g, mid) * row_bytes + 16 <= kLdsBytes) lo = mid; else hi = mid - 1;
+        }
+        band_h = lo;
+    }
+    if (band_h > 0) {
+        const uint32_t n_bands = (g.out_h + band_h - 1) / band_h;
+        const uint64_t blocks = planes * n_bands;
+        if (blocks <= 0x7FFFFFFFull) {
+            uint64_t need = rows_needed(g, band_h);
+            if (need > g.in_h) need = g.in_h;
+            const uint32_t lds = (uint32_t)(need * row_bytes + 16);
+            hipLaunchKernelGGL(pool_band<KIND>, dim3((uint32_t)blocks), dim3(kThreads), lds, s, x,
+                               y, g, band_h, n_bands, inv_full);
+            return cm_check_launch("pool_band");
+        }
+    }
+    hipLaunchKernelGGL(pool_direct<KIND>, dim3((uint32_t)cm_grid_blocks(total, kThreads)),
+                       dim3(kThreads), 0, s, x, y, g, total, inv_full);
+    return cm_check_launch("pool_direct");
 }
 
 // Exhaustive finaliser sweep: mode 0 = LP p=2 over accumulators lo + i;
@@ -229,54 +325,14 @@ int cm_pool_launch(const int16_t* x, int16_t* y, uint32_t batch, uint32_t ch, ui
                    hipStream_t s) {
     const uint64_t planes = (uint64_t)batch * ch;
     if (planes == 0 || out_h == 0 || out_w == 0) return CM_OK;
-    PoolGeom g{in_h, in_w, out_h, out_w, ph, pw, sh, sw, pad_top, pad_left, dh, dw,
-               pool_type, lp_order, cip};
-    if (ph == 0 || pw == 0 || in_h == 0 || in_w == 0) {
-        // empty window or empty input: every output is the finaliser of the initial accumulator
-        const uint64_t total = planes * out_h * out_w;
-        hipLaunchKernelGGL(pool_direct, dim3((uint32_t)cm_grid_blocks(total, kThreads)),
-                           dim3(kThreads), 0, s, x, y, g, total);
-        return cm_check_launch("pool_direct");
-    }
-    const bool global = out_h == 1 && out_w == 1 && ph == in_h && pw == in_w && pad_top == 0 &&
-                        pad_left == 0 && dh == 1 && dw == 1;
-    if (global) {
-        const uint64_t hw = (uint64_t)in_h * in_w;
-        if (hw > 0xFFFFFFFFull) return cm_set_error(CM_ERR_RANGE, "pool: plane too large");
-        const uint32_t vec_ok = (hw % 8 == 0) && (((uintptr_t)x & 15u) == 0);
-        const uint64_t blocks = (planes + 3) / 4;
-        if (blocks > 0x7FFFFFFFull) return cm_set_error(CM_ERR_RANGE, "pool: too many planes");
-        hipLaunchKernelGGL(pool_global, dim3((uint32_t)blocks), dim3(kThreads), 0, s, x, y,
-                           planes, (uint32_t)hw, pool_type, lp_order, (uint32_t)hw, vec_ok);
-        return cm_check_launch("pool_global");
-    }
-    // band height: as many output rows as fit the LDS budget (+16 B alignment slack)
-    uint32_t band_h = 0;
-    const uint64_t row_bytes = (uint64_t)in_w * 2;
-    if (rows_needed(g, 1) * row_bytes + 16 <= kLdsBytes) {
-        uint32_t lo = 1, hi = out_h;
-        while (lo < hi) {
-            const uint32_t mid = lo + (hi - lo + 1) / 2;
-            if (rows_needed(g, mid) * row_bytes + 16 <= kLdsBytes) lo = mid; else hi = mid - 1;
-        }
-        band_h = lo;
-    }
-    if (band_h > 0) {
-        const uint32_t n_bands = (out_h + band_h - 1) / band_h;
-        const uint64_t blocks = planes * n_bands;
-        if (blocks <= 0x7FFFFFFFull) {
-            uint64_t need = rows_needed(g, band_h);
-            if (need > in_h) need = in_h;
-            const uint32_t lds = (uint32_t)(need * row_bytes + 16);
-            hipLaunchKernelGGL(pool_band, dim3((uint32_t)blocks), dim3(kThreads), lds, s, x, y,
-                               g, band_h, n_bands);
-            return cm_check_launch("pool_band");
-        }
-    }
-    const uint64_t total = planes * out_h * out_w;
-    hipLaunchKernelGGL(pool_direct, dim3((uint32_t)cm_grid_blocks(total, kThreads)),
-                       dim3(kThreads), 0, s, x, y, g, total);
-    return cm_check_launch("pool_direct");
+    const PoolGeom g{in_h, in_w, out_h, out_w, ph, pw, sh, sw, pad_top, pad_left, dh, dw,
+                     pool_type, lp_order, cip};
+    // pool_type 0 MAX, 1 AVG, anything else Lp; lp_order 1 -> p=1, else p=2
+    // (PoolingKernel.cpp:214-224, 261-263)
+    if (pool_type == CM_POOL_MAX) return pool_launch<K_MAX>(x, y, planes, g, s);
+    if (pool_type == CM_POOL_AVG) return pool_launch<K_AVG>(x, y, planes, g, s);
+    if (lp_order == 1u) return pool_launch<K_LP1>(x, y, planes, g, s);
+    return pool_launch<K_LP2>(x, y, planes, g, s);
 }
 
 int cm_finalize_sweep_launch(uint32_t mode, uint32_t lo, uint32_t count, uint32_t d,

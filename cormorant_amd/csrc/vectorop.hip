@@ -185,8 +185,17 @@ __global__ __launch_bounds__(kThreads) void vecop_div_sweep(uint32_t b_lo, uint3
     if (b_idx >= b_lo + b_count || b_idx > 0xFFFFu) return;
     const int32_t bv = (int16_t)(uint16_t)b_idx;
     const int32_t av = (int16_t)(uint16_t)(blockIdx.x * kThreads + threadIdx.x);
+    // Reference value from double-precision division.  Integer division is
+    // not usable here: the compiler narrows a 32- or 64-bit signed division
+    // whose operands fit 24 bits to a 24-bit sequence, and that sequence
+    // returns -2^23 for (-2^23) / (-1).  In double, A / b (|A| <= 2^23,
+    // |b| <= 2^15) lies at least 2^-15 away from any integer it is not equal
+    // to, far above the 2^-30 rounding error, so trunc() is exact.
     int32_t want = 0;
-    if (bv != 0) want = q88::sat16((av * 256) / bv);
+    if (bv != 0) {
+        const double q = __builtin_trunc((double)(av * 256) / (double)bv);
+        want = (int32_t)(q > 32767.0 ? 32767.0 : (q < -32768.0 ? -32768.0 : q));
+    }
     const int32_t got = q88::div(av, bv);
     const unsigned long long bad = __ballot(got != want);
     if ((threadIdx.x & 63) == 0 && bad != 0) atomicAdd(out, (unsigned long long)__popcll(bad));
