@@ -40,29 +40,47 @@ def log(msg: str) -> None:
     sys.stderr.flush()
 
 
-class LaunchTimer:
-    """HIP events around each launch on torch's current stream (the stream the
-    C ABI wrappers launch on)."""
+def time_launches(calls, steps: int) -> float:
+    """Mean duration (ms) of one launch: HIP events on the launch stream (torch's
+    current stream, which the C-ABI wrappers use) bracket `steps` back-to-back
+    launches, cycling through `calls`."""
+    import torch
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        calls[i % len(calls)]()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
 
-    def __init__(self):
-        import torch
-        self.torch = torch
-        self.pairs: dict[str, list] = {}
 
-    def run(self, name: str, fn) -> None:
-        e0 = self.torch.cuda.Event(enable_timing=True)
-        e1 = self.torch.cuda.Event(enable_timing=True)
-        e0.record()
-        fn()
-        e1.record()
-        self.pairs.setdefault(name, []).append((e0, e1))
-
-    def mean_ms(self, name: str) -> float:
-        v = [a.elapsed_time(b) for a, b in self.pairs[name]]
-        return float(np.mean(v))
-
-    def reset(self) -> None:
-        self.pairs.clear()
+def time_graph(calls, steps: int) -> float:
+    """Mean duration (ms) of one launch with host overhead removed: `steps`
+    launches (cycling through `calls`) are captured into one HIP graph, which is
+    replayed once untimed and then once between HIP events."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for c in calls:
+            c()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(steps):
+            calls[i % len(calls)]()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
 
 
 def dev(a):
@@ -88,14 +106,14 @@ def vecop_bytes(op: int, n: int) -> int:
     return (3 if op < 4 else 2) * n * 2
 
 
-def run_vecop_step(bufs, timer: LaunchTimer | None):
+def vecop_call(bf):
     from cormorant_amd import kernels as K
+    return lambda: K.VectorOPKernel(bf["a"], bf["b"], bf["c"], bf["a"].numel(), bf["op"])
+
+
+def run_vecop_step(bufs):
     for bf in bufs:
-        fn = lambda bf=bf: K.VectorOPKernel(bf["a"], bf["b"], bf["c"], bf["a"].numel(), bf["op"])
-        if timer is None:
-            fn()
-        else:
-            timer.run(bf["name"], fn)
+        vecop_call(bf)()
 
 
 # ------------------------------------------------------------------- gemm --
@@ -112,12 +130,7 @@ def bench_gemm(steps: int, warmup: int):
                                     case.n * case.k, case.k * case.m, case.n * case.m)
         for _ in range(warmup):
             fn()
-        timer = LaunchTimer()
-        torch.cuda.synchronize()
-        for _ in range(steps):
-            timer.run(case.name, fn)
-        torch.cuda.synchronize()
-        ms = timer.mean_ms(case.name)
+        ms = time_launches([fn], steps)
         gops = 2.0 * case.macs / (ms * 1e-3) / 1e9
         out[case.name] = dict(
             shape=f"batch {case.batch}, {case.n}x{case.k}x{case.m}, U[{case.lo},{case.hi})",
@@ -145,12 +158,7 @@ def bench_conv(steps: int, warmup: int):
             case.k, case.stride, case.stride, case.dil, case.dil, case.pad, case.pad, 1, 0)
         for _ in range(warmup):
             fn()
-        timer = LaunchTimer()
-        torch.cuda.synchronize()
-        for _ in range(steps):
-            timer.run(case.name, fn)
-        torch.cuda.synchronize()
-        ms = timer.mean_ms(case.name)
+        ms = time_launches([fn], steps)
         gops = 2.0 * case.macs / (ms * 1e-3) / 1e9
         out[case.name] = dict(
             shape=f"N={case.batch} C {case.in_ch}->{case.out_ch} {case.hw}x{case.hw} {case.k}x{case.k} "
@@ -181,17 +189,12 @@ def bench_pool(steps: int, warmup: int):
         calls = [lambda i=i: K.PoolingKernel(xs[i], ys[i], **a) for i in range(POOL_ROTATE)]
         for i in range(warmup):
             calls[i % POOL_ROTATE]()
-        timer = LaunchTimer()
-        torch.cuda.synchronize()
-        for s in range(max(steps, POOL_ROTATE)):
-            timer.run(case.name, calls[s % POOL_ROTATE])
-        torch.cuda.synchronize()
-        ms = timer.mean_ms(case.name)
+        ms = time_graph(calls, max(steps, 4 * POOL_ROTATE))
         nbytes = (n * c * hw * hw + ny) * 2
         gbs = nbytes / (ms * 1e-3) / 1e9
         out[case.name] = dict(ms=round(ms, 5), gbs=round(gbs, 1),
                               hbm_frac=round(gbs / HBM_PEAK_GBS, 4), bytes=nbytes,
-                              rotating_inputs=POOL_ROTATE)
+                              rotating_inputs=POOL_ROTATE, timing="HIP graph of back-to-back launches")
         out[case.name]["_dev"] = (xs[0], ys[0], a)
     return out
 
@@ -308,19 +311,18 @@ def main() -> int:
     log("generating the 64Mi-element VectorOP operands")
     bufs = setup_vecop()
     for _ in range(args.warmup):
-        run_vecop_step(bufs, None)
+        run_vecop_step(bufs)
     torch.cuda.synchronize()
-    timer = LaunchTimer()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        run_vecop_step(bufs, timer)
+        run_vecop_step(bufs)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     from cormorant_amd import workloads as wl
     step_bytes = sum(vecop_bytes(op, wl.VECOP_N) for _, op in wl.VECOP_OPS)
     per_op = {}
-    for bf in bufs:
-        ms = timer.mean_ms(bf["name"])
+    for bf in bufs:   # each op alone: its average launch duration
+        ms = time_launches([vecop_call(bf)], max(args.steps, 10))
         gbs = vecop_bytes(bf["op"], wl.VECOP_N) / (ms * 1e-3) / 1e9
         per_op[bf["name"]] = dict(ms=round(ms, 5), gbs=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
     kernel_ms = sum(v["ms"] for v in per_op.values())

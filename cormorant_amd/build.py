@@ -32,6 +32,7 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",
     "-Wno-unused-function",
+    "-Wno-pass-failed",
     "-I", os.path.join(HERE, "..", "include"),
 ]
 

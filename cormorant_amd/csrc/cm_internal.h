@@ -3,7 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/cormorant_amd.h"   // error codes, pool types
+#include "cormorant_amd.h"   // include/: error codes, pool types
 
 // VectorOP opcodes (kernels/vectorop/include/VectorOP.h:50-57); any other value copies a.
 enum {

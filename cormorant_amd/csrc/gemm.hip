@@ -51,17 +51,19 @@ struct GemmArgs {
     uint64_t x_img, y_img;
 };
 
-// Split four int16 values held in two words into a word of high bytes and a
-// word of offset low bytes (value order preserved, low byte first).
-__device__ __forceinline__ void split4(uint32_t w0, uint32_t w1, uint32_t& hi, uint32_t& lo) {
-    hi = ((w0 >> 8) & 0xFFu) | ((w0 >> 16) & 0xFF00u) | ((w1 << 8) & 0xFF0000u) |
-         (w1 & 0xFF000000u);
-    lo = ((w0 & 0xFFu) | ((w0 >> 8) & 0xFF00u) | ((w1 << 16) & 0xFF0000u) |
-          ((w1 << 8) & 0xFF000000u)) ^ 0x80808080u;
+// Limb bytes of four int16 values held in two words w0 = (v0 | v1 << 16),
+// w1 = (v2 | v3 << 16): one v_perm_b32 gathers the high bytes (v >> 8) and one
+// more the low bytes, which the xor offsets by -128.  Byte i of the result is
+// value i, so k order is preserved.
+__device__ __forceinline__ uint32_t hi4(uint32_t w0, uint32_t w1) {
+    return __builtin_amdgcn_perm(w1, w0, 0x07050301u);
 }
-
-__device__ __forceinline__ int32_t wsum(uint32_t w) {
-    return (int32_t)(int16_t)(w & 0xFFFFu) + (int32_t)(int16_t)(w >> 16);
+__device__ __forceinline__ uint32_t lo4(uint32_t w0, uint32_t w1) {
+    return __builtin_amdgcn_perm(w1, w0, 0x06040200u) ^ 0x80808080u;
+}
+// Sum of the four signed bytes of w added to acc (v_dot4 with a ones vector).
+__device__ __forceinline__ int32_t bsum(uint32_t w, int32_t acc) {
+    return __builtin_amdgcn_sdot4((int)w, 0x01010101, acc, false);
 }
 
 __device__ __forceinline__ uint32_t pack2(int16_t lo, int16_t hi) {
@@ -106,16 +108,18 @@ struct ATile {
             }
         }
     }
-    __device__ __forceinline__ void store(Smem& s, uint32_t& row_sum) const {
+    // Stores the limbs; hs / ls accumulate the sums of the high and low limbs
+    // of this thread's values (sum a = 256*hs + ls + 128*count).
+    __device__ __forceinline__ void store(Smem& s, int32_t& hs, int32_t& ls) const {
         const uint32_t off = (threadIdx.x >> 1) * kStride + (threadIdx.x & 1) * 32;
         uint32_t hi[8], lo[8];
-        int32_t sum = 0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            split4(w[2 * j], w[2 * j + 1], hi[j], lo[j]);
-            sum += wsum(w[2 * j]) + wsum(w[2 * j + 1]);
+            hi[j] = hi4(w[2 * j], w[2 * j + 1]);
+            lo[j] = lo4(w[2 * j], w[2 * j + 1]);
+            hs = bsum(hi[j], hs);
+            ls = bsum(lo[j], ls);
         }
-        row_sum += (uint32_t)sum;
         v4i* dh = reinterpret_cast<v4i*>(s.a_hi + off);
         v4i* dl = reinterpret_cast<v4i*>(s.a_lo + off);
         dh[0] = v4i{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
@@ -126,19 +130,16 @@ struct ATile {
 };
 
 // ---------------------------------------------------------- dense B tile --
-// Thread t owns columns [8*(t&15), +8) and k rows [4*(t>>4), +4).
+// Thread t owns columns [8*(t>>4), +8) and k rows [4*(t&15), +4).  Lanes of a
+// wave differ mostly in k, so the transposing 4-byte LDS stores of one column
+// land in 16 different banks (4-way at worst) instead of one.
 struct DenseBTile {
     uint32_t w[4][4];   // [k row][word of 2 columns]
-    uint32_t col_sum[8];
 
-    __device__ __forceinline__ void init() {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) col_sum[j] = 0;
-    }
     __device__ __forceinline__ void load(const GemmArgs& g, const int16_t* bbase, uint32_t col0,
                                          uint32_t k0) {
-        const uint32_t cb = col0 + (threadIdx.x & 15) * 8;
-        const uint32_t kb = k0 + (threadIdx.x >> 4) * 4;
+        const uint32_t cb = col0 + (threadIdx.x >> 4) * 8;
+        const uint32_t kb = k0 + (threadIdx.x & 15) * 4;
         if (g.b_vec) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -162,39 +163,54 @@ struct DenseBTile {
             }
         }
     }
-    __device__ __forceinline__ void store(Smem& s) {
-        const uint32_t cl = (threadIdx.x & 15) * 8;
-        const uint32_t kbyte = (threadIdx.x >> 4) * 4;
+    // Transposes 4 k rows x 8 columns into one limb word per column: for the
+    // column pair held in word q, two perms interleave rows (0,1) and (2,3),
+    // two more split even / odd columns.  hs / ls accumulate per-column limb sums.
+    __device__ __forceinline__ void store(Smem& s, int32_t (&hs)[8], int32_t (&ls)[8]) const {
+        const uint32_t cl = (threadIdx.x >> 4) * 8;
+        const uint32_t kbyte = (threadIdx.x & 15) * 4;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int sh = (j & 1) * 16;
-            const int16_t v0 = (int16_t)(w[0][j >> 1] >> sh), v1 = (int16_t)(w[1][j >> 1] >> sh);
-            const int16_t v2 = (int16_t)(w[2][j >> 1] >> sh), v3 = (int16_t)(w[3][j >> 1] >> sh);
-            uint32_t hi, lo;
-            split4(pack2(v0, v1), pack2(v2, v3), hi, lo);
-            col_sum[j] += (uint32_t)((int32_t)v0 + v1 + v2 + v3);
-            *reinterpret_cast<uint32_t*>(s.b_hi + (cl + j) * kStride + kbyte) = hi;
-            *reinterpret_cast<uint32_t*>(s.b_lo + (cl + j) * kStride + kbyte) = lo;
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t t01 = __builtin_amdgcn_perm(w[1][q], w[0][q], 0x07030501u);
+            const uint32_t t23 = __builtin_amdgcn_perm(w[3][q], w[2][q], 0x07030501u);
+            const uint32_t u01 = __builtin_amdgcn_perm(w[1][q], w[0][q], 0x06020400u);
+            const uint32_t u23 = __builtin_amdgcn_perm(w[3][q], w[2][q], 0x06020400u);
+            const uint32_t hi_e = __builtin_amdgcn_perm(t23, t01, 0x05040100u);
+            const uint32_t hi_o = __builtin_amdgcn_perm(t23, t01, 0x07060302u);
+            const uint32_t lo_e = __builtin_amdgcn_perm(u23, u01, 0x05040100u) ^ 0x80808080u;
+            const uint32_t lo_o = __builtin_amdgcn_perm(u23, u01, 0x07060302u) ^ 0x80808080u;
+            hs[2 * q] = bsum(hi_e, hs[2 * q]);
+            hs[2 * q + 1] = bsum(hi_o, hs[2 * q + 1]);
+            ls[2 * q] = bsum(lo_e, ls[2 * q]);
+            ls[2 * q + 1] = bsum(lo_o, ls[2 * q + 1]);
+            const uint32_t c = cl + 2 * q;
+            *reinterpret_cast<uint32_t*>(s.b_hi + c * kStride + kbyte) = hi_e;
+            *reinterpret_cast<uint32_t*>(s.b_hi + (c + 1) * kStride + kbyte) = hi_o;
+            *reinterpret_cast<uint32_t*>(s.b_lo + c * kStride + kbyte) = lo_e;
+            *reinterpret_cast<uint32_t*>(s.b_lo + (c + 1) * kStride + kbyte) = lo_o;
         }
     }
-    __device__ __forceinline__ void publish_sums(Smem& s) const {
-        const uint32_t cl = (threadIdx.x & 15) * 8;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) atomicAdd(&s.col_sum[cl + j], col_sum[j]);
-    }
 };
+
+// Column sums of the dense B tile: count = k values per column this thread stored.
+__device__ __forceinline__ void publish_dense(Smem& s, const int32_t (&hs)[8], const int32_t (&ls)[8],
+                                              uint32_t count) {
+    const uint32_t cl = (threadIdx.x >> 4) * 8;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+        atomicAdd(&s.col_sum[cl + j], 256u * (uint32_t)hs[j] + (uint32_t)ls[j] + 128u * count);
+}
 
 // ------------------------------------------------------- im2col B tile --
 // Thread t owns column (pixel) t&127 and k values [32*(t>>7), +32).
 struct ConvBTile {
     uint32_t w[16];
-    uint32_t col_sum;
     const int16_t* xb;   // image base of this thread's column
-    int32_t ih0, iw0;
+    int32_t ih0, iw0;    // window origin of this thread's output pixel
+    int32_t pbase;       // ih0 * W + iw0 (may be negative; only valid taps are read)
     bool col_ok;
 
     __device__ __forceinline__ void init(const GemmArgs& g, uint32_t col0) {
-        col_sum = 0;
         const uint32_t col = col0 + (threadIdx.x & 127);
         col_ok = col < g.cols;
         const uint32_t n = col_ok ? col / g.P : 0;
@@ -202,7 +218,28 @@ struct ConvBTile {
         const uint32_t oh = p / g.OW, ow = p - (p / g.OW) * g.OW;
         ih0 = (int32_t)(oh * g.sh) - (int32_t)g.pt;
         iw0 = (int32_t)(ow * g.sw) - (int32_t)g.pl;
+        pbase = ih0 * (int32_t)g.W + iw0;
         xb = g.b + (uint64_t)n * g.x_img;
+    }
+    // Gather with the per-block k table: tab[k] = {c*H*W + dy*W + dx, dy << 16 | dx}
+    // with dy = khi*dh, dx = kwi*dw.  One broadcast LDS read per k, no divisions.
+    __device__ __forceinline__ void load_tab(const GemmArgs& g, uint32_t k0, const int2* tab) {
+        const uint32_t ks = k0 + (threadIdx.x >> 7) * 32;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+            int16_t v[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                v[e] = 0;
+                const uint32_t k = ks + 2 * j + e;
+                if (col_ok && k < g.k) {
+                    const int2 t = tab[k];
+                    const int32_t ih = ih0 + (t.y >> 16), iw = iw0 + (t.y & 0xFFFF);
+                    if ((uint32_t)ih < g.H && (uint32_t)iw < g.W) v[e] = xb[pbase + t.x];
+                }
+            }
+            w[j] = pack2(v[0], v[1]);
+        }
     }
     __device__ __forceinline__ void load(const GemmArgs& g, uint32_t k0) {
         const uint32_t ks = k0 + (threadIdx.x >> 7) * 32;
@@ -231,16 +268,16 @@ struct ConvBTile {
             w[j] = pack2(v[0], v[1]);
         }
     }
-    __device__ __forceinline__ void store(Smem& s) {
+    __device__ __forceinline__ void store(Smem& s, int32_t& hs, int32_t& ls) const {
         const uint32_t off = (threadIdx.x & 127) * kStride + (threadIdx.x >> 7) * 32;
         uint32_t hi[8], lo[8];
-        int32_t sum = 0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            split4(w[2 * j], w[2 * j + 1], hi[j], lo[j]);
-            sum += wsum(w[2 * j]) + wsum(w[2 * j + 1]);
+            hi[j] = hi4(w[2 * j], w[2 * j + 1]);
+            lo[j] = lo4(w[2 * j], w[2 * j + 1]);
+            hs = bsum(hi[j], hs);
+            ls = bsum(lo[j], ls);
         }
-        col_sum += (uint32_t)sum;
         v4i* dh = reinterpret_cast<v4i*>(s.b_hi + off);
         v4i* dl = reinterpret_cast<v4i*>(s.b_lo + off);
         dh[0] = v4i{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
@@ -248,13 +285,16 @@ struct ConvBTile {
         dl[0] = v4i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
         dl[1] = v4i{(int)lo[4], (int)lo[5], (int)lo[6], (int)lo[7]};
     }
-    __device__ __forceinline__ void publish_sums(Smem& s) const {
-        atomicAdd(&s.col_sum[threadIdx.x & 127], col_sum);
-    }
 };
 
-template <bool CONV, bool HAS_BIAS, bool FOLD>
+// B-operand modes: dense matrix, implicit-GEMM gather with an LDS k table
+// (K <= kTabMax), implicit-GEMM gather with incremental k decomposition.
+enum { B_DENSE = 0, B_CONV_TAB = 1, B_CONV_INC = 2 };
+constexpr uint32_t kTabMax = 2048;
+
+template <int MODE, bool HAS_BIAS, bool FOLD>
 __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
+    constexpr bool CONV = MODE != B_DENSE;
     __shared__ __align__(16) Smem s;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t wave = threadIdx.x >> 6;
@@ -266,12 +306,31 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     const int16_t* bbase = g.b + (CONV ? 0 : (uint64_t)blockIdx.z * g.b_bs);
 
     if (threadIdx.x < BN) s.col_sum[threadIdx.x] = 0;   // published with atomics at the end
+    const int2* tab = nullptr;
+    if constexpr (MODE == B_CONV_TAB) {
+        __shared__ int2 ktab[kTabMax];
+        const uint32_t kk = g.kh * g.kw, hw = g.H * g.W;
+        for (uint32_t k = threadIdx.x; k < g.k; k += kThreads) {
+            const uint32_t c = k / kk, r = k - (k / kk) * kk;
+            const uint32_t khi = r / g.kw, kwi = r - (r / g.kw) * g.kw;
+            const uint32_t dy = khi * g.dh, dx = kwi * g.dw;
+            ktab[k] = int2{(int)(c * hw + dy * g.W + dx), (int)((dy << 16) | dx)};
+        }
+        tab = ktab;
+    }
     __syncthreads();
 
-    ATile at;
-    typename std::conditional<CONV, ConvBTile, DenseBTile>::type bt;
-    uint32_t row_sum = 0;
-    if constexpr (CONV) bt.init(g, col0); else bt.init();
+    // One register stage: the next tile's global loads are issued before the
+    // MFMA phase and staged in LDS after it.  (A second register stage does not
+    // fit beside the 192 accumulator registers without spilling, and measured
+    // slower.)
+    ATile at0;
+    using BTile = typename std::conditional<CONV, ConvBTile, DenseBTile>::type;
+    BTile bt0;
+    int32_t row_hs = 0, row_ls = 0;
+    int32_t dhs[8] = {0, 0, 0, 0, 0, 0, 0, 0}, dls[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int32_t chs = 0, cls = 0;
+    if constexpr (CONV) bt0.init(g, col0);
 
     v4i hh[4][4], mid[4][4], ll[4][4], tot[4][4];
 #pragma unroll
@@ -282,20 +341,22 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
             if constexpr (FOLD) tot[i][j] = v4i{0, 0, 0, 0};
         }
 
-    const uint32_t nk = (g.k + BK - 1) / BK;
-    at.load(g, abase, row0, 0);
-    if constexpr (CONV) bt.load(g, 0); else bt.load(g, bbase, col0, 0);
-
-    for (uint32_t it = 0; it < nk; ++it) {
+    auto load_tile = [&](ATile& at, BTile& bt, uint32_t k0) {
+        at.load(g, abase, row0, k0);
+        if constexpr (MODE == B_CONV_TAB) bt.load_tab(g, k0, tab);
+        else if constexpr (MODE == B_CONV_INC) bt.load(g, k0);
+        else bt.load(g, bbase, col0, k0);
+    };
+    auto stage_tile = [&](const ATile& at, const BTile& bt) {
         __syncthreads();                 // previous tile fully consumed
-        at.store(s, row_sum);
-        bt.store(s);
+        at.store(s, row_hs, row_ls);
+        if constexpr (CONV) bt.store(s, chs, cls); else bt.store(s, dhs, dls);
         __syncthreads();
-        if (it + 1 < nk) {               // next tile's loads overlap the MFMAs below
-            at.load(g, abase, row0, (it + 1) * BK);
-            if constexpr (CONV) bt.load(g, (it + 1) * BK); else bt.load(g, bbase, col0, (it + 1) * BK);
-        }
-        v4i ah[4], al[4], bh[4], bl[4];
+    };
+    auto mfma_step = [&](uint32_t it) {
+        // A fragments for the wave's 4 row tiles stay live; B fragments are
+        // read one column tile at a time (8 registers instead of 32).
+        v4i ah[4], al[4];
         const uint32_t koff = (lane >> 4) * 16;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -306,29 +367,21 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint32_t cidx = (wcol + j * 16 + (lane & 15)) * kStride + koff;
-            bh[j] = *reinterpret_cast<const v4i*>(s.b_hi + cidx);
-            bl[j] = *reinterpret_cast<const v4i*>(s.b_lo + cidx);
+            const v4i bh = *reinterpret_cast<const v4i*>(s.b_hi + cidx);
+            const v4i bl = *reinterpret_cast<const v4i*>(s.b_lo + cidx);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                hh[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bh, hh[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                mid[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bl, mid[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                ll[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], bl, ll[i][j], 0, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                mid[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], bh, mid[i][j], 0, 0, 0);
         }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                hh[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bh[j], hh[i][j], 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                mid[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bl[j], mid[i][j], 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                mid[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], bh[j], mid[i][j], 0, 0, 0);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                ll[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], bl[j], ll[i][j], 0, 0, 0);
 
         if constexpr (FOLD) {
             if ((it + 1) % kFoldIters == 0) {
@@ -344,12 +397,25 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
                     }
             }
         }
+    };
+
+    const uint32_t nk = (g.k + BK - 1) / BK;
+    load_tile(at0, bt0, 0);
+    for (uint32_t it = 0; it < nk; ++it) {
+        stage_tile(at0, bt0);
+        if (it + 1 < nk) load_tile(at0, bt0, (it + 1) * BK);
+        mfma_step(it);
     }
 
-    // row sums: the two threads of a row are adjacent lanes
+    // row sums (sum a = 256*hs + ls + 128*count); the two threads of a row are
+    // adjacent lanes, each stored 32 k values per step
+    uint32_t row_sum = 256u * (uint32_t)row_hs + (uint32_t)row_ls + 128u * 32u * nk;
     row_sum += (uint32_t)__shfl_xor((int)row_sum, 1, 64);
     if ((threadIdx.x & 1) == 0) s.row_sum[threadIdx.x >> 1] = row_sum;
-    bt.publish_sums(s);
+    if constexpr (CONV)
+        atomicAdd(&s.col_sum[threadIdx.x & 127], 256u * (uint32_t)chs + (uint32_t)cls + 128u * 32u * nk);
+    else
+        publish_dense(s, dhs, dls, 4u * nk);
     __syncthreads();
 
     const uint32_t kp_term = 16384u * (nk * (uint32_t)BK);
@@ -390,7 +456,7 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
-template <bool CONV>
+template <int MODE>
 int launch_gemm(GemmArgs& g, uint32_t zdim, hipStream_t s, const char* name) {
     const dim3 grid((g.cols + BN - 1) / BN, (g.rows + BM - 1) / BM, zdim);
     if (grid.y > 65535u || grid.z > 65535u || grid.x > 0x7FFFFFFFu)
@@ -398,7 +464,7 @@ int launch_gemm(GemmArgs& g, uint32_t zdim, hipStream_t s, const char* name) {
     const bool fold = g.k > (uint32_t)(kFoldIters * BK);
     const bool bias = g.bias != nullptr;
 #define CM_GEMM_LAUNCH(B, F) \
-    hipLaunchKernelGGL((q88_gemm<CONV, B, F>), grid, dim3(kThreads), 0, s, g)
+    hipLaunchKernelGGL((q88_gemm<MODE, B, F>), grid, dim3(kThreads), 0, s, g)
     if (bias) { if (fold) CM_GEMM_LAUNCH(true, true); else CM_GEMM_LAUNCH(true, false); }
     else { if (fold) CM_GEMM_LAUNCH(false, true); else CM_GEMM_LAUNCH(false, false); }
 #undef CM_GEMM_LAUNCH
@@ -433,7 +499,7 @@ int cm_matmul_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n,
         gz.a = g.a + (uint64_t)done * a_bs;
         gz.b = g.b + (uint64_t)done * b_bs;
         gz.c = g.c + (uint64_t)done * c_bs;
-        const int rc = launch_gemm<false>(gz, z, s, "matmul");
+        const int rc = launch_gemm<B_DENSE>(gz, z, s, "matmul");
         if (rc) return rc;
         done += z;
     }
@@ -462,7 +528,11 @@ int cm_conv_gemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias,
     g.kh = kh; g.kw = kw; g.sh = sh; g.sw = sw; g.dh = dh; g.dw = dw; g.pt = pad_top; g.pl = pad_left;
     g.x_img = x_img;
     g.y_img = (uint64_t)out_ch * P;
-    return launch_gemm<true>(g, 1, s, "conv_gemm");
+    // the k table holds offsets < 2^31 and dy, dx < 2^16
+    const bool table = K <= kTabMax && (uint64_t)(kh - 1) * dh < 65536u &&
+                       (uint64_t)(kw - 1) * dw < 65536u;
+    if (table) return launch_gemm<B_CONV_TAB>(g, 1, s, "conv_gemm");
+    return launch_gemm<B_CONV_INC>(g, 1, s, "conv_gemm");
 }
 
 int cm_conv_pointwise_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
@@ -483,7 +553,7 @@ int cm_conv_pointwise_launch(const int16_t* x, const int16_t* w, const int16_t* 
         GemmArgs gz = g;
         gz.b = x + (uint64_t)done * g.b_bs;
         gz.c = y + (uint64_t)done * g.c_bs;
-        const int rc = launch_gemm<false>(gz, z, s, "conv_pointwise");
+        const int rc = launch_gemm<B_DENSE>(gz, z, s, "conv_pointwise");
         if (rc) return rc;
         done += z;
     }

@@ -107,14 +107,18 @@ __global__ __launch_bounds__(kThreads) void pool_global(const int16_t* __restric
 
 // ------------------------------------------------------------------ band --
 // Block = (plane, band of `band_h` output rows).  Stages the input rows the
-// band needs (full width) in LDS, then computes the band.  Padded taps are
-// skipped: they add 0 to sums, and for MAX the initial accumulator (kAccMin)
-// already gives -32768 when no tap is valid, as padding with kDataMin does.
-template <int KIND>
+// band needs (full width) in LDS, then computes the band.  Threads are laid
+// out as (row, column) with `tw` columns (a power of two covering out_w, at
+// most 64), so no per-output division is needed.  KH/KW > 0 fix the window
+// at compile time (dilation 1) so the tap loops unroll; 0 = runtime window.
+// Padded taps are skipped: they add 0 to sums, and for MAX the initial
+// accumulator (kAccMin) already gives -32768 when no tap is valid, as padding
+// with kDataMin does.
+template <int KIND, int KH, int KW>
 __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict__ x,
                                                       int16_t* __restrict__ y, PoolGeom g,
                                                       uint32_t band_h, uint32_t n_bands,
-                                                      float inv_full) {
+                                                      float inv_full, uint32_t tw_log2) {
     extern __shared__ __align__(16) int16_t lds[];
     const uint64_t plane = blockIdx.x / n_bands;
     const uint32_t band = blockIdx.x - (uint32_t)(plane * n_bands);
@@ -162,31 +166,35 @@ __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict_
 
     // staged element (ih, iw), ih in [r_lo, r_hi): lds[shift + (ih - r_lo) * in_w + iw]
     const int16_t* rows = lds + shift;
-    const uint32_t count = (oh1 - oh0) * g.out_w;
-    int16_t* yp = y + plane * (uint64_t)g.out_h * g.out_w + (uint64_t)oh0 * g.out_w;
-    const int32_t ph = (int32_t)g.ph, pw = (int32_t)g.pw, dh = (int32_t)g.dh, dw = (int32_t)g.dw;
-    for (uint32_t idx = threadIdx.x; idx < count; idx += kThreads) {
-        const uint32_t r = idx / g.out_w;
-        const uint32_t ow = idx - r * g.out_w;
-        const int32_t ih0 = (int32_t)((oh0 + r) * g.sh) - (int32_t)g.pt;
-        const int32_t iw0 = (int32_t)(ow * g.sw) - (int32_t)g.pl;
-        Acc<KIND> a;
-        for (int32_t khi = 0; khi < ph; ++khi) {
-            const int32_t ih = ih0 + khi * dh;
-            if ((uint32_t)ih >= (uint32_t)in_h) continue;
-            const int16_t* row = rows + (ih - r_lo) * in_w;
-            for (int32_t kwi = 0; kwi < pw; ++kwi) {
-                const int32_t iw = iw0 + kwi * dw;
-                if ((uint32_t)iw < (uint32_t)in_w) a.add(row[iw]);
+    int16_t* yp = y + plane * (uint64_t)g.out_h * g.out_w;
+    const int32_t ph = KH > 0 ? KH : (int32_t)g.ph, pw = KW > 0 ? KW : (int32_t)g.pw;
+    const int32_t dh = KH > 0 ? 1 : (int32_t)g.dh, dw = KW > 0 ? 1 : (int32_t)g.dw;
+    const uint32_t tw = 1u << tw_log2;
+    const uint32_t c0 = threadIdx.x & (tw - 1);
+    for (uint32_t oh = oh0 + (threadIdx.x >> tw_log2); oh < oh1; oh += kThreads >> tw_log2) {
+        const int32_t ih0 = (int32_t)(oh * g.sh) - (int32_t)g.pt;
+        for (uint32_t ow = c0; ow < g.out_w; ow += tw) {
+            const int32_t iw0 = (int32_t)(ow * g.sw) - (int32_t)g.pl;
+            Acc<KIND> a;
+#pragma unroll
+            for (int32_t khi = 0; khi < (KH > 0 ? KH : ph); ++khi) {
+                const int32_t ih = ih0 + khi * dh;
+                if ((uint32_t)ih >= (uint32_t)in_h) continue;
+                const int16_t* row = rows + (ih - r_lo) * in_w;
+#pragma unroll
+                for (int32_t kwi = 0; kwi < (KW > 0 ? KW : pw); ++kwi) {
+                    const int32_t iw = iw0 + kwi * dw;
+                    if ((uint32_t)iw < (uint32_t)in_w) a.add(row[iw]);
+                }
             }
+            float inv = inv_full;
+            if constexpr (KIND == K_AVG) {
+                if (!g.cip)
+                    inv = q88::inv_denom((uint32_t)(valid_taps(ih0, ph, dh, in_h) *
+                                                    valid_taps(iw0, pw, dw, in_w)));
+            }
+            yp[(uint64_t)oh * g.out_w + ow] = a.finish(inv);
         }
-        float inv = inv_full;
-        if constexpr (KIND == K_AVG) {
-            if (!g.cip)
-                inv = q88::inv_denom((uint32_t)(valid_taps(ih0, ph, dh, in_h) *
-                                                valid_taps(iw0, pw, dw, in_w)));
-        }
-        yp[idx] = a.finish(inv);
     }
 }
 
@@ -287,8 +295,19 @@ int pool_launch(const int16_t* x, int16_t* y, uint64_t planes, const PoolGeom& g
             uint64_t need = rows_needed(g, band_h);
             if (need > g.in_h) need = g.in_h;
             const uint32_t lds = (uint32_t)(need * row_bytes + 16);
-            hipLaunchKernelGGL(pool_band<KIND>, dim3((uint32_t)blocks), dim3(kThreads), lds, s, x,
-                               y, g, band_h, n_bands, inv_full);
+            uint32_t tw_log2 = 0;
+            while ((1u << tw_log2) < g.out_w && tw_log2 < 6) ++tw_log2;
+            const dim3 grid((uint32_t)blocks), block(kThreads);
+            const bool unit_dil = g.dh == 1 && g.dw == 1;
+            if (unit_dil && g.ph == 3 && g.pw == 3)
+                hipLaunchKernelGGL((pool_band<KIND, 3, 3>), grid, block, lds, s, x, y, g, band_h,
+                                   n_bands, inv_full, tw_log2);
+            else if (unit_dil && g.ph == 2 && g.pw == 2)
+                hipLaunchKernelGGL((pool_band<KIND, 2, 2>), grid, block, lds, s, x, y, g, band_h,
+                                   n_bands, inv_full, tw_log2);
+            else
+                hipLaunchKernelGGL((pool_band<KIND, 0, 0>), grid, block, lds, s, x, y, g, band_h,
+                                   n_bands, inv_full, tw_log2);
             return cm_check_launch("pool_band");
         }
     }

@@ -63,6 +63,8 @@ GEOMS = [
     (1, 130, 9, 9, 7, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0),      # K = 1170 (many k tiles)
     (2, 12, 10, 10, 12, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1),    # depthwise
     (1, 6, 9, 9, 4, 5, 5, 2, 2, 1, 1, 2, 2, 0, 1),        # depthwise, out_ch < in_ch
+    (1, 256, 6, 6, 20, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0),     # K = 2304: gather without the k table
+    (1, 40, 11, 11, 9, 7, 7, 1, 1, 3, 2, 9, 6, 1, 0),     # large dilation, pad beyond the window
 ]
 
 
