@@ -11,7 +11,10 @@ ports = 3 for binary and 2 for unary ops (bench_src/bench_vectorop.c:93-95).
 The same run also reports (under "results") the GEMM, convolution and pooling
 configurations: Q8.8 GOP/s = 2*MAC / t (bench_matmul.c:95, bench_conv.c:129-132)
 with the int8-MFMA utilisation of the four limb products, and pool GB/s =
-(x + y) * 2 B / t (bench_pool.c:116-117) with rotating input buffers.
+(x + y) * 2 B / t (bench_pool.c:116-117) with rotating input buffers; and the
+two ONNX graphs run by the scheduler's HIP backend: the MLP's batch-64 latency
+and the MobileNetV2-like graph's images/s at batch 16, each with its roofline
+fraction (sum of per-kernel lower bounds / measured time).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
 """
@@ -199,6 +202,79 @@ def bench_pool(steps: int, warmup: int):
     return out
 
 
+# ----------------------------------------------------------------- graphs --
+def graph_lower_bound_s(plan) -> float:
+    """Sum over kernel calls of max(HBM time of the algorithmic bytes, int8-MFMA time of
+    the four limb products): the graph's roofline time."""
+    total = 0.0
+    for _, call in plan.calls:
+        nbytes = 2 * sum(call.extents().values())
+        macs = 0
+        a = call.args
+        if call.kernel in ("matmul", "matmul_at"):
+            macs = a[0] * a[1] * a[2] * a[3]
+        elif call.kernel == "conv":
+            nb, c, _, _, mo, oh, ow, kh, kw = a[:9]
+            macs = nb * mo * oh * ow * (1 if a[16] else c) * kh * kw
+        total += max(nbytes / (HBM_PEAK_GBS * 1e9),
+                     LIMB_PRODUCTS * 2 * macs / (INT8_PEAK_TOPS * 1e12))
+    return total
+
+
+def bench_graphs(steps: int, warmup: int, check: bool):
+    """Config 1 (MLP b64 latency) and config 5 (MobileNetV2-like b16 images/s) through
+    the scheduler's HIP backend, inputs resident on the device."""
+    import torch
+    from cormorant_amd import workloads as wl
+    from cormorant_amd.scheduler import InferenceSession, OnnxGraph, onnx_io as ox
+    out = {}
+    cases = (("mlp_b64", wl.mlp_model(), wl.mlp_input(), wl.MLP_BATCH),
+             ("mobilenet_like_b16", wl.mobilenet_model(), wl.mobilenet_input(),
+              wl.MOBILENET_BATCH))
+    for name, model, x, batch in cases:
+        g = OnnxGraph(ox.encode_model(model))
+        sess = InferenceSession(g)
+        sess.write_input("X", x)
+        cur = lambda: torch.cuda.current_stream().cuda_stream
+        launch = lambda: sess.launch(cur())
+        for _ in range(warmup):
+            launch()
+        torch.cuda.synchronize()
+        ms = time_launches([launch], steps)
+        ms_graph = time_graph([launch], max(steps, 4))
+        macs = sum(c.args[0] * c.args[1] * c.args[2] * c.args[3]
+                   for _, c in sess.plan.calls if c.kernel.startswith("matmul"))
+        macs += sum(c.args[0] * c.args[4] * c.args[5] * c.args[6] *
+                    (1 if c.args[16] else c.args[1]) * c.args[7] * c.args[8]
+                    for _, c in sess.plan.calls if c.kernel == "conv")
+        lb = graph_lower_bound_s(sess.plan)
+        e = dict(kernel_calls=len(sess.plan.calls), gmac=round(macs / 1e9, 4),
+                 ms=round(ms, 4), ms_hip_graph=round(ms_graph, 4),
+                 images_s=round(batch / (ms * 1e-3), 1),
+                 images_s_hip_graph=round(batch / (ms_graph * 1e-3), 1),
+                 gops=round(2 * macs / (ms_graph * 1e-3) / 1e9, 1),
+                 roofline_lower_bound_ms=round(lb * 1e3, 4),
+                 roofline_frac=round(lb * 1e3 / ms_graph, 4),
+                 pool_bytes=2 * sess.plan.pool_elems)
+        y = sess.read_output("Y")
+        if check:
+            import oracle
+            from oracle import graph_sim as gs
+            threads = min(os.cpu_count() or 1, 16)
+            oracle.set_threads(threads)
+            t0 = time.perf_counter()
+            want = gs.run_plan(sess.plan, {"X": x}, threads=True)["Y"]
+            dt = time.perf_counter() - t0
+            if not np.array_equal(y, want):
+                raise SystemExit(f"bench: GPU {name} output differs from the oracle")
+            e["cpu"] = dict(ms=round(dt * 1e3, 2), images_s=round(batch / dt, 2), cores=threads,
+                            kind="port", sample="whole graph, kernel-call list on the oracle, "
+                                                "OpenMP over each kernel's outer loop")
+        sess.close()
+        out[name] = e
+    return out
+
+
 # ------------------------------------------------------------ cpu baseline --
 def cpu_baseline(vec_bufs, extras: dict):
     """The oracle (C restatement of the reference C-simulation loops, -O2) timed
@@ -345,6 +421,8 @@ def main() -> int:
         extras.update(bench_gemm(max(5, args.steps // 2), 2))
         extras.update(bench_conv(max(5, args.steps // 2), 2))
         extras.update(bench_pool(max(args.steps, POOL_ROTATE), 2))
+        log("scheduler graphs: MLP b64, MobileNetV2-like b16")
+        graphs = bench_graphs(max(5, args.steps // 2), 2, check=True)
         log("CPU baseline (oracle, 1 thread) and sample check")
         cpu_res = cpu_baseline(bufs, extras)
         for name, e in extras.items():
@@ -353,6 +431,7 @@ def main() -> int:
                 e["cpu_1t"] = {k: (round(v, 4) if isinstance(v, float) else v)
                                for k, v in cpu_res[name].items()}
             results[name] = e
+        results.update(graphs)
         cpu = dict(value=round(cpu_res["vecop"]["gbs"], 3), unit="GB/s", cores=1, kind="port",
                    sample="the full six-op 64Mi-element sweep, oracle C restatement -O2, one thread",
                    seconds=round(cpu_res["vecop"]["seconds"], 3))

@@ -27,6 +27,14 @@ int hip_fail(hipError_t e, const char* what) {
     return cm_set_error(CM_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+// A run_* call touches elements [off, off + need) of buffer b; it must hold them.
+bool fits(const cm_buf_t* b, uint64_t off, uint64_t need, const char* fn, const char* name) {
+    if (off + need <= b->count) return true;
+    cm_set_error(CM_ERR_RANGE, "%s: buffer %s holds %u elements, the call touches %llu", fn, name,
+                 b->count, (unsigned long long)(off + need));
+    return false;
+}
+
 }  // namespace
 
 int cm_set_error(int code, const char* fmt, ...) {
@@ -190,22 +198,35 @@ int cm_buf_sync_from_device(cm_buf_t* b) {
 
 int cm_run_op(cm_buf_t* a, cm_buf_t* b, cm_buf_t* c, uint32_t size, uint32_t op,
               uint32_t outer, uint32_t a_inc, uint32_t b_inc) {
-    if (!a || !c) return cm_set_error(CM_ERR_INVALID, "run_op: null buffer");
+    if (!a || !c || (op < CM_OP_RELU && !b)) return cm_set_error(CM_ERR_INVALID, "run_op: null buffer");
+    if (size && outer) {
+        const uint64_t o = outer - 1ull;
+        if (!fits(a, 0, o * a_inc + size, "run_op", "a") ||
+            (op < CM_OP_RELU && !fits(b, 0, o * b_inc + size, "run_op", "b")) ||
+            !fits(c, 0, o * ((uint64_t)a_inc + b_inc) + size, "run_op", "c"))
+            return CM_ERR_RANGE;
+    }
     return cm_vectorop(a->dev, b ? b->dev : nullptr, c->dev, size, op, outer, a_inc, b_inc, nullptr);
-}
-
-int cm_run_matmul(cm_buf_t* a, cm_buf_t* b, cm_buf_t* c, uint32_t n, uint32_t k, uint32_t m,
-                  uint32_t batch, uint32_t a_stride, uint32_t b_stride, uint32_t c_stride) {
-    if (!a || !b || !c) return cm_set_error(CM_ERR_INVALID, "run_matmul: null buffer");
-    return cm_matmul(a->dev, b->dev, c->dev, n, k, m, batch, a_stride, b_stride, c_stride, nullptr);
 }
 
 int cm_run_matmul_at(cm_buf_t* a, uint32_t a_off, cm_buf_t* b, uint32_t b_off, cm_buf_t* c,
                      uint32_t c_off, uint32_t n, uint32_t k, uint32_t m, uint32_t batch,
                      uint32_t a_stride, uint32_t b_stride, uint32_t c_stride) {
-    if (!a || !b || !c) return cm_set_error(CM_ERR_INVALID, "run_matmul_at: null buffer");
+    if (!a || !b || !c) return cm_set_error(CM_ERR_INVALID, "run_matmul: null buffer");
+    if (n && m && batch) {
+        const uint64_t o = batch - 1ull;
+        if (!fits(a, a_off, o * a_stride + (uint64_t)n * k, "run_matmul", "a") ||
+            !fits(b, b_off, o * b_stride + (uint64_t)k * m, "run_matmul", "b") ||
+            !fits(c, c_off, o * c_stride + (uint64_t)n * m, "run_matmul", "c"))
+            return CM_ERR_RANGE;
+    }
     return cm_matmul_at(a->dev, a_off, b->dev, b_off, c->dev, c_off, n, k, m, batch, a_stride,
                         b_stride, c_stride, nullptr);
+}
+
+int cm_run_matmul(cm_buf_t* a, cm_buf_t* b, cm_buf_t* c, uint32_t n, uint32_t k, uint32_t m,
+                  uint32_t batch, uint32_t a_stride, uint32_t b_stride, uint32_t c_stride) {
+    return cm_run_matmul_at(a, 0, b, 0, c, 0, n, k, m, batch, a_stride, b_stride, c_stride);
 }
 
 int cm_run_conv(cm_buf_t* x, cm_buf_t* weight, cm_buf_t* bias, cm_buf_t* y, uint32_t batch,
@@ -213,7 +234,15 @@ int cm_run_conv(cm_buf_t* x, cm_buf_t* weight, cm_buf_t* bias, cm_buf_t* y, uint
                 uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h, uint32_t stride_w,
                 uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top, uint32_t pad_left,
                 uint32_t has_bias, uint32_t is_depthwise) {
-    if (!x || !weight || !y) return cm_set_error(CM_ERR_INVALID, "run_conv: null buffer");
+    if (!x || !weight || !y || (has_bias && !bias))
+        return cm_set_error(CM_ERR_INVALID, "run_conv: null buffer");
+    const uint64_t ny = (uint64_t)batch * out_ch * out_h * out_w;
+    if (ny && (!fits(x, 0, (uint64_t)batch * in_ch * in_h * in_w, "run_conv", "x") ||
+               !fits(weight, 0, (uint64_t)out_ch * (is_depthwise ? 1u : in_ch) * kh * kw,
+                     "run_conv", "weight") ||
+               (has_bias && !fits(bias, 0, out_ch, "run_conv", "bias")) ||
+               !fits(y, 0, ny, "run_conv", "y")))
+        return CM_ERR_RANGE;
     return cm_conv(x->dev, weight->dev, bias ? bias->dev : nullptr, y->dev, batch, in_ch, in_h,
                    in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w, dilation_h,
                    dilation_w, pad_top, pad_left, has_bias, is_depthwise, nullptr);
@@ -225,6 +254,10 @@ int cm_run_pool(cm_buf_t* x, cm_buf_t* y, uint32_t batch, uint32_t channels, uin
                 uint32_t dil_h, uint32_t dil_w, uint32_t pool_type, uint32_t lp_order,
                 uint32_t count_include_pad) {
     if (!x || !y) return cm_set_error(CM_ERR_INVALID, "run_pool: null buffer");
+    const uint64_t ny = (uint64_t)batch * channels * out_h * out_w;
+    if (ny && (!fits(x, 0, (uint64_t)batch * channels * in_h * in_w, "run_pool", "x") ||
+               !fits(y, 0, ny, "run_pool", "y")))
+        return CM_ERR_RANGE;
     return cm_pool(x->dev, y->dev, batch, channels, in_h, in_w, out_h, out_w, pool_h, pool_w,
                    stride_h, stride_w, pad_top, pad_left, dil_h, dil_w, pool_type, lp_order,
                    count_include_pad, nullptr);

@@ -1,0 +1,149 @@
+"""HIP backend of the scheduler: run a scheduled ONNX graph on one GPU.
+
+Replaces the generated KV260 runtime (inference_init / inference_run,
+inference-scheduler/src/codegen/_source.py:475-791) with calls into
+libcormorant_amd.so:
+
+* init: one ``cm_buf_alloc`` for the pool (weights + intermediates, 64-byte
+  aligned slots, intermediates with disjoint lifetimes sharing a slot), one
+  buffer per graph input and output, weights copied in once;
+* run: graph inputs copied to the device, every kernel call enqueued in graph
+  order on one in-order stream, graph outputs copied back (the only host
+  synchronisation, as in the reference's sync_from_device).
+
+Reshape / Squeeze / Unsqueeze / Dropout outputs are the same device address
+as their source; a graph output at the end of a reshape chain is written
+directly by the producing kernel.  There is no CPU execution path: without the
+native library the constructor raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Dict, List, Optional, Tuple
+
+import numpy as np
+
+from .. import _native
+from .graph import OnnxGraph
+from .nodes import KernelCall
+from .plan import BufferPlan
+
+_FUNCS = {"op": "cm_vectorop", "matmul": "cm_matmul", "matmul_at": "cm_matmul",
+          "conv": "cm_conv", "pool": "cm_pool"}
+
+
+class InferenceSession:
+    """Device-resident instance of one model (weights loaded, buffers allocated)."""
+
+    def __init__(self, model, stream: int = 0) -> None:
+        self.graph = model if isinstance(model, OnnxGraph) else OnnxGraph(model)
+        self.plan = BufferPlan(self.graph)
+        self._lib = _native.load()
+        self.stream = int(stream)
+        _native.call("cm_buf_pool_init")
+        self._bufs: Dict[Tuple[str, str], object] = {}
+        try:
+            if self.plan.pool_elems:
+                pool = self._alloc(("pool", ""), self.plan.pool_elems)
+                self._host(pool, self.plan.pool_elems)[:] = self.plan.pool_image()
+                _native.call("cm_buf_sync_to_device", pool)
+            for t in self.graph.input_tensors:
+                self._alloc(("input", t.onnx_name), self.plan.layouts[t.onnx_name].alloc)
+            for t in self.graph.output_tensors:
+                self._alloc(("output", t.onnx_name), self.plan.layouts[t.onnx_name].alloc)
+            _native.call("cm_sync", None)
+            self._launches = [self._prepare(c) for _, c in self.plan.calls]
+        except Exception:
+            self.close()
+            raise
+
+    # ------------------------------------------------------------------ buffers
+
+    def _alloc(self, key, n: int):
+        if n >= 1 << 32:
+            raise ValueError(f"buffer {key} of {n} elements exceeds the uint32 element count")
+        b = self._lib.cm_buf_alloc(n)
+        if not b:
+            raise _native.CmError("cm_buf_alloc", _native.CM_ERR_NOMEM, _native.last_error())
+        self._bufs[key] = b
+        return b
+
+    @staticmethod
+    def _host(buf, n: int) -> np.ndarray:
+        p = buf.contents.host
+        return np.ctypeslib.as_array(ctypes.cast(p, ctypes.POINTER(ctypes.c_int16)), shape=(n,))
+
+    def device_ptr(self, name: str) -> int:
+        """Device address of a tensor's storage (graph inputs/outputs, weights, intermediates)."""
+        st = self.plan.storage[name]
+        buf = self._bufs[(st.kind, st.key)]
+        return int(buf.contents.dev) + 2 * st.offset
+
+    def _prepare(self, call: KernelCall):
+        fn = getattr(self._lib, _FUNCS[call.kernel])
+        ptrs = []
+        for i, name in enumerate(call.tensors):
+            if name is None:
+                ptrs.append(None)
+                continue
+            p = self.device_ptr(name)
+            if call.offsets:
+                p += 2 * call.offsets[i]
+            ptrs.append(p)
+        return fn, _FUNCS[call.kernel], tuple(ptrs) + tuple(call.args)
+
+    # ------------------------------------------------------------------ running
+
+    def launch(self, stream: Optional[int] = None) -> None:
+        """Enqueue every kernel of the graph (inputs must already be on the device)."""
+        s = self.stream if stream is None else int(stream)
+        s = s or None
+        for fn, name, args in self._launches:
+            rc = fn(*args, s)
+            if rc:
+                raise _native.CmError(name, rc, _native.last_error())
+
+    def write_input(self, name: str, raw) -> None:
+        """Copy one graph input (raw int16 Q8.8, logical shape) to the device."""
+        buf = self._bufs[("input", name)]
+        host = self._host(buf, self.plan.layouts[name].alloc)
+        self.plan.scatter(name, raw, host)
+        _native.call("cm_buf_sync_to_device", buf)
+
+    def read_output(self, name: str) -> np.ndarray:
+        """Wait for the stream and return one graph output (raw int16, logical shape)."""
+        buf = self._bufs[("output", name)]
+        _native.call("cm_buf_sync_from_device", buf)
+        return self.plan.gather(name, self._host(buf, self.plan.layouts[name].alloc))
+
+    def run(self, feeds: Dict[str, np.ndarray]) -> Dict[str, np.ndarray]:
+        """inference_run: raw int16 inputs -> raw int16 outputs, by tensor name."""
+        missing = [t.onnx_name for t in self.graph.input_tensors if t.onnx_name not in feeds]
+        if missing:
+            raise KeyError(f"missing graph inputs: {missing}")
+        prev = self._lib.cm_get_stream()
+        if self.stream:
+            self._lib.cm_set_stream(self.stream)
+        try:
+            for t in self.graph.input_tensors:
+                self.write_input(t.onnx_name, feeds[t.onnx_name])
+            self.launch()
+            return {t.onnx_name: self.read_output(t.onnx_name) for t in self.graph.output_tensors}
+        finally:
+            if self.stream:
+                self._lib.cm_set_stream(prev)
+
+    @property
+    def kernel_calls(self) -> List[KernelCall]:
+        return [c for _, c in self.plan.calls]
+
+    def close(self) -> None:
+        for b in self._bufs.values():
+            self._lib.cm_buf_free(b)
+        self._bufs = {}
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -160,3 +160,104 @@ def pool_args(case: PoolCase, n: int, c: int, hw: int):
     return dict(batch=n, channels=c, in_h=hw, in_w=hw, out_h=o, out_w=o, pool_h=k, pool_w=k,
                 stride_h=s, stride_w=s, pad_top=p, pad_left=p, dil_h=1, dil_w=1,
                 pool_type=case.pool_type, lp_order=case.lp_order, count_include_pad=case.cip)
+
+
+# ---------------------------------------------------------------- ONNX graphs --
+def _q88_initializer(name: str, raw: np.ndarray):
+    """An ONNX float32 initializer holding on-grid Q8.8 values (raw / 256, exact)."""
+    from .scheduler import onnx_io as ox
+    return ox.from_array((raw.astype(np.float32) / np.float32(256.0)), name)
+
+
+# config 1: 2-layer MLP, batch 64: Gemm 784->256, Relu, Gemm 256->10
+MLP_BATCH, MLP_IN, MLP_HIDDEN, MLP_OUT = 64, 784, 256, 10
+
+
+def mlp_model(batch: int = MLP_BATCH):
+    """X[b,784] -> Gemm(W1,b1) -> Relu -> Gemm(W2,b2) -> Y[b,10]; weights N(0,0.1),
+    biases N(0,0.05), quantised AP_TRN+AP_SAT."""
+    from .scheduler import onnx_io as ox
+    w1 = normal_q88(rng(1, 1), (MLP_IN, MLP_HIDDEN), 0.1)
+    b1 = normal_q88(rng(1, 2), (MLP_HIDDEN,), 0.05)
+    w2 = normal_q88(rng(1, 3), (MLP_HIDDEN, MLP_OUT), 0.1)
+    b2 = normal_q88(rng(1, 4), (MLP_OUT,), 0.05)
+    nodes = [
+        ox.make_node("Gemm", ["X", "W1", "B1"], ["H"], name="fc1"),
+        ox.make_node("Relu", ["H"], ["R"], name="relu1"),
+        ox.make_node("Gemm", ["R", "W2", "B2"], ["Y"], name="fc2"),
+    ]
+    g = ox.make_graph(nodes, "mlp_784_256_10", [ox.value_info("X", [batch, MLP_IN])],
+                      [ox.value_info("Y", [batch, MLP_OUT])],
+                      [_q88_initializer("W1", w1), _q88_initializer("B1", b1),
+                       _q88_initializer("W2", w2), _q88_initializer("B2", b2)])
+    return ox.make_model(g, opset=13)
+
+
+def mlp_input(batch: int = MLP_BATCH) -> np.ndarray:
+    return uniform_q88(rng(1, 0), (batch, MLP_IN), -1.0, 1.0)
+
+
+# config 5: MobileNetV2-like graph without grouped convolutions.
+# The MobileNetV2 stage schedule (channels, repeats, first stride) with expansion
+# 1: every block is Conv3x3(c_in -> c_in, stride) + Clip(0,6), then a linear
+# Conv1x1(c_in -> c_out); a block with stride 1 and c_in == c_out adds its input
+# back.  Stem Conv3x3 s2 3->32 + Clip; head Conv1x1 -> 1280 + Clip,
+# GlobalAveragePool, Reshape, Gemm 1280 -> 1000.
+MOBILENET_STAGES = ((16, 1, 1), (24, 2, 2), (32, 3, 2), (64, 4, 2), (96, 3, 1), (160, 3, 2),
+                    (320, 1, 1))
+MOBILENET_BATCH, MOBILENET_HW, MOBILENET_HEAD, MOBILENET_CLASSES = 16, 224, 1280, 1000
+
+
+def mobilenet_model(batch: int = MOBILENET_BATCH, hw: int = MOBILENET_HW,
+                    stages=MOBILENET_STAGES, head: int = MOBILENET_HEAD,
+                    classes: int = MOBILENET_CLASSES):
+    """The MobileNetV2-like graph; weights and biases N(0, 0.05), AP_TRN+AP_SAT."""
+    from .scheduler import onnx_io as ox
+    nodes, inits = [], []
+    counter = [0]
+
+    def conv(x, cin, cout, k, stride, clip):
+        i = counter[0]
+        counter[0] += 1
+        w = normal_q88(rng(5, i, 0), (cout, cin, k, k), 0.05)
+        b = normal_q88(rng(5, i, 1), (cout,), 0.05)
+        inits.extend([_q88_initializer(f"conv{i}_w", w), _q88_initializer(f"conv{i}_b", b)])
+        y = f"conv{i}_y"
+        p = k // 2
+        nodes.append(ox.make_node("Conv", [x, f"conv{i}_w", f"conv{i}_b"], [y], name=f"conv{i}",
+                                  kernel_shape=[k, k], strides=[stride, stride],
+                                  pads=[p, p, p, p]))
+        if clip:
+            nodes.append(ox.make_node("Clip", [y, "clip_lo", "clip_hi"], [f"{y}_r6"],
+                                      name=f"clip{i}"))
+            y = f"{y}_r6"
+        return y
+
+    inits.append(ox.from_array(np.array(0.0, np.float32), "clip_lo"))
+    inits.append(ox.from_array(np.array(6.0, np.float32), "clip_hi"))
+    x = conv("X", 3, 32, 3, 2, True)
+    cin = 32
+    for cout, reps, s in stages:
+        for r in range(reps):
+            stride = s if r == 0 else 1
+            h = conv(x, cin, cin, 3, stride, True)
+            y = conv(h, cin, cout, 1, 1, False)
+            if stride == 1 and cin == cout:
+                nodes.append(ox.make_node("Add", [y, x], [f"{y}_res"], name=f"res_{y}"))
+                y = f"{y}_res"
+            x, cin = y, cout
+    x = conv(x, cin, head, 1, 1, True)
+    nodes.append(ox.make_node("GlobalAveragePool", [x], ["gap"], name="gap"))
+    inits.append(ox.from_array(np.array([batch, head], np.int64), "flat_shape"))
+    nodes.append(ox.make_node("Reshape", ["gap", "flat_shape"], ["flat"], name="flatten"))
+    fw = normal_q88(rng(5, 1000, 0), (head, classes), 0.05)
+    fb = normal_q88(rng(5, 1000, 1), (classes,), 0.05)
+    inits.extend([_q88_initializer("fc_w", fw), _q88_initializer("fc_b", fb)])
+    nodes.append(ox.make_node("Gemm", ["flat", "fc_w", "fc_b"], ["Y"], name="fc"))
+    g = ox.make_graph(nodes, "mobilenetv2_like", [ox.value_info("X", [batch, 3, hw, hw])],
+                      [ox.value_info("Y", [batch, classes])], inits)
+    return ox.make_model(g, opset=13)
+
+
+def mobilenet_input(batch: int = MOBILENET_BATCH, hw: int = MOBILENET_HW) -> np.ndarray:
+    return uniform_q88(rng(5, 9999), (batch, 3, hw, hw), -1.0, 1.0)

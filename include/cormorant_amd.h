@@ -128,7 +128,10 @@ void cm_buf_init_view(cm_buf_t *view, cm_buf_t *base, uint32_t offset_elems,
 int cm_buf_sync_to_device(cm_buf_t *buf);         /* host -> device, stream-ordered */
 int cm_buf_sync_from_device(cm_buf_t *buf);       /* device -> host, then waits */
 
-/* Buffer-level helpers with the generated run_* signatures (_source.py:198-421). */
+/* Buffer-level helpers with the generated run_* signatures (_source.py:198-421).
+ * They enqueue on the stream set by cm_set_stream.  Unlike the reference's void
+ * helpers they check every element the call touches against each buffer's
+ * count and return CM_ERR_RANGE (nothing launched) when a buffer is too small. */
 int cm_run_op(cm_buf_t *a, cm_buf_t *b, cm_buf_t *c, uint32_t size, uint32_t op,
               uint32_t outer, uint32_t a_inc, uint32_t b_inc);
 int cm_run_matmul(cm_buf_t *a, cm_buf_t *b, cm_buf_t *c, uint32_t n, uint32_t k, uint32_t m,
