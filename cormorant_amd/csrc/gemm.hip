@@ -49,7 +49,19 @@ struct GemmArgs {
     // implicit GEMM: column = n*P + p, k = (c*kh + khi)*kw + kwi
     uint32_t C, H, W, OW, P, kh, kw, sh, sw, dh, dw, pt, pl;
     uint64_t x_img, y_img;
+    uint32_t x_bytes;            // table mode: size of the whole input tensor, < 2^31
 };
+
+// Raw buffer resource word 3 for gfx950 (32-bit data, no swizzle): loads past
+// num_records return 0.  kOob is an offset past every resource used here.
+constexpr int kBufferWord3 = 0x00020000;
+constexpr uint32_t kOob = 0x80000000u;
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const int16_t* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<int16_t*>(base), (short)0, (int)bytes,
+                                             kBufferWord3);
+}
 
 // Limb bytes of four int16 values held in two words w0 = (v0 | v1 << 16),
 // w1 = (v2 | v3 << 16): one v_perm_b32 gathers the high bytes (v >> 8) and one
@@ -80,37 +92,71 @@ struct Smem {
 };
 
 // ---------------------------------------------------------------- A tile --
-// Thread t owns row t/2 and k values [32*(t&1), +32) of the 64-k slice.
+// Thread t owns row t/2 and k values [32*(t&1), +32) of the 64-k slice.  The
+// global loads only fill registers (16 words for 16-byte loads, 32 raw values
+// otherwise); packing and the limb split happen in store(), after the MFMA
+// phase, so every load of a tile is in flight at once.  Loads are
+// unconditional: out-of-range elements read a valid address and are zeroed.
 struct ATile {
-    uint32_t w[16];
+    uint32_t w[16];     // vector path: two int16 per word
+    uint32_t raw[32];   // element path: one int16 per register
+
     __device__ __forceinline__ void load(const GemmArgs& g, const int16_t* abase, uint32_t row0,
                                          uint32_t k0) {
         const uint32_t r = row0 + (threadIdx.x >> 1);
         const uint32_t ks = k0 + (threadIdx.x & 1) * 32;
+        const bool rok = r < g.rows;
+        const int16_t* p = abase + (uint64_t)(rok ? r : 0u) * g.lda;
         if (g.a_vec) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-                v4i v = {0, 0, 0, 0};
-                if (r < g.rows && ks + q * 8 < g.k)
-                    v = *reinterpret_cast<const v4i*>(abase + (uint64_t)r * g.lda + ks + q * 8);
+                const bool ok = rok && ks + q * 8 < g.k;
+                v4i v = *reinterpret_cast<const v4i*>(p + (ok ? ks + q * 8 : 0u));
+                const v4i z = {0, 0, 0, 0};
+                v = ok ? v : z;
                 w[4 * q + 0] = v[0]; w[4 * q + 1] = v[1]; w[4 * q + 2] = v[2]; w[4 * q + 3] = v[3];
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                int16_t v0 = 0, v1 = 0;
-                if (r < g.rows) {
-                    const int16_t* p = abase + (uint64_t)r * g.lda;
-                    if (ks + 2 * j < g.k) v0 = p[ks + 2 * j];
-                    if (ks + 2 * j + 1 < g.k) v1 = p[ks + 2 * j + 1];
-                }
-                w[j] = pack2(v0, v1);
+            for (int j = 0; j < 32; ++j) {
+                const bool ok = rok && ks + j < g.k;
+                raw[j] = ok ? (uint32_t)(uint16_t)p[ok ? ks + j : 0u] : 0u;
+            }
+        }
+    }
+    // Same tile through a buffer resource based at the block's first row (the
+    // tile spans fewer than 2^31 bytes): an element outside the matrix gets
+    // offset kOob and reads as 0, so no load needs a condition or a select.
+    template <bool VEC>
+    __device__ __forceinline__ void load_buf(const GemmArgs& g, __amdgpu_buffer_rsrc_t ra,
+                                             uint32_t row0, uint32_t k0) {
+        const uint32_t rel = threadIdx.x >> 1;
+        const uint32_t ks = k0 + (threadIdx.x & 1) * 32;
+        const bool rok = row0 + rel < g.rows;
+        const uint32_t rbyte = rel * (uint32_t)g.lda * 2u;
+        if constexpr (VEC) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const bool ok = rok && ks + q * 8 < g.k;
+                const v4u v = __builtin_amdgcn_raw_buffer_load_b128(
+                    ra, ok ? rbyte + (ks + q * 8) * 2u : kOob, 0, 0);
+                w[4 * q + 0] = v[0]; w[4 * q + 1] = v[1]; w[4 * q + 2] = v[2]; w[4 * q + 3] = v[3];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 32; ++j) {
+                const bool ok = rok && ks + j < g.k;
+                raw[j] = __builtin_amdgcn_raw_buffer_load_b16(ra, ok ? rbyte + (ks + j) * 2u : kOob, 0, 0);
             }
         }
     }
     // Stores the limbs; hs / ls accumulate the sums of the high and low limbs
     // of this thread's values (sum a = 256*hs + ls + 128*count).
-    __device__ __forceinline__ void store(Smem& s, int32_t& hs, int32_t& ls) const {
+    __device__ __forceinline__ void store(bool vec, Smem& s, int32_t& hs, int32_t& ls) {
+        if (!vec) {
+#pragma unroll
+            for (int j = 0; j < 16; ++j) w[j] = __builtin_amdgcn_perm(raw[2 * j + 1], raw[2 * j], 0x05040100u);
+        }
         const uint32_t off = (threadIdx.x >> 1) * kStride + (threadIdx.x & 1) * 32;
         uint32_t hi[8], lo[8];
 #pragma unroll
@@ -134,7 +180,44 @@ struct ATile {
 // wave differ mostly in k, so the transposing 4-byte LDS stores of one column
 // land in 16 different banks (4-way at worst) instead of one.
 struct DenseBTile {
-    uint32_t w[4][4];   // [k row][word of 2 columns]
+    uint32_t w[4][4];     // [k row][word of 2 columns]
+    uint32_t raw[4][8];   // buffer element path: [k row][column], one int16 each
+
+    // Buffer resource based at (k0, col0) for each k step (64 rows span fewer
+    // than 2^31 bytes); elements outside the matrix read as 0 through kOob.
+    template <bool VEC>
+    __device__ __forceinline__ void load_buf(const GemmArgs& g, __amdgpu_buffer_rsrc_t rb,
+                                             uint32_t col0, uint32_t k0) {
+        const uint32_t cr = (threadIdx.x >> 4) * 8;
+        const uint32_t kr = (threadIdx.x & 15) * 4;
+        if constexpr (VEC) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bool ok = k0 + kr + i < g.k && col0 + cr < g.cols;
+                const v4u v = __builtin_amdgcn_raw_buffer_load_b128(
+                    rb, ok ? ((kr + i) * (uint32_t)g.ldb + cr) * 2u : kOob, 0, 0);
+                w[i][0] = v[0]; w[i][1] = v[1]; w[i][2] = v[2]; w[i][3] = v[3];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bool kok = k0 + kr + i < g.k;
+#pragma unroll
+                for (int q = 0; q < 8; ++q) {
+                    const bool ok = kok && col0 + cr + q < g.cols;
+                    raw[i][q] = __builtin_amdgcn_raw_buffer_load_b16(
+                        rb, ok ? ((kr + i) * (uint32_t)g.ldb + cr + q) * 2u : kOob, 0, 0);
+                }
+            }
+        }
+    }
+    __device__ __forceinline__ void pack_raw() {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                w[i][q] = __builtin_amdgcn_perm(raw[i][2 * q + 1], raw[i][2 * q], 0x05040100u);
+    }
 
     __device__ __forceinline__ void load(const GemmArgs& g, const int16_t* bbase, uint32_t col0,
                                          uint32_t k0) {
@@ -143,22 +226,23 @@ struct DenseBTile {
         if (g.b_vec) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                v4i v = {0, 0, 0, 0};
-                if (kb + i < g.k && cb < g.cols)
-                    v = *reinterpret_cast<const v4i*>(bbase + (uint64_t)(kb + i) * g.ldb + cb);
+                const bool ok = kb + i < g.k && cb < g.cols;
+                v4i v = *reinterpret_cast<const v4i*>(bbase + (ok ? (uint64_t)(kb + i) * g.ldb + cb : 0u));
+                const v4i z = {0, 0, 0, 0};
+                v = ok ? v : z;
                 w[i][0] = v[0]; w[i][1] = v[1]; w[i][2] = v[2]; w[i][3] = v[3];
             }
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const bool kok = kb + i < g.k;
-                const int16_t* p = bbase + (uint64_t)(kb + i) * g.ldb;
+                const int16_t* p = bbase + (kok ? (uint64_t)(kb + i) * g.ldb : 0u);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    int16_t v0 = 0, v1 = 0;
-                    if (kok && cb + 2 * q < g.cols) v0 = p[cb + 2 * q];
-                    if (kok && cb + 2 * q + 1 < g.cols) v1 = p[cb + 2 * q + 1];
-                    w[i][q] = pack2(v0, v1);
+                    const uint32_t c = cb + 2 * q;
+                    const bool ok0 = kok && c < g.cols, ok1 = kok && c + 1 < g.cols;
+                    int16_t v0 = p[ok0 ? c : 0u], v1 = p[ok1 ? c + 1 : 0u];
+                    w[i][q] = pack2(ok0 ? v0 : (int16_t)0, ok1 ? v1 : (int16_t)0);
                 }
             }
         }
@@ -202,12 +286,15 @@ __device__ __forceinline__ void publish_dense(Smem& s, const int32_t (&hs)[8], c
 }
 
 // ------------------------------------------------------- im2col B tile --
-// Thread t owns column (pixel) t&127 and k values [32*(t>>7), +32).
+// Thread t owns column (pixel) t&127 and k values [32*(t>>7), +32): the lanes
+// of one load instruction read 64 neighbouring output pixels at the same k,
+// which coalesce.  The 32 values stay raw until store().
 struct ConvBTile {
-    uint32_t w[16];
+    uint32_t raw[32];
     const int16_t* xb;   // image base of this thread's column
     int32_t ih0, iw0;    // window origin of this thread's output pixel
     int32_t pbase;       // ih0 * W + iw0 (may be negative; only valid taps are read)
+    int32_t pbyte;       // byte offset of the window origin from the tensor start
     bool col_ok;
 
     __device__ __forceinline__ void init(const GemmArgs& g, uint32_t col0) {
@@ -219,28 +306,30 @@ struct ConvBTile {
         ih0 = (int32_t)(oh * g.sh) - (int32_t)g.pt;
         iw0 = (int32_t)(ow * g.sw) - (int32_t)g.pl;
         pbase = ih0 * (int32_t)g.W + iw0;
+        pbyte = (int32_t)(2 * ((int64_t)n * (int64_t)g.x_img + pbase));
         xb = g.b + (uint64_t)n * g.x_img;
     }
-    // Gather with the per-block k table: tab[k] = {c*H*W + dy*W + dx, dy << 16 | dx}
-    // with dy = khi*dh, dx = kwi*dw.  One broadcast LDS read per k, no divisions.
-    __device__ __forceinline__ void load_tab(const GemmArgs& g, uint32_t k0, const int2* tab) {
-        const uint32_t ks = k0 + (threadIdx.x >> 7) * 32;
+    // Gather through the per-block k table tab[k] = {2*(c*H*W + dy*W + dx), dy << 16 | dx}
+    // (dy = khi*dh, dx = kwi*dw) with buffer loads over the whole input tensor
+    // (fewer than 2^31 bytes): an invalid tap gets offset 0x80000000, past the
+    // buffer's size, and the hardware returns 0 for it.
+    __device__ __forceinline__ void load_tab(const GemmArgs& g, uint32_t k0, const int2* tab,
+                                             __amdgpu_buffer_rsrc_t rsrc) {
+        const uint32_t ks = __builtin_amdgcn_readfirstlane(k0 + (threadIdx.x >> 7) * 32);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            int16_t v[2];
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                v[e] = 0;
-                const uint32_t k = ks + 2 * j + e;
-                if (col_ok && k < g.k) {
-                    const int2 t = tab[k];
-                    const int32_t ih = ih0 + (t.y >> 16), iw = iw0 + (t.y & 0xFFFF);
-                    if ((uint32_t)ih < g.H && (uint32_t)iw < g.W) v[e] = xb[pbase + t.x];
-                }
-            }
-            w[j] = pack2(v[0], v[1]);
+        for (int j = 0; j < 32; ++j) {
+            // k < kTabMax always (the padded k range of a K <= kTabMax problem);
+            // entries past g.k are never used.
+            const uint32_t k = ks + j;
+            const int2 t = tab[k];
+            const int32_t ih = ih0 + (t.y >> 16), iw = iw0 + (t.y & 0xFFFF);
+            const bool ok = col_ok && k < g.k && (uint32_t)ih < g.H && (uint32_t)iw < g.W;
+            const uint32_t off = ok ? (uint32_t)(pbyte + t.x) : 0x80000000u;
+            raw[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, 0);
         }
     }
+    // Gather for any size: k decomposed incrementally, global loads of a valid
+    // address (element 0 of the image for invalid taps), zeroed afterwards.
     __device__ __forceinline__ void load(const GemmArgs& g, uint32_t k0) {
         const uint32_t ks = k0 + (threadIdx.x >> 7) * 32;
         const uint32_t kk = g.kh * g.kw;
@@ -250,22 +339,17 @@ struct ConvBTile {
         uint32_t kwi = r - khi * g.kw;
         const uint32_t hw = g.H * g.W;
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-            int16_t v[2];
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                v[e] = 0;
-                const int32_t ih = ih0 + (int32_t)(khi * g.dh);
-                const int32_t iw = iw0 + (int32_t)(kwi * g.dw);
-                if (col_ok && ks + 2 * j + e < g.k && ih >= 0 && ih < (int32_t)g.H && iw >= 0 &&
-                    iw < (int32_t)g.W)
-                    v[e] = xb[c * hw + (uint32_t)ih * g.W + (uint32_t)iw];
-                if (++kwi == g.kw) {
-                    kwi = 0;
-                    if (++khi == g.kh) { khi = 0; ++c; }
-                }
+        for (int j = 0; j < 32; ++j) {
+            const int32_t ih = ih0 + (int32_t)(khi * g.dh);
+            const int32_t iw = iw0 + (int32_t)(kwi * g.dw);
+            const bool ok = col_ok && ks + j < g.k && ih >= 0 && ih < (int32_t)g.H && iw >= 0 &&
+                            iw < (int32_t)g.W;
+            const int16_t x = xb[ok ? (uint64_t)c * hw + (uint32_t)ih * g.W + (uint32_t)iw : 0u];
+            raw[j] = ok ? (uint32_t)(uint16_t)x : 0u;
+            if (++kwi == g.kw) {
+                kwi = 0;
+                if (++khi == g.kh) { khi = 0; ++c; }
             }
-            w[j] = pack2(v[0], v[1]);
         }
     }
     __device__ __forceinline__ void store(Smem& s, int32_t& hs, int32_t& ls) const {
@@ -273,8 +357,10 @@ struct ConvBTile {
         uint32_t hi[8], lo[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            hi[j] = hi4(w[2 * j], w[2 * j + 1]);
-            lo[j] = lo4(w[2 * j], w[2 * j + 1]);
+            const uint32_t w0 = __builtin_amdgcn_perm(raw[4 * j + 1], raw[4 * j], 0x05040100u);
+            const uint32_t w1 = __builtin_amdgcn_perm(raw[4 * j + 3], raw[4 * j + 2], 0x05040100u);
+            hi[j] = hi4(w0, w1);
+            lo[j] = lo4(w0, w1);
             hs = bsum(hi[j], hs);
             ls = bsum(lo[j], ls);
         }
@@ -292,7 +378,11 @@ struct ConvBTile {
 enum { B_DENSE = 0, B_CONV_TAB = 1, B_CONV_INC = 2 };
 constexpr uint32_t kTabMax = 2048;
 
-template <int MODE, bool HAS_BIAS, bool FOLD>
+// AV / BV: 0 = 16-byte loads chosen at run time (g.a_vec / g.b_vec, global
+// loads), 1 = 16-byte buffer loads, 2 = element buffer loads.  Fixing the path
+// at compile time keeps the staged registers identical on every path, so no
+// copy (and no wait for outstanding loads) is needed where paths would merge.
+template <int MODE, bool HAS_BIAS, bool FOLD, bool BUF, int AV, int BV>
 __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     constexpr bool CONV = MODE != B_DENSE;
     __shared__ __align__(16) Smem s;
@@ -314,7 +404,7 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
             const uint32_t c = k / kk, r = k - (k / kk) * kk;
             const uint32_t khi = r / g.kw, kwi = r - (r / g.kw) * g.kw;
             const uint32_t dy = khi * g.dh, dx = kwi * g.dw;
-            ktab[k] = int2{(int)(c * hw + dy * g.W + dx), (int)((dy << 16) | dx)};
+            ktab[k] = int2{(int)(2 * (c * hw + dy * g.W + dx)), (int)((dy << 16) | dx)};
         }
         tab = ktab;
     }
@@ -331,6 +421,10 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     int32_t dhs[8] = {0, 0, 0, 0, 0, 0, 0, 0}, dls[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     int32_t chs = 0, cls = 0;
     if constexpr (CONV) bt0.init(g, col0);
+    const __amdgpu_buffer_rsrc_t xrsrc = make_rsrc(g.b, g.x_bytes);   // table mode only
+    const uint32_t arows = g.rows - row0 < (uint32_t)BM ? g.rows - row0 : (uint32_t)BM;
+    const __amdgpu_buffer_rsrc_t arsrc =
+        make_rsrc(abase + (uint64_t)row0 * g.lda, arows * (uint32_t)g.lda * 2u);   // BUF only
 
     v4i hh[4][4], mid[4][4], ll[4][4], tot[4][4];
 #pragma unroll
@@ -342,15 +436,31 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
         }
 
     auto load_tile = [&](ATile& at, BTile& bt, uint32_t k0) {
-        at.load(g, abase, row0, k0);
-        if constexpr (MODE == B_CONV_TAB) bt.load_tab(g, k0, tab);
-        else if constexpr (MODE == B_CONV_INC) bt.load(g, k0);
-        else bt.load(g, bbase, col0, k0);
+        if constexpr (BUF) at.template load_buf<AV == 1>(g, arsrc, row0, k0);
+        else at.load(g, abase, row0, k0);
+        if constexpr (MODE == B_CONV_TAB) {
+            bt.load_tab(g, k0, tab, xrsrc);
+        } else if constexpr (MODE == B_CONV_INC) {
+            bt.load(g, k0);
+        } else if constexpr (BUF) {
+            const uint32_t kr = g.k - k0 < (uint32_t)BK ? g.k - k0 : (uint32_t)BK;
+            const uint32_t cr = g.cols - col0 < (uint32_t)BN ? g.cols - col0 : (uint32_t)BN;
+            bt.template load_buf<BV == 1>(g, make_rsrc(bbase + (uint64_t)k0 * g.ldb + col0,
+                                                       ((kr - 1) * (uint32_t)g.ldb + cr) * 2u),
+                                          col0, k0);
+        } else {
+            bt.load(g, bbase, col0, k0);
+        }
     };
-    auto stage_tile = [&](const ATile& at, const BTile& bt) {
+    auto stage_tile = [&](ATile& at, BTile& bt) {
         __syncthreads();                 // previous tile fully consumed
-        at.store(s, row_hs, row_ls);
-        if constexpr (CONV) bt.store(s, chs, cls); else bt.store(s, dhs, dls);
+        at.store(AV == 0 ? g.a_vec != 0 : AV == 1, s, row_hs, row_ls);
+        if constexpr (CONV) {
+            bt.store(s, chs, cls);
+        } else {
+            if constexpr (BUF && BV == 2) bt.pack_raw();
+            bt.store(s, dhs, dls);
+        }
         __syncthreads();
     };
     auto mfma_step = [&](uint32_t it) {
@@ -463,10 +573,32 @@ int launch_gemm(GemmArgs& g, uint32_t zdim, hipStream_t s, const char* name) {
         return cm_set_error(CM_ERR_RANGE, "%s: grid too large", name);
     const bool fold = g.k > (uint32_t)(kFoldIters * BK);
     const bool bias = g.bias != nullptr;
-#define CM_GEMM_LAUNCH(B, F) \
-    hipLaunchKernelGGL((q88_gemm<MODE, B, F>), grid, dim3(kThreads), 0, s, g)
-    if (bias) { if (fold) CM_GEMM_LAUNCH(true, true); else CM_GEMM_LAUNCH(true, false); }
-    else { if (fold) CM_GEMM_LAUNCH(false, true); else CM_GEMM_LAUNCH(false, false); }
+    // Buffer loads need each per-block resource below 2^31 bytes: 128 rows of A
+    // and 64 k rows of dense B.  The table-gather conv always satisfies it.
+    const bool buf = MODE == B_CONV_TAB ||
+                     (MODE == B_DENSE && !fold && g.lda < (1ull << 23) && g.ldb < (1ull << 24) - 128);
+#define CM_GEMM_LAUNCH(B, F, U, AV, BV) \
+    hipLaunchKernelGGL((q88_gemm<MODE, B, F, U, AV, BV>), grid, dim3(kThreads), 0, s, g)
+#define CM_GEMM_BIAS(F, U, AV, BV) \
+    do { if (bias) CM_GEMM_LAUNCH(true, F, U, AV, BV); else CM_GEMM_LAUNCH(false, F, U, AV, BV); } while (0)
+    if constexpr (MODE == B_CONV_TAB) {
+        if (g.a_vec) CM_GEMM_BIAS(false, true, 1, 0); else CM_GEMM_BIAS(false, true, 2, 0);
+    } else if constexpr (MODE == B_DENSE) {
+        if (buf) {
+            if (g.a_vec) {
+                if (g.b_vec) CM_GEMM_BIAS(false, true, 1, 1); else CM_GEMM_BIAS(false, true, 1, 2);
+            } else {
+                if (g.b_vec) CM_GEMM_BIAS(false, true, 2, 1); else CM_GEMM_BIAS(false, true, 2, 2);
+            }
+        } else if (fold) {
+            CM_GEMM_BIAS(true, false, 0, 0);
+        } else {
+            CM_GEMM_BIAS(false, false, 0, 0);
+        }
+    } else {
+        if (fold) CM_GEMM_BIAS(true, false, 0, 0); else CM_GEMM_BIAS(false, false, 0, 0);
+    }
+#undef CM_GEMM_BIAS
 #undef CM_GEMM_LAUNCH
     return cm_check_launch(name);
 }
@@ -528,9 +660,11 @@ int cm_conv_gemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias,
     g.kh = kh; g.kw = kw; g.sh = sh; g.sw = sw; g.dh = dh; g.dw = dw; g.pt = pad_top; g.pl = pad_left;
     g.x_img = x_img;
     g.y_img = (uint64_t)out_ch * P;
-    // the k table holds offsets < 2^31 and dy, dx < 2^16
+    // the k table holds byte offsets < 2^31 and dy, dx < 2^16
+    const uint64_t x_bytes = 2 * x_img * batch;
+    g.x_bytes = (uint32_t)(x_bytes < 0x80000000ull ? x_bytes : 0);
     const bool table = K <= kTabMax && (uint64_t)(kh - 1) * dh < 65536u &&
-                       (uint64_t)(kw - 1) * dw < 65536u;
+                       (uint64_t)(kw - 1) * dw < 65536u && x_bytes < 0x80000000ull;
     if (table) return launch_gemm<B_CONV_TAB>(g, 1, s, "conv_gemm");
     return launch_gemm<B_CONV_INC>(g, 1, s, "conv_gemm");
 }
