@@ -25,7 +25,7 @@ namespace {
 typedef short v8s __attribute__((ext_vector_type(8)));
 
 constexpr int kThreads = 256;
-constexpr uint32_t kLdsBytes = 32768;
+constexpr uint64_t kPoolBlocks = 2048;   // 256 CUs x 8 resident blocks of 256 threads
 
 struct PoolGeom {
     uint32_t in_h, in_w, out_h, out_w, ph, pw, sh, sw, pt, pl, dh, dw;
@@ -39,6 +39,9 @@ enum Kind { K_MAX = 0, K_AVG = 1, K_LP1 = 2, K_LP2 = 3 };
 // initialised like PoolingKernel.cpp:185-190 (kAccMin = raw -2^31 for MAX).
 template <int KIND>
 struct Acc {
+    // A padded tap: kDataMin for MAX (PoolingKernel pads with it; the result
+    // equals skipping the tap, since the initial accumulator is lower), 0 for sums.
+    static constexpr int32_t kPad = KIND == K_MAX ? -32768 : 0;
     uint32_t v;
     __device__ __forceinline__ Acc() : v(KIND == K_MAX ? 0x80000000u : 0u) {}
     __device__ __forceinline__ void add(int32_t x) {
@@ -106,95 +109,166 @@ __global__ __launch_bounds__(kThreads) void pool_global(const int16_t* __restric
 }
 
 // ------------------------------------------------------------------ band --
-// Block = (plane, band of `band_h` output rows).  Stages the input rows the
-// band needs (full width) in LDS, then computes the band.  Threads are laid
-// out as (row, column) with `tw` columns (a power of two covering out_w, at
-// most 64), so no per-output division is needed.  KH/KW > 0 fix the window
-// at compile time (dilation 1) so the tap loops unroll; 0 = runtime window.
-// Padded taps are skipped: they add 0 to sums, and for MAX the initial
-// accumulator (kAccMin) already gives -32768 when no tap is valid, as padding
-// with kDataMin does.
+// Work item = (plane, band of `band_h` output rows).  The block stages the
+// band's whole window footprint in LDS *including the padding*: rows
+// [ih_lo, ih_hi] and columns [-pl, in_w + pr), padded positions holding the
+// pad value (kDataMin for MAX, 0 for sums; PoolingKernel.cpp:168-172), so
+// every window reads LDS without a bounds check.  LDS element (r, c) holds
+// input (ih_lo + r, c - cofs); cofs >= pl is a multiple of 8 so that the
+// 16-byte body of each staged input row is aligned, and the row pitch is a
+// multiple of 8 elements.
+//
+// Blocks are persistent and software-pipelined: the 16-byte loads of the
+// next item are issued into registers before the current item is reduced,
+// so HBM traffic continues while windows are computed.  Each thread owns a
+// fixed (row, column) of a pass of `rows_pp` output rows, computed once.
+//
+// `vec` (in_w % 8 == 0, 16-byte aligned planes) selects 16-byte row copies;
+// otherwise rows are copied element by element.  KH/KW > 0 fix the window at
+// compile time (dilation 1) so the taps unroll with immediate LDS offsets.
+constexpr int kPre = 4;
+constexpr uint32_t kBandBytes = kPre * kThreads * 16;
+constexpr uint32_t kInvTab = 64;   // AVG: 1/d for every denominator d <= 63, per block
+
+struct BandGeom {
+    uint32_t band_h, n_bands, n_items;
+    uint32_t pitch, cofs, lds_rows;    // LDS tile: lds_rows x pitch elements
+    uint32_t rows_pp, vec;             // output rows per pass, 16-byte row copies
+};
+
+struct BandItem {
+    uint64_t plane;
+    uint32_t oh0, oh1;
+    int32_t ih_lo;        // input row of LDS row 0 (may be negative: top padding)
+    uint32_t r0, r1;      // LDS rows [r0, r1) hold real input rows
+};
+
+__device__ __forceinline__ BandItem band_item(const PoolGeom& g, const BandGeom& b, uint32_t item) {
+    BandItem it;
+    it.plane = item / b.n_bands;
+    const uint32_t band = item - (uint32_t)(it.plane * b.n_bands);
+    it.oh0 = band * b.band_h;
+    it.oh1 = min(it.oh0 + b.band_h, g.out_h);
+    it.ih_lo = (int32_t)(it.oh0 * g.sh) - (int32_t)g.pt;
+    const int32_t last = (int32_t)((it.oh1 - 1) * g.sh) - (int32_t)g.pt + (int32_t)((g.ph - 1) * g.dh);
+    const int32_t lo = it.ih_lo < 0 ? 0 : it.ih_lo;
+    const int32_t hi = last + 1 > (int32_t)g.in_h ? (int32_t)g.in_h : last + 1;
+    it.r0 = (uint32_t)(lo - it.ih_lo);
+    it.r1 = hi > lo ? (uint32_t)(hi - it.ih_lo) : it.r0;
+    return it;
+}
+
 template <int KIND, int KH, int KW>
 __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict__ x,
                                                       int16_t* __restrict__ y, PoolGeom g,
-                                                      uint32_t band_h, uint32_t n_bands,
-                                                      float inv_full, uint32_t tw_log2) {
+                                                      BandGeom b, float inv_full) {
     extern __shared__ __align__(16) int16_t lds[];
-    const uint64_t plane = blockIdx.x / n_bands;
-    const uint32_t band = blockIdx.x - (uint32_t)(plane * n_bands);
-    const uint32_t oh0 = band * band_h;
-    const uint32_t oh1 = min(oh0 + band_h, g.out_h);
-    const int32_t in_h = (int32_t)g.in_h, in_w = (int32_t)g.in_w;
-
-    // input rows touched by output rows [oh0, oh1)
-    const int32_t lo = (int32_t)(oh0 * g.sh) - (int32_t)g.pt;
-    const int32_t hi = (int32_t)((oh1 - 1) * g.sh) - (int32_t)g.pt + (int32_t)((g.ph - 1) * g.dh) + 1;
-    const int32_t r_lo = lo < 0 ? 0 : lo;
-    const int32_t r_hi = hi > in_h ? in_h : hi;
-    const int16_t* xp = x + plane * (uint64_t)g.in_h * g.in_w;
-    const int16_t* src = xp + (int64_t)r_lo * in_w;
-    const uint32_t shift = (uint32_t)(((uintptr_t)src >> 1) & 7u);
-
-    if (r_hi > r_lo) {
-        // Copy elements [0, n) of src to lds[shift + i]; the 16-byte body of
-        // the copy is aligned identically in global memory and in LDS.  Each
-        // thread issues the loads of a round before it stores any of them.
-        const uint32_t n = (uint32_t)(r_hi - r_lo) * (uint32_t)in_w;
-        const uint32_t head = min((8u - shift) & 7u, n);
-        const uint32_t nv = (n - head) / 8;
-        int16_t* dst = lds + shift;
-        if (threadIdx.x < head) dst[threadIdx.x] = src[threadIdx.x];
-        const v8s* sv = reinterpret_cast<const v8s*>(src + head);
-        v8s* dv = reinterpret_cast<v8s*>(dst + head);
-        constexpr int kRound = 4;
-        for (uint32_t base = 0; base < nv; base += kThreads * kRound) {
-            v8s t[kRound];
-#pragma unroll
-            for (int u = 0; u < kRound; ++u) {
-                const uint32_t v = base + u * kThreads + threadIdx.x;
-                if (v < nv) t[u] = __builtin_nontemporal_load(sv + v);
-            }
-#pragma unroll
-            for (int u = 0; u < kRound; ++u) {
-                const uint32_t v = base + u * kThreads + threadIdx.x;
-                if (v < nv) dv[v] = t[u];
-            }
-        }
-        for (uint32_t i = head + nv * 8 + threadIdx.x; i < n; i += kThreads) dst[i] = src[i];
-    }
-    __syncthreads();
-
-    // staged element (ih, iw), ih in [r_lo, r_hi): lds[shift + (ih - r_lo) * in_w + iw]
-    const int16_t* rows = lds + shift;
-    int16_t* yp = y + plane * (uint64_t)g.out_h * g.out_w;
+    __shared__ float inv_tab[kInvTab];
+    constexpr int16_t kPadV = KIND == K_MAX ? (int16_t)-32768 : (int16_t)0;
     const int32_t ph = KH > 0 ? KH : (int32_t)g.ph, pw = KW > 0 ? KW : (int32_t)g.pw;
     const int32_t dh = KH > 0 ? 1 : (int32_t)g.dh, dw = KW > 0 ? 1 : (int32_t)g.dw;
-    const uint32_t tw = 1u << tw_log2;
-    const uint32_t c0 = threadIdx.x & (tw - 1);
-    for (uint32_t oh = oh0 + (threadIdx.x >> tw_log2); oh < oh1; oh += kThreads >> tw_log2) {
-        const int32_t ih0 = (int32_t)(oh * g.sh) - (int32_t)g.pt;
-        for (uint32_t ow = c0; ow < g.out_w; ow += tw) {
-            const int32_t iw0 = (int32_t)(ow * g.sw) - (int32_t)g.pl;
-            Acc<KIND> a;
+    const bool avg_tab = KIND == K_AVG && !g.cip && (uint32_t)(ph * pw) < kInvTab;
+    if (KIND == K_AVG && threadIdx.x < kInvTab) inv_tab[threadIdx.x] = q88::inv_denom(threadIdx.x);
+
+    const uint32_t vpr = g.in_w / 8;                 // 16-byte vectors per input row (vec path)
+    const uint32_t my_r = threadIdx.x / g.out_w;     // this thread's row within a pass ...
+    const uint32_t my_c = threadIdx.x - my_r * g.out_w;   // ... and column (when out_w <= 256)
+    const uint32_t cstep = g.out_w > kThreads ? kThreads : g.out_w;
+
+    // fetch: the real input rows of an item into registers, vector v = u * kThreads + t
+    v8s pre[kPre];
+    auto fetch = [&](const BandItem& it) {
+        if (!b.vec) return;
+        const int16_t* xp = x + it.plane * (uint64_t)g.in_h * g.in_w;
+        const uint32_t nv = (it.r1 - it.r0) * vpr;
+        const v8s* sv = reinterpret_cast<const v8s*>(xp + (int64_t)(it.ih_lo + (int32_t)it.r0) * g.in_w);
 #pragma unroll
-            for (int32_t khi = 0; khi < (KH > 0 ? KH : ph); ++khi) {
-                const int32_t ih = ih0 + khi * dh;
-                if ((uint32_t)ih >= (uint32_t)in_h) continue;
-                const int16_t* row = rows + (ih - r_lo) * in_w;
-#pragma unroll
-                for (int32_t kwi = 0; kwi < (KW > 0 ? KW : pw); ++kwi) {
-                    const int32_t iw = iw0 + kwi * dw;
-                    if ((uint32_t)iw < (uint32_t)in_w) a.add(row[iw]);
+        for (int u = 0; u < kPre; ++u) {
+            const uint32_t v = u * kThreads + threadIdx.x;
+            if (v < nv) pre[u] = __builtin_nontemporal_load(sv + v);
+        }
+    };
+
+    uint32_t item = blockIdx.x;
+    if (item >= b.n_items) return;
+    BandItem cur = band_item(g, b, item);
+    fetch(cur);
+    for (;;) {
+        const uint32_t next = item + gridDim.x;
+        __syncthreads();                       // the previous item's LDS reads are done
+        {
+            // padding: whole LDS rows outside [r0, r1), then the left [0, cofs) and
+            // right [cofs + in_w, pitch) columns of the real rows
+            const uint32_t top = cur.r0 * b.pitch;
+            const uint32_t bottom = (b.lds_rows - cur.r1) * b.pitch;
+            for (uint32_t i = threadIdx.x; i < top; i += kThreads) lds[i] = kPadV;
+            for (uint32_t i = threadIdx.x; i < bottom; i += kThreads) lds[cur.r1 * b.pitch + i] = kPadV;
+            const uint32_t rcols = b.pitch - b.cofs - g.in_w;
+            const uint32_t strip = b.cofs + rcols;
+            if (strip) {
+                const uint32_t n = (cur.r1 - cur.r0) * strip;
+                for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
+                    const uint32_t r = i / strip, c = i - r * strip;
+                    lds[(cur.r0 + r) * b.pitch + (c < b.cofs ? c : c + g.in_w)] = kPadV;
                 }
             }
-            float inv = inv_full;
-            if constexpr (KIND == K_AVG) {
-                if (!g.cip)
-                    inv = q88::inv_denom((uint32_t)(valid_taps(ih0, ph, dh, in_h) *
-                                                    valid_taps(iw0, pw, dw, in_w)));
+            if (b.vec) {
+                const uint32_t nv = (cur.r1 - cur.r0) * vpr;
+#pragma unroll
+                for (int u = 0; u < kPre; ++u) {
+                    const uint32_t v = u * kThreads + threadIdx.x;
+                    if (v < nv) {
+                        const uint32_t r = v / vpr, q = v - r * vpr;
+                        *reinterpret_cast<v8s*>(lds + (cur.r0 + r) * b.pitch + b.cofs + q * 8) = pre[u];
+                    }
+                }
+            } else {
+                const int16_t* xp = x + cur.plane * (uint64_t)g.in_h * g.in_w;
+                const uint32_t n = (cur.r1 - cur.r0) * g.in_w;
+                for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
+                    const uint32_t r = i / g.in_w, c = i - r * g.in_w;
+                    lds[(cur.r0 + r) * b.pitch + b.cofs + c] =
+                        xp[(int64_t)(cur.ih_lo + (int32_t)(cur.r0 + r)) * g.in_w + c];
+                }
             }
-            yp[(uint64_t)oh * g.out_w + ow] = a.finish(inv);
         }
+        __syncthreads();
+        BandItem nb;
+        const bool more = next < b.n_items;
+        if (more) {
+            nb = band_item(g, b, next);
+            fetch(nb);                         // in flight while this item is reduced
+        }
+
+        int16_t* yp = y + cur.plane * (uint64_t)g.out_h * g.out_w;
+        for (uint32_t oh = cur.oh0 + my_r; my_r < b.rows_pp && oh < cur.oh1; oh += b.rows_pp) {
+            // LDS row of the window's first tap: oh*sh - pt - ih_lo
+            const int16_t* wrow = lds + (oh - cur.oh0) * g.sh * b.pitch + b.cofs - g.pl;
+            const int32_t ih0 = (int32_t)(oh * g.sh) - (int32_t)g.pt;
+            for (uint32_t ow = my_c; ow < g.out_w; ow += cstep) {
+                const int16_t* w0 = wrow + ow * g.sw;
+                Acc<KIND> a;
+#pragma unroll
+                for (int32_t khi = 0; khi < (KH > 0 ? KH : ph); ++khi) {
+                    const int16_t* rp = w0 + khi * dh * b.pitch;
+#pragma unroll
+                    for (int32_t kwi = 0; kwi < (KW > 0 ? KW : pw); ++kwi) a.add(rp[kwi * dw]);
+                }
+                float inv = inv_full;
+                if constexpr (KIND == K_AVG) {
+                    if (!g.cip) {
+                        const int32_t iw0 = (int32_t)(ow * g.sw) - (int32_t)g.pl;
+                        const uint32_t d = (uint32_t)(valid_taps(ih0, ph, dh, (int32_t)g.in_h) *
+                                                      valid_taps(iw0, pw, dw, (int32_t)g.in_w));
+                        inv = avg_tab ? inv_tab[d] : q88::inv_denom(d);
+                    }
+                }
+                yp[(uint64_t)oh * g.out_w + ow] = a.finish(inv);
+            }
+        }
+        if (!more) break;
+        item = next;
+        cur = nb;
     }
 }
 
@@ -278,36 +352,45 @@ int pool_launch(const int16_t* x, int16_t* y, uint64_t planes, const PoolGeom& g
                        g.pw < (1u << 10) && (uint64_t)g.out_w * g.sw < (1u << 30) &&
                        (uint64_t)g.out_h * g.sh < (1u << 30) &&
                        (uint64_t)g.in_h * g.in_w < (1u << 30);
+    // Padded LDS tile: columns [-pl, in_w + pr) at offset cofs = round_up(pl, 8),
+    // pitch a multiple of 8; rows = the window footprint of `band_h` output rows.
+    const uint64_t pr_need = (uint64_t)(g.out_w - 1) * g.sw + (uint64_t)(g.pw - 1) * g.dw + 1;
+    const uint64_t cofs = ((uint64_t)g.pl + 7) / 8 * 8;
+    const uint64_t right = pr_need > (uint64_t)g.pl + g.in_w ? pr_need - g.pl : g.in_w;
+    const uint64_t pitch = (cofs + right + 7) / 8 * 8;
     uint32_t band_h = 0;
-    const uint64_t row_bytes = (uint64_t)g.in_w * 2;
-    if (small && rows_needed(g, 1) * row_bytes + 16 <= kLdsBytes) {
+    if (small && rows_needed(g, 1) * pitch * 2 <= kBandBytes) {
         uint32_t lo = 1, hi = g.out_h;
         while (lo < hi) {
             const uint32_t mid = lo + (hi - lo + 1) / 2;
-            if (rows_needed(g, mid) * row_bytes + 16 <= kLdsBytes) lo = mid; else hi = mid - 1;
+            if (rows_needed(g, mid) * pitch * 2 <= kBandBytes) lo = mid; else hi = mid - 1;
         }
         band_h = lo;
     }
     if (band_h > 0) {
         const uint32_t n_bands = (g.out_h + band_h - 1) / band_h;
-        const uint64_t blocks = planes * n_bands;
-        if (blocks <= 0x7FFFFFFFull) {
-            uint64_t need = rows_needed(g, band_h);
-            if (need > g.in_h) need = g.in_h;
-            const uint32_t lds = (uint32_t)(need * row_bytes + 16);
-            uint32_t tw_log2 = 0;
-            while ((1u << tw_log2) < g.out_w && tw_log2 < 6) ++tw_log2;
-            const dim3 grid((uint32_t)blocks), block(kThreads);
+        const uint64_t items = planes * n_bands;
+        if (items <= 0x7FFFFFFFull) {
+            BandGeom b;
+            b.band_h = band_h;
+            b.n_bands = n_bands;
+            b.n_items = (uint32_t)items;
+            b.pitch = (uint32_t)pitch;
+            b.cofs = (uint32_t)cofs;
+            b.lds_rows = (uint32_t)rows_needed(g, band_h);
+            b.rows_pp = g.out_w >= (uint32_t)kThreads ? 1u : (uint32_t)kThreads / g.out_w;
+            b.vec = (g.in_w % 8 == 0) && (((uintptr_t)x & 15u) == 0);
+            const uint32_t lds = b.lds_rows * b.pitch * 2;
+            // persistent blocks: up to 8 per CU (2048 threads) on every CU
+            const uint32_t blocks = (uint32_t)(items < kPoolBlocks ? items : kPoolBlocks);
+            const dim3 grid(blocks), block(kThreads);
             const bool unit_dil = g.dh == 1 && g.dw == 1;
             if (unit_dil && g.ph == 3 && g.pw == 3)
-                hipLaunchKernelGGL((pool_band<KIND, 3, 3>), grid, block, lds, s, x, y, g, band_h,
-                                   n_bands, inv_full, tw_log2);
+                hipLaunchKernelGGL((pool_band<KIND, 3, 3>), grid, block, lds, s, x, y, g, b, inv_full);
             else if (unit_dil && g.ph == 2 && g.pw == 2)
-                hipLaunchKernelGGL((pool_band<KIND, 2, 2>), grid, block, lds, s, x, y, g, band_h,
-                                   n_bands, inv_full, tw_log2);
+                hipLaunchKernelGGL((pool_band<KIND, 2, 2>), grid, block, lds, s, x, y, g, b, inv_full);
             else
-                hipLaunchKernelGGL((pool_band<KIND, 0, 0>), grid, block, lds, s, x, y, g, band_h,
-                                   n_bands, inv_full, tw_log2);
+                hipLaunchKernelGGL((pool_band<KIND, 0, 0>), grid, block, lds, s, x, y, g, b, inv_full);
             return cm_check_launch("pool_band");
         }
     }
