@@ -18,11 +18,15 @@
 // grows by at most 2^15 per k, so MFMA partials are folded into a uint32
 // total every 32768 k when K is larger than that (never overflow int32).
 //
-// Tiling: 256 threads (4 waves, 2x2), block tile 128 rows x 128 cols x 64 k,
-// wave tile 64x64 = 4x4 MFMA 16x16x64 tiles, 3 accumulator sets (hh, mid, ll).
+// Tiling: 512 threads = 8 waves (2 x 4), block tile 128 rows x 128 cols x 64 k,
+// wave tile 64 x 32 = 4 x 2 MFMA 16x16x64 tiles with 3 accumulator sets (hh,
+// mid, ll): 96 accumulator registers, so two waves share each SIMD and one
+// wave's MFMAs run while the other waits on memory or does its limb split.
 // Tiles are split into limbs while being stored to LDS (rows of 64 int8 k
 // values, padded to 80 B so the 16 lanes of a fragment read hit distinct
-// banks).  The next tile's global loads are issued before the MFMA phase.
+// banks).  The next tile's loads are issued before the MFMA phase; loads are
+// unconditional (out-of-range elements are zeroed by the buffer range check
+// or by a select), so all of a tile's loads are in flight at once.
 #include <type_traits>
 
 #include "cm_internal.h"
@@ -31,11 +35,15 @@
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
 constexpr int BM = 128, BN = 128, BK = 64;
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr int kStride = 80;          // LDS bytes per row of 64 int8 (k) values
 constexpr int kFoldIters = 512;      // fold MFMA partials every 512*64 = 32768 k
+constexpr int TI = 4, TJ = 2;        // MFMA tiles per wave: 4 row tiles x 2 column tiles
 
 struct GemmArgs {
     const int16_t* a;     // [rows][k], row stride lda (weights for conv)
@@ -45,7 +53,7 @@ struct GemmArgs {
     uint32_t rows, cols, k;
     uint64_t lda, ldb, ldc;
     uint64_t a_bs, b_bs, c_bs;   // per blockIdx.z (dense only)
-    uint32_t a_vec, b_vec;       // 16-byte loads allowed
+    uint32_t a_vec, b_vec;       // A: 16-byte row loads; B: 8-byte row loads
     // implicit GEMM: column = n*P + p, k = (c*kh + khi)*kw + kwi
     uint32_t C, H, W, OW, P, kh, kw, sh, sw, dh, dw, pt, pl;
     uint64_t x_img, y_img;
@@ -56,7 +64,6 @@ struct GemmArgs {
 // num_records return 0.  kOob is an offset past every resource used here.
 constexpr int kBufferWord3 = 0x00020000;
 constexpr uint32_t kOob = 0x80000000u;
-typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const int16_t* base, uint32_t bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<int16_t*>(base), (short)0, (int)bytes,
@@ -77,9 +84,9 @@ __device__ __forceinline__ uint32_t lo4(uint32_t w0, uint32_t w1) {
 __device__ __forceinline__ int32_t bsum(uint32_t w, int32_t acc) {
     return __builtin_amdgcn_sdot4((int)w, 0x01010101, acc, false);
 }
-
-__device__ __forceinline__ uint32_t pack2(int16_t lo, int16_t hi) {
-    return (uint32_t)(uint16_t)lo | ((uint32_t)(uint16_t)hi << 16);
+// Two zero-extended int16 values -> one word (lo | hi << 16).
+__device__ __forceinline__ uint32_t pack(uint32_t lo, uint32_t hi) {
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
 struct Smem {
@@ -91,25 +98,43 @@ struct Smem {
     uint32_t col_sum[BN];
 };
 
-// ---------------------------------------------------------------- A tile --
-// Thread t owns row t/2 and k values [32*(t&1), +32) of the 64-k slice.  The
-// global loads only fill registers (16 words for 16-byte loads, 32 raw values
-// otherwise); packing and the limb split happen in store(), after the MFMA
-// phase, so every load of a tile is in flight at once.  Loads are
-// unconditional: out-of-range elements read a valid address and are zeroed.
-struct ATile {
-    uint32_t w[16];     // vector path: two int16 per word
-    uint32_t raw[32];   // element path: one int16 per register
+// Splits 16 int16 values (8 packed words, k order) into 16 high and 16 low
+// limb bytes, stores both at byte offset `off` of the two planes, and adds the
+// limb sums to hs / ls.
+__device__ __forceinline__ void store16(uint8_t* hi_plane, uint8_t* lo_plane, uint32_t off,
+                                        const uint32_t (&w)[8], int32_t& hs, int32_t& ls) {
+    uint32_t hi[4], lo[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        hi[j] = hi4(w[2 * j], w[2 * j + 1]);
+        lo[j] = lo4(w[2 * j], w[2 * j + 1]);
+        hs = bsum(hi[j], hs);
+        ls = bsum(lo[j], ls);
+    }
+    *reinterpret_cast<v4i*>(hi_plane + off) = v4i{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+    *reinterpret_cast<v4i*>(lo_plane + off) = v4i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
+}
 
+// ---------------------------------------------------------------- A tile --
+// Thread t owns row t/4 and k values [16*(t&3), +16) of the 64-k slice.  The
+// loads only fill registers (8 words for 16-byte loads, 16 raw values
+// otherwise); packing and the limb split happen in store(), after the MFMA
+// phase, so every load of a tile is in flight at once.
+struct ATile {
+    uint32_t w[8];      // vector path: two int16 per word
+    uint32_t raw[16];   // element path: one int16 per register
+
+    // Global loads (any size): out-of-range elements read a valid address of
+    // the same row and are zeroed afterwards.
     __device__ __forceinline__ void load(const GemmArgs& g, const int16_t* abase, uint32_t row0,
                                          uint32_t k0) {
-        const uint32_t r = row0 + (threadIdx.x >> 1);
-        const uint32_t ks = k0 + (threadIdx.x & 1) * 32;
+        const uint32_t r = row0 + (threadIdx.x >> 2);
+        const uint32_t ks = k0 + (threadIdx.x & 3) * 16;
         const bool rok = r < g.rows;
         const int16_t* p = abase + (uint64_t)(rok ? r : 0u) * g.lda;
         if (g.a_vec) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < 2; ++q) {
                 const bool ok = rok && ks + q * 8 < g.k;
                 v4i v = *reinterpret_cast<const v4i*>(p + (ok ? ks + q * 8 : 0u));
                 const v4i z = {0, 0, 0, 0};
@@ -118,25 +143,25 @@ struct ATile {
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < 32; ++j) {
+            for (int j = 0; j < 16; ++j) {
                 const bool ok = rok && ks + j < g.k;
                 raw[j] = ok ? (uint32_t)(uint16_t)p[ok ? ks + j : 0u] : 0u;
             }
         }
     }
     // Same tile through a buffer resource based at the block's first row (the
-    // tile spans fewer than 2^31 bytes): an element outside the matrix gets
+    // 128 rows span fewer than 2^31 bytes): an element outside the matrix gets
     // offset kOob and reads as 0, so no load needs a condition or a select.
     template <bool VEC>
     __device__ __forceinline__ void load_buf(const GemmArgs& g, __amdgpu_buffer_rsrc_t ra,
                                              uint32_t row0, uint32_t k0) {
-        const uint32_t rel = threadIdx.x >> 1;
-        const uint32_t ks = k0 + (threadIdx.x & 1) * 32;
+        const uint32_t rel = threadIdx.x >> 2;
+        const uint32_t ks = k0 + (threadIdx.x & 3) * 16;
         const bool rok = row0 + rel < g.rows;
         const uint32_t rbyte = rel * (uint32_t)g.lda * 2u;
         if constexpr (VEC) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
+            for (int q = 0; q < 2; ++q) {
                 const bool ok = rok && ks + q * 8 < g.k;
                 const v4u v = __builtin_amdgcn_raw_buffer_load_b128(
                     ra, ok ? rbyte + (ks + q * 8) * 2u : kOob, 0, 0);
@@ -144,7 +169,7 @@ struct ATile {
             }
         } else {
 #pragma unroll
-            for (int j = 0; j < 32; ++j) {
+            for (int j = 0; j < 16; ++j) {
                 const bool ok = rok && ks + j < g.k;
                 raw[j] = __builtin_amdgcn_raw_buffer_load_b16(ra, ok ? rbyte + (ks + j) * 2u : kOob, 0, 0);
             }
@@ -155,55 +180,68 @@ struct ATile {
     __device__ __forceinline__ void store(bool vec, Smem& s, int32_t& hs, int32_t& ls) {
         if (!vec) {
 #pragma unroll
-            for (int j = 0; j < 16; ++j) w[j] = __builtin_amdgcn_perm(raw[2 * j + 1], raw[2 * j], 0x05040100u);
+            for (int j = 0; j < 8; ++j) w[j] = pack(raw[2 * j], raw[2 * j + 1]);
         }
-        const uint32_t off = (threadIdx.x >> 1) * kStride + (threadIdx.x & 1) * 32;
-        uint32_t hi[8], lo[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            hi[j] = hi4(w[2 * j], w[2 * j + 1]);
-            lo[j] = lo4(w[2 * j], w[2 * j + 1]);
-            hs = bsum(hi[j], hs);
-            ls = bsum(lo[j], ls);
-        }
-        v4i* dh = reinterpret_cast<v4i*>(s.a_hi + off);
-        v4i* dl = reinterpret_cast<v4i*>(s.a_lo + off);
-        dh[0] = v4i{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-        dh[1] = v4i{(int)hi[4], (int)hi[5], (int)hi[6], (int)hi[7]};
-        dl[0] = v4i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
-        dl[1] = v4i{(int)lo[4], (int)lo[5], (int)lo[6], (int)lo[7]};
+        store16(s.a_hi, s.a_lo, (threadIdx.x >> 2) * kStride + (threadIdx.x & 3) * 16, w, hs, ls);
     }
 };
 
 // ---------------------------------------------------------- dense B tile --
-// Thread t owns columns [8*(t>>4), +8) and k rows [4*(t&15), +4).  Lanes of a
+// Thread t owns columns [4*(t>>4), +4) and k rows [4*(t&15), +4).  Lanes of a
 // wave differ mostly in k, so the transposing 4-byte LDS stores of one column
-// land in 16 different banks (4-way at worst) instead of one.
+// land in 16 different banks instead of one.
 struct DenseBTile {
-    uint32_t w[4][4];     // [k row][word of 2 columns]
-    uint32_t raw[4][8];   // buffer element path: [k row][column], one int16 each
+    uint32_t w[4][2];     // [k row][word of 2 columns]
+    uint32_t raw[4][4];   // element path: [k row][column], one int16 each
 
+    __device__ __forceinline__ void load(const GemmArgs& g, const int16_t* bbase, uint32_t col0,
+                                         uint32_t k0) {
+        const uint32_t cb = col0 + (threadIdx.x >> 4) * 4;
+        const uint32_t kb = k0 + (threadIdx.x & 15) * 4;
+        if (g.b_vec) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bool ok = kb + i < g.k && cb < g.cols;
+                v2i v = *reinterpret_cast<const v2i*>(bbase + (ok ? (uint64_t)(kb + i) * g.ldb + cb : 0u));
+                const v2i z = {0, 0};
+                v = ok ? v : z;
+                w[i][0] = v[0]; w[i][1] = v[1];
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const bool kok = kb + i < g.k;
+                const int16_t* p = bbase + (kok ? (uint64_t)(kb + i) * g.ldb : 0u);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const bool ok = kok && cb + q < g.cols;
+                    const int16_t v = p[ok ? cb + q : 0u];
+                    raw[i][q] = ok ? (uint32_t)(uint16_t)v : 0u;
+                }
+            }
+        }
+    }
     // Buffer resource based at (k0, col0) for each k step (64 rows span fewer
     // than 2^31 bytes); elements outside the matrix read as 0 through kOob.
     template <bool VEC>
     __device__ __forceinline__ void load_buf(const GemmArgs& g, __amdgpu_buffer_rsrc_t rb,
                                              uint32_t col0, uint32_t k0) {
-        const uint32_t cr = (threadIdx.x >> 4) * 8;
+        const uint32_t cr = (threadIdx.x >> 4) * 4;
         const uint32_t kr = (threadIdx.x & 15) * 4;
         if constexpr (VEC) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const bool ok = k0 + kr + i < g.k && col0 + cr < g.cols;
-                const v4u v = __builtin_amdgcn_raw_buffer_load_b128(
+                const v2u v = __builtin_amdgcn_raw_buffer_load_b64(
                     rb, ok ? ((kr + i) * (uint32_t)g.ldb + cr) * 2u : kOob, 0, 0);
-                w[i][0] = v[0]; w[i][1] = v[1]; w[i][2] = v[2]; w[i][3] = v[3];
+                w[i][0] = v[0]; w[i][1] = v[1];
             }
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const bool kok = k0 + kr + i < g.k;
 #pragma unroll
-                for (int q = 0; q < 8; ++q) {
+                for (int q = 0; q < 4; ++q) {
                     const bool ok = kok && col0 + cr + q < g.cols;
                     raw[i][q] = __builtin_amdgcn_raw_buffer_load_b16(
                         rb, ok ? ((kr + i) * (uint32_t)g.ldb + cr + q) * 2u : kOob, 0, 0);
@@ -215,46 +253,16 @@ struct DenseBTile {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-                w[i][q] = __builtin_amdgcn_perm(raw[i][2 * q + 1], raw[i][2 * q], 0x05040100u);
+            for (int q = 0; q < 2; ++q) w[i][q] = pack(raw[i][2 * q], raw[i][2 * q + 1]);
     }
-
-    __device__ __forceinline__ void load(const GemmArgs& g, const int16_t* bbase, uint32_t col0,
-                                         uint32_t k0) {
-        const uint32_t cb = col0 + (threadIdx.x >> 4) * 8;
-        const uint32_t kb = k0 + (threadIdx.x & 15) * 4;
-        if (g.b_vec) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const bool ok = kb + i < g.k && cb < g.cols;
-                v4i v = *reinterpret_cast<const v4i*>(bbase + (ok ? (uint64_t)(kb + i) * g.ldb + cb : 0u));
-                const v4i z = {0, 0, 0, 0};
-                v = ok ? v : z;
-                w[i][0] = v[0]; w[i][1] = v[1]; w[i][2] = v[2]; w[i][3] = v[3];
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const bool kok = kb + i < g.k;
-                const int16_t* p = bbase + (kok ? (uint64_t)(kb + i) * g.ldb : 0u);
-#pragma unroll
-                for (int q = 0; q < 4; ++q) {
-                    const uint32_t c = cb + 2 * q;
-                    const bool ok0 = kok && c < g.cols, ok1 = kok && c + 1 < g.cols;
-                    int16_t v0 = p[ok0 ? c : 0u], v1 = p[ok1 ? c + 1 : 0u];
-                    w[i][q] = pack2(ok0 ? v0 : (int16_t)0, ok1 ? v1 : (int16_t)0);
-                }
-            }
-        }
-    }
-    // Transposes 4 k rows x 8 columns into one limb word per column: for the
+    // Transposes 4 k rows x 4 columns into one limb word per column: for the
     // column pair held in word q, two perms interleave rows (0,1) and (2,3),
     // two more split even / odd columns.  hs / ls accumulate per-column limb sums.
-    __device__ __forceinline__ void store(Smem& s, int32_t (&hs)[8], int32_t (&ls)[8]) const {
-        const uint32_t cl = (threadIdx.x >> 4) * 8;
+    __device__ __forceinline__ void store(Smem& s, int32_t (&hs)[4], int32_t (&ls)[4]) const {
+        const uint32_t cl = (threadIdx.x >> 4) * 4;
         const uint32_t kbyte = (threadIdx.x & 15) * 4;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < 2; ++q) {
             const uint32_t t01 = __builtin_amdgcn_perm(w[1][q], w[0][q], 0x07030501u);
             const uint32_t t23 = __builtin_amdgcn_perm(w[3][q], w[2][q], 0x07030501u);
             const uint32_t u01 = __builtin_amdgcn_perm(w[1][q], w[0][q], 0x06020400u);
@@ -277,20 +285,20 @@ struct DenseBTile {
 };
 
 // Column sums of the dense B tile: count = k values per column this thread stored.
-__device__ __forceinline__ void publish_dense(Smem& s, const int32_t (&hs)[8], const int32_t (&ls)[8],
+__device__ __forceinline__ void publish_dense(Smem& s, const int32_t (&hs)[4], const int32_t (&ls)[4],
                                               uint32_t count) {
-    const uint32_t cl = (threadIdx.x >> 4) * 8;
+    const uint32_t cl = (threadIdx.x >> 4) * 4;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < 4; ++j)
         atomicAdd(&s.col_sum[cl + j], 256u * (uint32_t)hs[j] + (uint32_t)ls[j] + 128u * count);
 }
 
 // ------------------------------------------------------- im2col B tile --
-// Thread t owns column (pixel) t&127 and k values [32*(t>>7), +32): the lanes
+// Thread t owns column (pixel) t&127 and k values [16*(t>>7), +16): the lanes
 // of one load instruction read 64 neighbouring output pixels at the same k,
-// which coalesce.  The 32 values stay raw until store().
+// which coalesce.  The 16 values stay raw until store().
 struct ConvBTile {
-    uint32_t raw[32];
+    uint32_t raw[16];
     const int16_t* xb;   // image base of this thread's column
     int32_t ih0, iw0;    // window origin of this thread's output pixel
     int32_t pbase;       // ih0 * W + iw0 (may be negative; only valid taps are read)
@@ -311,27 +319,26 @@ struct ConvBTile {
     }
     // Gather through the per-block k table tab[k] = {2*(c*H*W + dy*W + dx), dy << 16 | dx}
     // (dy = khi*dh, dx = kwi*dw) with buffer loads over the whole input tensor
-    // (fewer than 2^31 bytes): an invalid tap gets offset 0x80000000, past the
+    // (fewer than 2^31 bytes): an invalid tap gets offset kOob, past the
     // buffer's size, and the hardware returns 0 for it.
     __device__ __forceinline__ void load_tab(const GemmArgs& g, uint32_t k0, const int2* tab,
                                              __amdgpu_buffer_rsrc_t rsrc) {
-        const uint32_t ks = __builtin_amdgcn_readfirstlane(k0 + (threadIdx.x >> 7) * 32);
+        const uint32_t ks = __builtin_amdgcn_readfirstlane(k0 + (threadIdx.x >> 7) * 16);
 #pragma unroll
-        for (int j = 0; j < 32; ++j) {
+        for (int j = 0; j < 16; ++j) {
             // k < kTabMax always (the padded k range of a K <= kTabMax problem);
             // entries past g.k are never used.
             const uint32_t k = ks + j;
             const int2 t = tab[k];
             const int32_t ih = ih0 + (t.y >> 16), iw = iw0 + (t.y & 0xFFFF);
             const bool ok = col_ok && k < g.k && (uint32_t)ih < g.H && (uint32_t)iw < g.W;
-            const uint32_t off = ok ? (uint32_t)(pbyte + t.x) : 0x80000000u;
-            raw[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, 0);
+            raw[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, ok ? (uint32_t)(pbyte + t.x) : kOob, 0, 0);
         }
     }
     // Gather for any size: k decomposed incrementally, global loads of a valid
     // address (element 0 of the image for invalid taps), zeroed afterwards.
     __device__ __forceinline__ void load(const GemmArgs& g, uint32_t k0) {
-        const uint32_t ks = k0 + (threadIdx.x >> 7) * 32;
+        const uint32_t ks = k0 + (threadIdx.x >> 7) * 16;
         const uint32_t kk = g.kh * g.kw;
         uint32_t c = ks / kk;
         uint32_t r = ks - c * kk;
@@ -339,7 +346,7 @@ struct ConvBTile {
         uint32_t kwi = r - khi * g.kw;
         const uint32_t hw = g.H * g.W;
 #pragma unroll
-        for (int j = 0; j < 32; ++j) {
+        for (int j = 0; j < 16; ++j) {
             const int32_t ih = ih0 + (int32_t)(khi * g.dh);
             const int32_t iw = iw0 + (int32_t)(kwi * g.dw);
             const bool ok = col_ok && ks + j < g.k && ih >= 0 && ih < (int32_t)g.H && iw >= 0 &&
@@ -353,23 +360,10 @@ struct ConvBTile {
         }
     }
     __device__ __forceinline__ void store(Smem& s, int32_t& hs, int32_t& ls) const {
-        const uint32_t off = (threadIdx.x & 127) * kStride + (threadIdx.x >> 7) * 32;
-        uint32_t hi[8], lo[8];
+        uint32_t w[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const uint32_t w0 = __builtin_amdgcn_perm(raw[4 * j + 1], raw[4 * j], 0x05040100u);
-            const uint32_t w1 = __builtin_amdgcn_perm(raw[4 * j + 3], raw[4 * j + 2], 0x05040100u);
-            hi[j] = hi4(w0, w1);
-            lo[j] = lo4(w0, w1);
-            hs = bsum(hi[j], hs);
-            ls = bsum(lo[j], ls);
-        }
-        v4i* dh = reinterpret_cast<v4i*>(s.b_hi + off);
-        v4i* dl = reinterpret_cast<v4i*>(s.b_lo + off);
-        dh[0] = v4i{(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-        dh[1] = v4i{(int)hi[4], (int)hi[5], (int)hi[6], (int)hi[7]};
-        dl[0] = v4i{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
-        dl[1] = v4i{(int)lo[4], (int)lo[5], (int)lo[6], (int)lo[7]};
+        for (int j = 0; j < 8; ++j) w[j] = pack(raw[2 * j], raw[2 * j + 1]);
+        store16(s.b_hi, s.b_lo, (threadIdx.x & 127) * kStride + (threadIdx.x >> 7) * 16, w, hs, ls);
     }
 };
 
@@ -378,8 +372,8 @@ struct ConvBTile {
 enum { B_DENSE = 0, B_CONV_TAB = 1, B_CONV_INC = 2 };
 constexpr uint32_t kTabMax = 2048;
 
-// AV / BV: 0 = 16-byte loads chosen at run time (g.a_vec / g.b_vec, global
-// loads), 1 = 16-byte buffer loads, 2 = element buffer loads.  Fixing the path
+// AV / BV: 0 = vector loads chosen at run time (g.a_vec / g.b_vec, global
+// loads), 1 = vector buffer loads, 2 = element buffer loads.  Fixing the path
 // at compile time keeps the staged registers identical on every path, so no
 // copy (and no wait for outstanding loads) is needed where paths would merge.
 template <int MODE, bool HAS_BIAS, bool FOLD, bool BUF, int AV, int BV>
@@ -390,7 +384,7 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t row0 = blockIdx.y * BM;
     const uint32_t col0 = blockIdx.x * BN;
-    const uint32_t wrow = (wave >> 1) * 64, wcol = (wave & 1) * 64;
+    const uint32_t wrow = (wave >> 2) * 64, wcol = (wave & 3) * 32;
 
     const int16_t* abase = g.a + (CONV ? 0 : (uint64_t)blockIdx.z * g.a_bs);
     const int16_t* bbase = g.b + (CONV ? 0 : (uint64_t)blockIdx.z * g.b_bs);
@@ -410,15 +404,11 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     }
     __syncthreads();
 
-    // One register stage: the next tile's global loads are issued before the
-    // MFMA phase and staged in LDS after it.  (A second register stage does not
-    // fit beside the 192 accumulator registers without spilling, and measured
-    // slower.)
     ATile at0;
     using BTile = typename std::conditional<CONV, ConvBTile, DenseBTile>::type;
     BTile bt0;
     int32_t row_hs = 0, row_ls = 0;
-    int32_t dhs[8] = {0, 0, 0, 0, 0, 0, 0, 0}, dls[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int32_t dhs[4] = {0, 0, 0, 0}, dls[4] = {0, 0, 0, 0};
     int32_t chs = 0, cls = 0;
     if constexpr (CONV) bt0.init(g, col0);
     const __amdgpu_buffer_rsrc_t xrsrc = make_rsrc(g.b, g.x_bytes);   // table mode only
@@ -426,11 +416,11 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     const __amdgpu_buffer_rsrc_t arsrc =
         make_rsrc(abase + (uint64_t)row0 * g.lda, arows * (uint32_t)g.lda * 2u);   // BUF only
 
-    v4i hh[4][4], mid[4][4], ll[4][4], tot[4][4];
+    v4i hh[TI][TJ], mid[TI][TJ], ll[TI][TJ], tot[TI][TJ];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < TJ; ++j) {
             hh[i][j] = v4i{0, 0, 0, 0}; mid[i][j] = v4i{0, 0, 0, 0}; ll[i][j] = v4i{0, 0, 0, 0};
             if constexpr (FOLD) tot[i][j] = v4i{0, 0, 0, 0};
         }
@@ -458,47 +448,45 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
         if constexpr (CONV) {
             bt.store(s, chs, cls);
         } else {
-            if constexpr (BUF && BV == 2) bt.pack_raw();
+            if (BUF ? BV == 2 : !g.b_vec) bt.pack_raw();
             bt.store(s, dhs, dls);
         }
         __syncthreads();
     };
     auto mfma_step = [&](uint32_t it) {
-        // A fragments for the wave's 4 row tiles stay live; B fragments are
-        // read one column tile at a time (8 registers instead of 32).
-        v4i ah[4], al[4];
         const uint32_t koff = (lane >> 4) * 16;
+        v4i ah[TI], al[TI];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < TI; ++i) {
             const uint32_t r = (wrow + i * 16 + (lane & 15)) * kStride + koff;
             ah[i] = *reinterpret_cast<const v4i*>(s.a_hi + r);
             al[i] = *reinterpret_cast<const v4i*>(s.a_lo + r);
         }
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
+        for (int j = 0; j < TJ; ++j) {
             const uint32_t cidx = (wcol + j * 16 + (lane & 15)) * kStride + koff;
             const v4i bh = *reinterpret_cast<const v4i*>(s.b_hi + cidx);
             const v4i bl = *reinterpret_cast<const v4i*>(s.b_lo + cidx);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < TI; ++i)
                 hh[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bh, hh[i][j], 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < TI; ++i)
                 mid[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bl, mid[i][j], 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < TI; ++i)
                 ll[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], bl, ll[i][j], 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < TI; ++i)
                 mid[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], bh, mid[i][j], 0, 0, 0);
         }
 
         if constexpr (FOLD) {
             if ((it + 1) % kFoldIters == 0) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < TI; ++i)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
+                    for (int j = 0; j < TJ; ++j) {
 #pragma unroll
                         for (int e = 0; e < 4; ++e)
                             tot[i][j][e] = (int)((uint32_t)tot[i][j][e] + ((uint32_t)hh[i][j][e] << 16) +
@@ -517,13 +505,14 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
         mfma_step(it);
     }
 
-    // row sums (sum a = 256*hs + ls + 128*count); the two threads of a row are
-    // adjacent lanes, each stored 32 k values per step
-    uint32_t row_sum = 256u * (uint32_t)row_hs + (uint32_t)row_ls + 128u * 32u * nk;
+    // row sums (sum a = 256*hs + ls + 128*count); the four threads of a row are
+    // adjacent lanes, each stored 16 k values per step
+    uint32_t row_sum = 256u * (uint32_t)row_hs + (uint32_t)row_ls + 128u * 16u * nk;
     row_sum += (uint32_t)__shfl_xor((int)row_sum, 1, 64);
-    if ((threadIdx.x & 1) == 0) s.row_sum[threadIdx.x >> 1] = row_sum;
+    row_sum += (uint32_t)__shfl_xor((int)row_sum, 2, 64);
+    if ((threadIdx.x & 3) == 0) s.row_sum[threadIdx.x >> 2] = row_sum;
     if constexpr (CONV)
-        atomicAdd(&s.col_sum[threadIdx.x & 127], 256u * (uint32_t)chs + (uint32_t)cls + 128u * 32u * nk);
+        atomicAdd(&s.col_sum[threadIdx.x & 127], 256u * (uint32_t)chs + (uint32_t)cls + 128u * 16u * nk);
     else
         publish_dense(s, dhs, dls, 4u * nk);
     __syncthreads();
@@ -531,7 +520,7 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     const uint32_t kp_term = 16384u * (nk * (uint32_t)BK);
     int16_t* cptr = g.c + (CONV ? 0 : (uint64_t)blockIdx.z * g.c_bs);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < TJ; ++j) {
         const uint32_t cl = wcol + j * 16 + (lane & 15);
         const uint32_t col = col0 + cl;
         if (col >= g.cols) continue;
@@ -547,7 +536,7 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
         }
         const uint32_t csum = s.col_sum[cl];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < TI; ++i) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const uint32_t rl = wrow + i * 16 + (lane >> 4) * 4 + e;
@@ -564,7 +553,7 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     }
 }
 
-inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+inline bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p & (n - 1)) == 0; }
 
 template <int MODE>
 int launch_gemm(GemmArgs& g, uint32_t zdim, hipStream_t s, const char* name) {
@@ -614,14 +603,14 @@ int cm_matmul_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n,
     g.rows = n; g.cols = m; g.k = k;
     g.lda = k; g.ldb = m; g.ldc = m;
     g.a_bs = a_bs; g.b_bs = b_bs; g.c_bs = c_bs;
-    g.a_vec = aligned16(a) && k % 8 == 0 && a_bs % 8 == 0;
-    g.b_vec = aligned16(b) && m % 8 == 0 && b_bs % 8 == 0;
+    g.a_vec = aligned(a, 16) && k % 8 == 0 && a_bs % 8 == 0;
+    g.b_vec = aligned(b, 8) && m % 4 == 0 && b_bs % 4 == 0;
     if (c_bs == 0 && batch > 1) {
         // every batch step overwrites the same C; the sequential reference leaves the last one
         g.a = a + (uint64_t)(batch - 1) * a_bs;
         g.b = b + (uint64_t)(batch - 1) * b_bs;
-        g.a_vec = aligned16(g.a) && k % 8 == 0;
-        g.b_vec = aligned16(g.b) && m % 8 == 0;
+        g.a_vec = aligned(g.a, 16) && k % 8 == 0;
+        g.b_vec = aligned(g.b, 8) && m % 4 == 0;
         batch = 1;
     }
     uint32_t done = 0;
@@ -654,7 +643,7 @@ int cm_conv_gemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias,
     g.a = w; g.b = x; g.c = y; g.bias = bias;
     g.rows = out_ch; g.cols = (uint32_t)cols; g.k = (uint32_t)K;
     g.lda = K;
-    g.a_vec = aligned16(w) && K % 8 == 0;
+    g.a_vec = aligned(w, 16) && K % 8 == 0;
     g.b_vec = 0;
     g.C = in_ch; g.H = in_h; g.W = in_w; g.OW = out_w; g.P = (uint32_t)P;
     g.kh = kh; g.kw = kw; g.sh = sh; g.sw = sw; g.dh = dh; g.dw = dw; g.pt = pad_top; g.pl = pad_left;
@@ -679,8 +668,8 @@ int cm_conv_pointwise_launch(const int16_t* x, const int16_t* w, const int16_t* 
     g.rows = out_ch; g.cols = hw; g.k = in_ch;
     g.lda = in_ch; g.ldb = hw; g.ldc = hw;
     g.a_bs = 0; g.b_bs = (uint64_t)in_ch * hw; g.c_bs = (uint64_t)out_ch * hw;
-    g.a_vec = aligned16(w) && in_ch % 8 == 0;
-    g.b_vec = aligned16(x) && hw % 8 == 0 && g.b_bs % 8 == 0;
+    g.a_vec = aligned(w, 16) && in_ch % 8 == 0;
+    g.b_vec = aligned(x, 8) && hw % 4 == 0 && g.b_bs % 4 == 0;
     uint32_t done = 0;
     while (done < batch) {
         const uint32_t z = (batch - done) > 65535u ? 65535u : (batch - done);
