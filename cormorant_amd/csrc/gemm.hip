@@ -89,11 +89,17 @@ __device__ __forceinline__ uint32_t pack(uint32_t lo, uint32_t hi) {
     return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
 }
 
-struct Smem {
+// One k step's limb planes.  Two of them alternate: the MFMA phase reads one
+// while the next tile is split into the other.
+struct Planes {
     uint8_t a_hi[BM * kStride];
     uint8_t a_lo[BM * kStride];
     uint8_t b_hi[BN * kStride];
     uint8_t b_lo[BN * kStride];
+};
+
+struct Smem {
+    Planes st[2];
     uint32_t row_sum[BM];
     uint32_t col_sum[BN];
 };
@@ -177,7 +183,7 @@ struct ATile {
     }
     // Stores the limbs; hs / ls accumulate the sums of the high and low limbs
     // of this thread's values (sum a = 256*hs + ls + 128*count).
-    __device__ __forceinline__ void store(bool vec, Smem& s, int32_t& hs, int32_t& ls) {
+    __device__ __forceinline__ void store(bool vec, Planes& s, int32_t& hs, int32_t& ls) {
         if (!vec) {
 #pragma unroll
             for (int j = 0; j < 8; ++j) w[j] = pack(raw[2 * j], raw[2 * j + 1]);
@@ -258,7 +264,7 @@ struct DenseBTile {
     // Transposes 4 k rows x 4 columns into one limb word per column: for the
     // column pair held in word q, two perms interleave rows (0,1) and (2,3),
     // two more split even / odd columns.  hs / ls accumulate per-column limb sums.
-    __device__ __forceinline__ void store(Smem& s, int32_t (&hs)[4], int32_t (&ls)[4]) const {
+    __device__ __forceinline__ void store(Planes& s, int32_t (&hs)[4], int32_t (&ls)[4]) const {
         const uint32_t cl = (threadIdx.x >> 4) * 4;
         const uint32_t kbyte = (threadIdx.x & 15) * 4;
 #pragma unroll
@@ -359,7 +365,7 @@ struct ConvBTile {
             }
         }
     }
-    __device__ __forceinline__ void store(Smem& s, int32_t& hs, int32_t& ls) const {
+    __device__ __forceinline__ void store(Planes& s, int32_t& hs, int32_t& ls) const {
         uint32_t w[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) w[j] = pack(raw[2 * j], raw[2 * j + 1]);
@@ -404,13 +410,19 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     }
     __syncthreads();
 
-    ATile at0;
+    // Two register stages and two LDS planes: while the MFMA phase reads the
+    // planes of step k, the loads of step k+2 are in flight and step k+1 (already
+    // in registers) is split into the other planes; one barrier per step.
+    ATile at[2];
     using BTile = typename std::conditional<CONV, ConvBTile, DenseBTile>::type;
-    BTile bt0;
+    BTile bt[2];
     int32_t row_hs = 0, row_ls = 0;
     int32_t dhs[4] = {0, 0, 0, 0}, dls[4] = {0, 0, 0, 0};
     int32_t chs = 0, cls = 0;
-    if constexpr (CONV) bt0.init(g, col0);
+    if constexpr (CONV) {
+        bt[0].init(g, col0);
+        bt[1].init(g, col0);
+    }
     const __amdgpu_buffer_rsrc_t xrsrc = make_rsrc(g.b, g.x_bytes);   // table mode only
     const uint32_t arows = g.rows - row0 < (uint32_t)BM ? g.rows - row0 : (uint32_t)BM;
     const __amdgpu_buffer_rsrc_t arsrc =
@@ -425,48 +437,46 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
             if constexpr (FOLD) tot[i][j] = v4i{0, 0, 0, 0};
         }
 
-    auto load_tile = [&](ATile& at, BTile& bt, uint32_t k0) {
-        if constexpr (BUF) at.template load_buf<AV == 1>(g, arsrc, row0, k0);
-        else at.load(g, abase, row0, k0);
+    auto load_tile = [&](ATile& a, BTile& b, uint32_t k0) {
+        if constexpr (BUF) a.template load_buf<AV == 1>(g, arsrc, row0, k0);
+        else a.load(g, abase, row0, k0);
         if constexpr (MODE == B_CONV_TAB) {
-            bt.load_tab(g, k0, tab, xrsrc);
+            b.load_tab(g, k0, tab, xrsrc);
         } else if constexpr (MODE == B_CONV_INC) {
-            bt.load(g, k0);
+            b.load(g, k0);
         } else if constexpr (BUF) {
             const uint32_t kr = g.k - k0 < (uint32_t)BK ? g.k - k0 : (uint32_t)BK;
             const uint32_t cr = g.cols - col0 < (uint32_t)BN ? g.cols - col0 : (uint32_t)BN;
-            bt.template load_buf<BV == 1>(g, make_rsrc(bbase + (uint64_t)k0 * g.ldb + col0,
-                                                       ((kr - 1) * (uint32_t)g.ldb + cr) * 2u),
-                                          col0, k0);
+            b.template load_buf<BV == 1>(g, make_rsrc(bbase + (uint64_t)k0 * g.ldb + col0,
+                                                      ((kr - 1) * (uint32_t)g.ldb + cr) * 2u),
+                                         col0, k0);
         } else {
-            bt.load(g, bbase, col0, k0);
+            b.load(g, bbase, col0, k0);
         }
     };
-    auto stage_tile = [&](ATile& at, BTile& bt) {
-        __syncthreads();                 // previous tile fully consumed
-        at.store(AV == 0 ? g.a_vec != 0 : AV == 1, s, row_hs, row_ls);
+    auto stage_tile = [&](ATile& a, BTile& b, Planes& p) {
+        a.store(AV == 0 ? g.a_vec != 0 : AV == 1, p, row_hs, row_ls);
         if constexpr (CONV) {
-            bt.store(s, chs, cls);
+            b.store(p, chs, cls);
         } else {
-            if (BUF ? BV == 2 : !g.b_vec) bt.pack_raw();
-            bt.store(s, dhs, dls);
+            if (BUF ? BV == 2 : !g.b_vec) b.pack_raw();
+            b.store(p, dhs, dls);
         }
-        __syncthreads();
     };
-    auto mfma_step = [&](uint32_t it) {
+    auto mfma_step = [&](const Planes& p, uint32_t it) {
         const uint32_t koff = (lane >> 4) * 16;
         v4i ah[TI], al[TI];
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
             const uint32_t r = (wrow + i * 16 + (lane & 15)) * kStride + koff;
-            ah[i] = *reinterpret_cast<const v4i*>(s.a_hi + r);
-            al[i] = *reinterpret_cast<const v4i*>(s.a_lo + r);
+            ah[i] = *reinterpret_cast<const v4i*>(p.a_hi + r);
+            al[i] = *reinterpret_cast<const v4i*>(p.a_lo + r);
         }
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
             const uint32_t cidx = (wcol + j * 16 + (lane & 15)) * kStride + koff;
-            const v4i bh = *reinterpret_cast<const v4i*>(s.b_hi + cidx);
-            const v4i bl = *reinterpret_cast<const v4i*>(s.b_lo + cidx);
+            const v4i bh = *reinterpret_cast<const v4i*>(p.b_hi + cidx);
+            const v4i bl = *reinterpret_cast<const v4i*>(p.b_lo + cidx);
 #pragma unroll
             for (int i = 0; i < TI; ++i)
                 hh[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bh, hh[i][j], 0, 0, 0);
@@ -498,11 +508,24 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     };
 
     const uint32_t nk = (g.k + BK - 1) / BK;
-    load_tile(at0, bt0, 0);
-    for (uint32_t it = 0; it < nk; ++it) {
-        stage_tile(at0, bt0);
-        if (it + 1 < nk) load_tile(at0, bt0, (it + 1) * BK);
-        mfma_step(it);
+    load_tile(at[0], bt[0], 0);
+    if (nk > 1) load_tile(at[1], bt[1], BK);
+    stage_tile(at[0], bt[0], s.st[0]);
+    __syncthreads();
+    // Step it computes on planes it%2; register set it%2 is free (its tile was
+    // staged one step earlier) and receives step it+2; set (it+1)%2 holds step
+    // it+1 and is staged into planes (it+1)%2.  The loop is unrolled by two so
+    // every register set and plane index is static.
+    for (uint32_t it = 0; it < nk; it += 2) {
+        if (it + 2 < nk) load_tile(at[0], bt[0], (it + 2) * BK);
+        mfma_step(s.st[0], it);
+        if (it + 1 < nk) stage_tile(at[1], bt[1], s.st[1]);
+        __syncthreads();
+        if (it + 1 >= nk) break;
+        if (it + 3 < nk) load_tile(at[1], bt[1], (it + 3) * BK);
+        mfma_step(s.st[1], it + 1);
+        if (it + 2 < nk) stage_tile(at[0], bt[0], s.st[0]);
+        __syncthreads();
     }
 
     // row sums (sum a = 256*hs + ls + 128*count); the four threads of a row are
