@@ -454,13 +454,39 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
             b.load(g, bbase, col0, k0);
         }
     };
-    auto stage_tile = [&](ATile& a, BTile& b, Planes& p) {
-        a.store(AV == 0 ? g.a_vec != 0 : AV == 1, p, row_hs, row_ls);
+    // Splits a staged tile into planes p.  Its limb sums count only if the tile
+    // is a real k step (`real`); the last step of the unrolled loop stages a
+    // stale register set into planes nobody reads, without a branch, so the
+    // split can interleave with the MFMA phase.
+    auto stage_tile = [&](ATile& a, BTile& b, Planes& p, bool real) {
+        int32_t h = 0, l = 0;
+        a.store(AV == 0 ? g.a_vec != 0 : AV == 1, p, h, l);
+        row_hs += real ? h : 0;
+        row_ls += real ? l : 0;
         if constexpr (CONV) {
-            b.store(p, chs, cls);
+            int32_t ch = 0, cl = 0;
+            b.store(p, ch, cl);
+            chs += real ? ch : 0;
+            cls += real ? cl : 0;
         } else {
             if (BUF ? BV == 2 : !g.b_vec) b.pack_raw();
-            b.store(p, dhs, dls);
+            int32_t th[4] = {0, 0, 0, 0}, tl[4] = {0, 0, 0, 0};
+            b.store(p, th, tl);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                dhs[j] += real ? th[j] : 0;
+                dls[j] += real ? tl[j] : 0;
+            }
+        }
+    };
+    // Scheduling hint for the block of one k step: alternate each MFMA with two
+    // VALU instructions of the split, so the matrix core and the vector ALU run
+    // together.
+    auto interleave = [&]() {
+#pragma unroll
+        for (int q = 0; q < TI * TJ * 4; ++q) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
         }
     };
     auto mfma_step = [&](const Planes& p, uint32_t it) {
@@ -510,7 +536,7 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     const uint32_t nk = (g.k + BK - 1) / BK;
     load_tile(at[0], bt[0], 0);
     if (nk > 1) load_tile(at[1], bt[1], BK);
-    stage_tile(at[0], bt[0], s.st[0]);
+    stage_tile(at[0], bt[0], s.st[0], true);
     __syncthreads();
     // Step it computes on planes it%2; register set it%2 is free (its tile was
     // staged one step earlier) and receives step it+2; set (it+1)%2 holds step
@@ -519,12 +545,14 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     for (uint32_t it = 0; it < nk; it += 2) {
         if (it + 2 < nk) load_tile(at[0], bt[0], (it + 2) * BK);
         mfma_step(s.st[0], it);
-        if (it + 1 < nk) stage_tile(at[1], bt[1], s.st[1]);
+        stage_tile(at[1], bt[1], s.st[1], it + 1 < nk);
+        interleave();
         __syncthreads();
         if (it + 1 >= nk) break;
         if (it + 3 < nk) load_tile(at[1], bt[1], (it + 3) * BK);
         mfma_step(s.st[1], it + 1);
-        if (it + 2 < nk) stage_tile(at[0], bt[0], s.st[0]);
+        stage_tile(at[0], bt[0], s.st[0], it + 2 < nk);
+        interleave();
         __syncthreads();
     }
 
