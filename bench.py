@@ -17,6 +17,7 @@ and the MobileNetV2-like graph's images/s at batch 16, each with its roofline
 fraction (sum of per-kernel lower bounds / measured time).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
+                       [--workloads vecop,gemm,conv,pool,graphs] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -358,13 +359,15 @@ def cpu_baseline(vec_bufs, extras: dict):
 
 
 def load_traffic(kernel: str):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC summary, if any."""
+    """Calibrated HBM bytes per launch of `kernel` (FETCH_SIZE + WRITE_SIZE, each scaled by
+    the factor the same counter reads for the copy kernel) from the committed PMC summary."""
     p = os.path.join(ROOT, "profiles", "hbm_traffic.json")
     try:
         with open(p) as f:
-            return json.load(f).get(kernel)
-    except (OSError, ValueError):
+            entry = json.load(f)["kernels"].get(kernel)
+    except (OSError, ValueError, KeyError):
         return None
+    return None if entry is None else entry.get("traffic_bytes")
 
 
 def main() -> int:
@@ -373,7 +376,13 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--quick", action="store_true", help="headline workload only, no CPU baseline")
+    ap.add_argument("--workloads", default="vecop,gemm,conv,pool,graphs",
+                    help="comma list of vecop (always run: the headline), gemm, conv, pool, graphs")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
+    work = set(args.workloads.split(","))
+    if args.quick:
+        work, args.no_cpu = {"vecop"}, True
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one MI355X; multi-GPU runs are not part of it "
               "(--gpus must be 1).", file=sys.stderr)
@@ -401,6 +410,15 @@ def main() -> int:
         ms = time_launches([vecop_call(bf)], max(args.steps, 10))
         gbs = vecop_bytes(bf["op"], wl.VECOP_N) / (ms * 1e-3) / 1e9
         per_op[bf["name"]] = dict(ms=round(ms, 5), gbs=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4))
+    # copy calibration: VectorOP's copy opcode (op >= 6 copies a) over the same 64 Mi
+    # elements -- the streaming ceiling at this size, and the PMC byte-count reference
+    from cormorant_amd import kernels as K
+    src = bufs[0]["a"]
+    dst = torch.empty_like(src)       # its own output: the sweep's outputs are checked later
+    copy_ms = time_launches([lambda: K.VectorOPKernel(src, None, dst, src.numel(), 6)],
+                            max(args.steps, 10))
+    del dst
+    copy_gbs = vecop_bytes(6, wl.VECOP_N) / (copy_ms * 1e-3) / 1e9
     kernel_ms = sum(v["ms"] for v in per_op.values())
     ms_per_step = wall * 1e3 / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
@@ -413,28 +431,38 @@ def main() -> int:
                     kernel=dom_kernel, op=dom_name,
                     bytes_per_launch=vecop_bytes(dom_op, wl.VECOP_N))
 
-    results = dict(vecop_ops=per_op, vecop_kernel_ms_per_step=round(kernel_ms, 5))
+    results = dict(vecop_ops=per_op, vecop_kernel_ms_per_step=round(kernel_ms, 5),
+                   vecop_copy_ceiling=dict(ms=round(copy_ms, 5), gbs=round(copy_gbs, 1),
+                                           hbm_frac=round(copy_gbs / HBM_PEAK_GBS, 4),
+                                           kernel="vecop_flat<6>", bytes_per_launch=vecop_bytes(6, wl.VECOP_N)))
     cpu = None
-    if not args.quick:
-        log("GEMM / conv / pool configurations")
-        extras = {}
+    extras, graphs = {}, {}
+    if "gemm" in work:
+        log("GEMM configurations")
         extras.update(bench_gemm(max(5, args.steps // 2), 2))
+    if "conv" in work:
+        log("convolution configurations")
         extras.update(bench_conv(max(5, args.steps // 2), 2))
+    if "pool" in work:
+        log("pool configurations")
         extras.update(bench_pool(max(args.steps, POOL_ROTATE), 2))
+    if "graphs" in work:
         log("scheduler graphs: MLP b64, MobileNetV2-like b16")
-        graphs = bench_graphs(max(5, args.steps // 2), 2, check=True)
+        graphs = bench_graphs(max(5, args.steps // 2), 2, check=not args.no_cpu)
+    cpu_res = {}
+    if not args.no_cpu:
         log("CPU baseline (oracle, 1 thread) and sample check")
         cpu_res = cpu_baseline(bufs, extras)
-        for name, e in extras.items():
-            e.pop("_dev", None)
-            if name in cpu_res:
-                e["cpu_1t"] = {k: (round(v, 4) if isinstance(v, float) else v)
-                               for k, v in cpu_res[name].items()}
-            results[name] = e
-        results.update(graphs)
         cpu = dict(value=round(cpu_res["vecop"]["gbs"], 3), unit="GB/s", cores=1, kind="port",
                    sample="the full six-op 64Mi-element sweep, oracle C restatement -O2, one thread",
                    seconds=round(cpu_res["vecop"]["seconds"], 3))
+    for name, e in extras.items():
+        e.pop("_dev", None)
+        if name in cpu_res:
+            e["cpu_1t"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                           for k, v in cpu_res[name].items()}
+        results[name] = e
+    results.update(graphs)
 
     line = {
         "metric": METRIC,
