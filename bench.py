@@ -249,7 +249,8 @@ def bench_graphs(steps: int, warmup: int, check: bool):
                     (1 if c.args[16] else c.args[1]) * c.args[7] * c.args[8]
                     for _, c in sess.plan.calls if c.kernel == "conv")
         lb = graph_lower_bound_s(sess.plan)
-        e = dict(kernel_calls=len(sess.plan.calls), gmac=round(macs / 1e9, 4),
+        e = dict(kernel_calls=len(sess.plan.calls), launches=len(sess.launch_list),
+                 gmac=round(macs / 1e9, 4),
                  ms=round(ms, 4), ms_hip_graph=round(ms_graph, 4),
                  images_s=round(batch / (ms * 1e-3), 1),
                  images_s_hip_graph=round(batch / (ms_graph * 1e-3), 1),

@@ -19,7 +19,7 @@ EXPORTS = (
     "cm_buf_dev", "cm_buf_count", "cm_buf_init_view", "cm_buf_sync_to_device",
     "cm_buf_sync_from_device", "cm_run_op", "cm_run_matmul", "cm_run_matmul_at", "cm_run_conv",
     "cm_run_pool", "cm_set_stream", "cm_get_stream", "cm_sync", "cm_last_error", "cm_version",
-    "cm_selftest_div", "cm_selftest_finalize",
+    "cm_selftest_div", "cm_selftest_finalize", "cm_matmul_ex", "cm_conv_ex",
 )
 
 CM_OK = 0
@@ -27,6 +27,10 @@ CM_ERR_INVALID = -1
 CM_ERR_HIP = -2
 CM_ERR_RANGE = -3
 CM_ERR_NOMEM = -4
+
+# cm_epilogue_t add_mode / act
+CM_EPI_ADD_NONE, CM_EPI_ADD_SAME, CM_EPI_ADD_COLUMN = 0, 1, 2
+CM_EPI_ACT_NONE, CM_EPI_ACT_RELU, CM_EPI_ACT_RELU6 = 0, 1, 2
 
 
 class NativeLibraryError(RuntimeError):
@@ -49,6 +53,15 @@ class CmBuf(ctypes.Structure):
         ("dev", ctypes.c_void_p),
         ("count", ctypes.c_uint32),
         ("is_owner", ctypes.c_uint8),
+    ]
+
+
+class CmEpilogue(ctypes.Structure):
+    """Mirror of cm_epilogue_t (include/cormorant_amd.h)."""
+    _fields_ = [
+        ("add", ctypes.c_void_p),
+        ("add_mode", ctypes.c_uint32),
+        ("act", ctypes.c_uint32),
     ]
 
 
@@ -86,6 +99,8 @@ _SIGS = {
     "cm_selftest_div": (_i, [_u32, _u32, ctypes.POINTER(ctypes.c_uint64),
                                 ctypes.POINTER(ctypes.c_uint64), _vp]),
     "cm_selftest_finalize": (_i, [_u32, _u32, _u32, _u32, ctypes.POINTER(ctypes.c_uint64), _vp]),
+    "cm_matmul_ex": (_i, [_vp, _vp, _vp] + [_u32] * 7 + [ctypes.POINTER(CmEpilogue), _vp]),
+    "cm_conv_ex": (_i, [_vp, _vp, _vp, _vp] + [_u32] * 17 + [ctypes.POINTER(CmEpilogue), _vp]),
 }
 
 _lib = None

@@ -35,6 +35,18 @@ bool fits(const cm_buf_t* b, uint64_t off, uint64_t need, const char* fn, const 
     return false;
 }
 
+// add_mode / act in range, add present when used, column adds only for MatMul.
+int check_epilogue(const cm_epilogue_t* e, bool column_ok, const char* fn) {
+    if (!e) return CM_OK;
+    if (e->add_mode > CM_EPI_ADD_COLUMN || (e->add_mode == CM_EPI_ADD_COLUMN && !column_ok))
+        return cm_set_error(CM_ERR_INVALID, "%s: unsupported epilogue add_mode %u", fn, e->add_mode);
+    if (e->act > CM_EPI_ACT_RELU6)
+        return cm_set_error(CM_ERR_INVALID, "%s: unsupported epilogue act %u", fn, e->act);
+    if (e->add_mode != CM_EPI_ADD_NONE && !e->add)
+        return cm_set_error(CM_ERR_INVALID, "%s: epilogue add_mode %u with null add", fn, e->add_mode);
+    return CM_OK;
+}
+
 }  // namespace
 
 int cm_set_error(int code, const char* fmt, ...) {
@@ -82,12 +94,21 @@ int cm_vectorop(const int16_t* a, const int16_t* b, int16_t* c, uint32_t size, u
     return cm_vectorop_launch(a, b, c, size, op, outer, a_inc, b_inc, pick(stream));
 }
 
+int cm_matmul_ex(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
+                 uint32_t m, uint32_t batch, uint32_t a_stride, uint32_t b_stride,
+                 uint32_t c_stride, const cm_epilogue_t* epi, hipStream_t stream) {
+    if (batch == 0 || n == 0 || m == 0) return CM_OK;
+    if (!c || (k > 0 && (!a || !b))) return cm_set_error(CM_ERR_INVALID, "matmul: null pointer");
+    const int rc = check_epilogue(epi, true, "matmul");
+    if (rc) return rc;
+    return cm_matmul_launch(a, b, c, n, k, m, batch, a_stride, b_stride, c_stride, epi,
+                            pick(stream));
+}
+
 int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
               uint32_t m, uint32_t batch, uint32_t a_stride, uint32_t b_stride,
               uint32_t c_stride, hipStream_t stream) {
-    if (batch == 0 || n == 0 || m == 0) return CM_OK;
-    if (!c || (k > 0 && (!a || !b))) return cm_set_error(CM_ERR_INVALID, "matmul: null pointer");
-    return cm_matmul_launch(a, b, c, n, k, m, batch, a_stride, b_stride, c_stride, pick(stream));
+    return cm_matmul_ex(a, b, c, n, k, m, batch, a_stride, b_stride, c_stride, nullptr, stream);
 }
 
 int cm_matmul_at(const int16_t* a, uint32_t a_off, const int16_t* b, uint32_t b_off,
@@ -99,19 +120,32 @@ int cm_matmul_at(const int16_t* a, uint32_t a_off, const int16_t* b, uint32_t b_
                      c_stride, stream);
 }
 
-int cm_conv(const int16_t* x, const int16_t* weight, const int16_t* bias, int16_t* y,
-            uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
-            uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
-            uint32_t stride_w, uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
-            uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise, hipStream_t stream) {
+int cm_conv_ex(const int16_t* x, const int16_t* weight, const int16_t* bias, int16_t* y,
+               uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
+               uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
+               uint32_t stride_w, uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
+               uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise,
+               const cm_epilogue_t* epi, hipStream_t stream) {
     if ((uint64_t)batch * out_ch * out_h * out_w == 0) return CM_OK;
     if (!x || !weight || !y) return cm_set_error(CM_ERR_INVALID, "conv: null x, weight or y");
     if (has_bias && !bias) return cm_set_error(CM_ERR_INVALID, "conv: has_bias with null bias");
     if (is_depthwise && out_ch > in_ch)
         return cm_set_error(CM_ERR_INVALID, "conv: depthwise needs out_ch (%u) <= in_ch (%u)", out_ch, in_ch);
+    const int rc = check_epilogue(epi, false, "conv");
+    if (rc) return rc;
     return cm_conv_launch(x, weight, bias, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh,
                           kw, stride_h, stride_w, dilation_h, dilation_w, pad_top, pad_left,
-                          has_bias, is_depthwise, pick(stream));
+                          has_bias, is_depthwise, epi, pick(stream));
+}
+
+int cm_conv(const int16_t* x, const int16_t* weight, const int16_t* bias, int16_t* y,
+            uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
+            uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
+            uint32_t stride_w, uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
+            uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise, hipStream_t stream) {
+    return cm_conv_ex(x, weight, bias, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw,
+                      stride_h, stride_w, dilation_h, dilation_w, pad_top, pad_left, has_bias,
+                      is_depthwise, nullptr, stream);
 }
 
 int cm_pool(const int16_t* x, int16_t* y, uint32_t batch, uint32_t channels, uint32_t in_h,

@@ -18,6 +18,16 @@ enum {
 
 
 int cm_set_error(int code, const char* fmt, ...);
+
+// Epilogue of a MatMul / Conv launch, flattened for kernel arguments:
+// add_mode / act as in cm_epilogue_t (0 = none).
+struct EpiArgs {
+    const int16_t* add;
+    uint32_t add_mode, act;
+};
+inline EpiArgs cm_epi_args(const cm_epilogue_t* e) {
+    return e ? EpiArgs{e->add, e->add_mode, e->act} : EpiArgs{nullptr, 0u, 0u};
+}
 int cm_check_launch(const char* what);
 
 inline uint64_t cm_grid_blocks(uint64_t work, uint32_t threads, uint64_t cap = 1u << 20) {
@@ -40,9 +50,10 @@ int cm_finalize_sweep_launch(uint32_t mode, uint32_t lo, uint32_t count, uint32_
                              unsigned long long* checksum, hipStream_t s);
 int cm_matmul_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
                      uint32_t m, uint32_t batch, uint32_t a_bs, uint32_t b_bs, uint32_t c_bs,
-                     hipStream_t s);
+                     const cm_epilogue_t* epi, hipStream_t s);
 int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
                    uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
                    uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
                    uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
-                   uint32_t pad_left, uint32_t has_bias, uint32_t is_dw, hipStream_t s);
+                   uint32_t pad_left, uint32_t has_bias, uint32_t is_dw, const cm_epilogue_t* epi,
+                   hipStream_t s);

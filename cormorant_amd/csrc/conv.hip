@@ -7,7 +7,8 @@
 //     straight from NCHW x while the B tile is built (no im2col buffer);
 //   * depthwise (is_depthwise = 1, weights [out_ch][1][kh][kw]): direct kernel,
 //     one thread per output, uint32 wrapping accumulator (ConvKernel.cpp:251-319).
-// All paths: acc = wrap32((has_bias ? bias << 8 : 0) + sum x*w), y = sat16(acc >> 8).
+// All paths: acc = wrap32((has_bias ? bias << 8 : 0) + sum x*w), y = sat16(acc >> 8),
+// then the optional fused epilogue (Add of a same-shaped tensor, Relu / Relu6).
 #include "cm_internal.h"
 #include "q88.h"
 
@@ -15,10 +16,10 @@ int cm_conv_gemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias,
                         uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
                         uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
                         uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
-                        uint32_t pad_left, hipStream_t s);
+                        uint32_t pad_left, const cm_epilogue_t* epi, hipStream_t s);
 int cm_conv_pointwise_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
                              uint32_t batch, uint32_t in_ch, uint32_t out_ch, uint32_t hw,
-                             hipStream_t s);
+                             const cm_epilogue_t* epi, hipStream_t s);
 
 namespace {
 
@@ -34,7 +35,7 @@ __global__ __launch_bounds__(kThreads) void conv_depthwise(const int16_t* __rest
                                                            const int16_t* __restrict__ w,
                                                            const int16_t* __restrict__ bias,
                                                            int16_t* __restrict__ y, DwGeom g,
-                                                           uint64_t total) {
+                                                           uint64_t total, EpiArgs epi) {
     const uint64_t stride = (uint64_t)gridDim.x * kThreads;
     const uint64_t ohw = (uint64_t)g.out_h * g.out_w;
     for (uint64_t o = (uint64_t)blockIdx.x * kThreads + threadIdx.x; o < total; o += stride) {
@@ -56,7 +57,9 @@ __global__ __launch_bounds__(kThreads) void conv_depthwise(const int16_t* __rest
                 acc += (uint32_t)((int32_t)xc[(uint64_t)ih * g.in_w + iw] * (int32_t)wm[khi * g.kw + kwi]);
             }
         }
-        y[o] = q88::acc_to_data(acc);
+        int32_t v = q88::acc_to_data(acc);
+        if (epi.add_mode == 1u) v = q88::add(v, epi.add[o]);
+        y[o] = (int16_t)q88::epi_act(v, epi.act);
     }
 }
 
@@ -66,20 +69,22 @@ int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int1
                    uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
                    uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
                    uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
-                   uint32_t pad_left, uint32_t has_bias, uint32_t is_dw, hipStream_t s) {
+                   uint32_t pad_left, uint32_t has_bias, uint32_t is_dw, const cm_epilogue_t* epi,
+                   hipStream_t s) {
     const int16_t* b = has_bias ? bias : nullptr;
+    const EpiArgs ea = cm_epi_args(epi);
     if (is_dw) {
         const uint64_t total = (uint64_t)batch * out_ch * out_h * out_w;
         if (total == 0) return CM_OK;
         DwGeom g{in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, sh, sw, dh, dw, pad_top, pad_left};
         const dim3 grid((uint32_t)cm_grid_blocks(total, kThreads));
-        if (b) hipLaunchKernelGGL(conv_depthwise<true>, grid, dim3(kThreads), 0, s, x, w, b, y, g, total);
-        else hipLaunchKernelGGL(conv_depthwise<false>, grid, dim3(kThreads), 0, s, x, w, b, y, g, total);
+        if (b) hipLaunchKernelGGL(conv_depthwise<true>, grid, dim3(kThreads), 0, s, x, w, b, y, g, total, ea);
+        else hipLaunchKernelGGL(conv_depthwise<false>, grid, dim3(kThreads), 0, s, x, w, b, y, g, total, ea);
         return cm_check_launch("conv_depthwise");
     }
     if (kh == 1 && kw == 1 && sh == 1 && sw == 1 && pad_top == 0 && pad_left == 0 &&
         out_h == in_h && out_w == in_w && (uint64_t)in_h * in_w <= 0x7FFFFFFFull)
-        return cm_conv_pointwise_launch(x, w, b, y, batch, in_ch, out_ch, in_h * in_w, s);
+        return cm_conv_pointwise_launch(x, w, b, y, batch, in_ch, out_ch, in_h * in_w, epi, s);
     return cm_conv_gemm_launch(x, w, b, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw,
-                               sh, sw, dh, dw, pad_top, pad_left, s);
+                               sh, sw, dh, dw, pad_top, pad_left, epi, s);
 }

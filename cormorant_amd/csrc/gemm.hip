@@ -44,6 +44,7 @@ constexpr int kThreads = 512;
 constexpr int kStride = 80;          // LDS bytes per row of 64 int8 (k) values
 constexpr int kFoldIters = 512;      // fold MFMA partials every 512*64 = 32768 k
 constexpr int TI = 4, TJ = 2;        // MFMA tiles per wave: 4 row tiles x 2 column tiles
+constexpr uint32_t kTabMax = 2048;   // largest K of the table-driven convolution gather
 
 struct GemmArgs {
     const int16_t* a;     // [rows][k], row stride lda (weights for conv)
@@ -58,6 +59,7 @@ struct GemmArgs {
     uint32_t C, H, W, OW, P, kh, kw, sh, sw, dh, dw, pt, pl;
     uint64_t x_img, y_img;
     uint32_t x_bytes;            // table mode: size of the whole input tensor, < 2^31
+    EpiArgs epi;                 // fused Add / Relu / Clip; add_mode 1 follows C's layout
 };
 
 // Raw buffer resource word 3 for gfx950 (32-bit data, no swizzle): loads past
@@ -102,6 +104,7 @@ struct Smem {
     Planes st[2];
     uint32_t row_sum[BM];
     uint32_t col_sum[BN];
+    int32_t bias[BM];      // bias << 8 of the block's rows (0 past the last row)
 };
 
 // Splits 16 int16 values (8 packed words, k order) into 16 high and 16 low
@@ -309,6 +312,7 @@ struct ConvBTile {
     int32_t ih0, iw0;    // window origin of this thread's output pixel
     int32_t pbase;       // ih0 * W + iw0 (may be negative; only valid taps are read)
     int32_t pbyte;       // byte offset of the window origin from the tensor start
+    uint32_t holes;      // table mode: bit r set iff tap r of the window lies outside the image
     bool col_ok;
 
     __device__ __forceinline__ void init(const GemmArgs& g, uint32_t col0) {
@@ -317,28 +321,44 @@ struct ConvBTile {
         const uint32_t n = col_ok ? col / g.P : 0;
         const uint32_t p = col_ok ? col - n * g.P : 0;
         const uint32_t oh = p / g.OW, ow = p - (p / g.OW) * g.OW;
-        ih0 = (int32_t)(oh * g.sh) - (int32_t)g.pt;
+        // a column past the end gets a window origin no tap can reach, so the
+        // per-tap bounds test alone rejects it (a separate lane-varying test
+        // would let the compiler branch around the gather and serialise it)
+        ih0 = col_ok ? (int32_t)(oh * g.sh) - (int32_t)g.pt : 0x40000000;
         iw0 = (int32_t)(ow * g.sw) - (int32_t)g.pl;
         pbase = ih0 * (int32_t)g.W + iw0;
         pbyte = (int32_t)(2 * ((int64_t)n * (int64_t)g.x_img + pbase));
         xb = g.b + (uint64_t)n * g.x_img;
     }
-    // Gather through the per-block k table tab[k] = {2*(c*H*W + dy*W + dx), dy << 16 | dx}
-    // (dy = khi*dh, dx = kwi*dw) with buffer loads over the whole input tensor
-    // (fewer than 2^31 bytes): an invalid tap gets offset kOob, past the
-    // buffer's size, and the hardware returns 0 for it.
+    // Table mode (kh*kw <= 31): which of the window's taps r = khi*kw + kwi lie
+    // outside the image (bit 31, the tap of every k >= K, is always set).
+    __device__ __forceinline__ void init_taps(const GemmArgs& g) {
+        uint32_t taps = 0;
+        uint32_t khi = 0, kwi = 0;
+        for (uint32_t r = 0; r < g.kh * g.kw; ++r) {
+            const uint32_t ih = (uint32_t)(ih0 + (int32_t)(khi * g.dh));
+            const uint32_t iw = (uint32_t)(iw0 + (int32_t)(kwi * g.dw));
+            taps |= (ih < g.H && iw < g.W) ? 1u << r : 0u;
+            if (++kwi == g.kw) { kwi = 0; ++khi; }
+        }
+        holes = ~taps;
+    }
+    // Gather through the per-block k table tab[k] = {2*(c*H*W + khi*dh*W + kwi*dw), tap r}
+    // with buffer loads over the whole input tensor (fewer than 2^31 bytes):
+    // the offset of a tap outside the image gets bit 31 set (its hole bit,
+    // shifted), which puts it past the buffer's size, and the hardware returns
+    // 0.  Three VALU operations per value, and no select the compiler could
+    // turn into a branch around the table read.
     __device__ __forceinline__ void load_tab(const GemmArgs& g, uint32_t k0, const int2* tab,
                                              __amdgpu_buffer_rsrc_t rsrc) {
+        // the table covers every k the loop loads, also past K (tap 31: never valid)
         const uint32_t ks = __builtin_amdgcn_readfirstlane(k0 + (threadIdx.x >> 7) * 16);
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            // k < kTabMax always (the padded k range of a K <= kTabMax problem);
-            // entries past g.k are never used.
-            const uint32_t k = ks + j;
-            const int2 t = tab[k];
-            const int32_t ih = ih0 + (t.y >> 16), iw = iw0 + (t.y & 0xFFFF);
-            const bool ok = col_ok && k < g.k && (uint32_t)ih < g.H && (uint32_t)iw < g.W;
-            raw[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, ok ? (uint32_t)(pbyte + t.x) : kOob, 0, 0);
+            const int2 t = tab[ks + j];
+            const uint32_t hole = __builtin_amdgcn_ubfe(holes, (uint32_t)t.y, 1u);
+            const uint32_t off = (hole << 31) | (uint32_t)(pbyte + t.x);
+            raw[j] = __builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, 0);
         }
     }
     // Gather for any size: k decomposed incrementally, global loads of a valid
@@ -355,8 +375,7 @@ struct ConvBTile {
         for (int j = 0; j < 16; ++j) {
             const int32_t ih = ih0 + (int32_t)(khi * g.dh);
             const int32_t iw = iw0 + (int32_t)(kwi * g.dw);
-            const bool ok = col_ok && ks + j < g.k && ih >= 0 && ih < (int32_t)g.H && iw >= 0 &&
-                            iw < (int32_t)g.W;
+            const bool ok = ks + j < g.k && (uint32_t)ih < g.H && (uint32_t)iw < g.W;
             const int16_t x = xb[ok ? (uint64_t)c * hw + (uint32_t)ih * g.W + (uint32_t)iw : 0u];
             raw[j] = ok ? (uint32_t)(uint16_t)x : 0u;
             if (++kwi == g.kw) {
@@ -374,9 +393,9 @@ struct ConvBTile {
 };
 
 // B-operand modes: dense matrix, implicit-GEMM gather with an LDS k table
-// (K <= kTabMax), implicit-GEMM gather with incremental k decomposition.
+// (K + 2 steps <= kTabMax, at most 31 taps), implicit-GEMM gather with
+// incremental k decomposition (any size).
 enum { B_DENSE = 0, B_CONV_TAB = 1, B_CONV_INC = 2 };
-constexpr uint32_t kTabMax = 2048;
 
 // AV / BV: 0 = vector loads chosen at run time (g.a_vec / g.b_vec, global
 // loads), 1 = vector buffer loads, 2 = element buffer loads.  Fixing the path
@@ -396,15 +415,22 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     const int16_t* bbase = g.b + (CONV ? 0 : (uint64_t)blockIdx.z * g.b_bs);
 
     if (threadIdx.x < BN) s.col_sum[threadIdx.x] = 0;   // published with atomics at the end
+    if (HAS_BIAS && threadIdx.x < BM) {
+        const uint32_t r = row0 + threadIdx.x;
+        s.bias[threadIdx.x] = r < g.rows ? (int32_t)g.bias[r] * 256 : 0;
+    }
     const int2* tab = nullptr;
     if constexpr (MODE == B_CONV_TAB) {
+        // one entry per k the main loop loads: its k steps plus the two past
+        // the end (the host keeps that below kTabMax); k >= K gets tap 31
         __shared__ int2 ktab[kTabMax];
         const uint32_t kk = g.kh * g.kw, hw = g.H * g.W;
-        for (uint32_t k = threadIdx.x; k < g.k; k += kThreads) {
+        const uint32_t kend = ((g.k + BK - 1) / BK + 2) * BK;
+        for (uint32_t k = threadIdx.x; k < kend; k += kThreads) {
             const uint32_t c = k / kk, r = k - (k / kk) * kk;
             const uint32_t khi = r / g.kw, kwi = r - (r / g.kw) * g.kw;
             const uint32_t dy = khi * g.dh, dx = kwi * g.dw;
-            ktab[k] = int2{(int)(2 * (c * hw + dy * g.W + dx)), (int)((dy << 16) | dx)};
+            ktab[k] = k < g.k ? int2{(int)(2 * (c * hw + dy * g.W + dx)), (int)r} : int2{0, 31};
         }
         tab = ktab;
     }
@@ -421,7 +447,8 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     int32_t chs = 0, cls = 0;
     if constexpr (CONV) {
         bt[0].init(g, col0);
-        bt[1].init(g, col0);
+        if constexpr (MODE == B_CONV_TAB) bt[0].init_taps(g);
+        bt[1] = bt[0];
     }
     const __amdgpu_buffer_rsrc_t xrsrc = make_rsrc(g.b, g.x_bytes);   // table mode only
     const uint32_t arows = g.rows - row0 < (uint32_t)BM ? g.rows - row0 : (uint32_t)BM;
@@ -445,11 +472,13 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
         } else if constexpr (MODE == B_CONV_INC) {
             b.load(g, k0);
         } else if constexpr (BUF) {
-            const uint32_t kr = g.k - k0 < (uint32_t)BK ? g.k - k0 : (uint32_t)BK;
+            // k0 may lie past the last step (see the main loop): an empty resource
+            const uint32_t kr = k0 >= g.k ? 0u : (g.k - k0 < (uint32_t)BK ? g.k - k0 : (uint32_t)BK);
             const uint32_t cr = g.cols - col0 < (uint32_t)BN ? g.cols - col0 : (uint32_t)BN;
-            b.template load_buf<BV == 1>(g, make_rsrc(bbase + (uint64_t)k0 * g.ldb + col0,
-                                                      ((kr - 1) * (uint32_t)g.ldb + cr) * 2u),
-                                         col0, k0);
+            b.template load_buf<BV == 1>(
+                g, make_rsrc(bbase + (uint64_t)(kr ? k0 : 0u) * g.ldb + col0,
+                             kr ? ((kr - 1) * (uint32_t)g.ldb + cr) * 2u : 0u),
+                col0, k0);
         } else {
             b.load(g, bbase, col0, k0);
         }
@@ -535,26 +564,34 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
 
     const uint32_t nk = (g.k + BK - 1) / BK;
     load_tile(at[0], bt[0], 0);
-    if (nk > 1) load_tile(at[1], bt[1], BK);
+    load_tile(at[1], bt[1], BK);
     stage_tile(at[0], bt[0], s.st[0], true);
     __syncthreads();
-    // Step it computes on planes it%2; register set it%2 is free (its tile was
-    // staged one step earlier) and receives step it+2; set (it+1)%2 holds step
-    // it+1 and is staged into planes (it+1)%2.  The loop is unrolled by two so
-    // every register set and plane index is static.
-    for (uint32_t it = 0; it < nk; it += 2) {
-        if (it + 2 < nk) load_tile(at[0], bt[0], (it + 2) * BK);
+    // Steps go in pairs (it, it + 1).  Step it computes on planes 0 while the
+    // loads of step it+2 fly into register set 0 (free: its tile was staged one
+    // step earlier) and set 1 (step it+1) is split into planes 1; step it+1 is
+    // the mirror image.  Loads are issued on every path, also for the (all
+    // zero, out-of-range) steps past the last one, and the loop has no exit but
+    // its end: a path that skips loads or leaves the loop mid-body makes the
+    // compiler's wait before each split count the just-issued loads too, which
+    // exposes their full latency every step.  An odd last step runs after the
+    // loop from planes 0.
+    uint32_t it = 0;
+    for (; it + 2 <= nk; it += 2) {
+        load_tile(at[0], bt[0], (it + 2) * BK);
+        __builtin_amdgcn_sched_barrier(0);   // keep the loads ahead of this step's work
         mfma_step(s.st[0], it);
-        stage_tile(at[1], bt[1], s.st[1], it + 1 < nk);
+        stage_tile(at[1], bt[1], s.st[1], true);
         interleave();
         __syncthreads();
-        if (it + 1 >= nk) break;
-        if (it + 3 < nk) load_tile(at[1], bt[1], (it + 3) * BK);
+        load_tile(at[1], bt[1], (it + 3) * BK);
+        __builtin_amdgcn_sched_barrier(0);
         mfma_step(s.st[1], it + 1);
         stage_tile(at[0], bt[0], s.st[0], it + 2 < nk);
         interleave();
         __syncthreads();
     }
+    if (it < nk) mfma_step(s.st[0], it);
 
     // row sums (sum a = 256*hs + ls + 128*count); the four threads of a row are
     // adjacent lanes, each stored 16 k values per step
@@ -568,13 +605,17 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
         publish_dense(s, dhs, dls, 4u * nk);
     __syncthreads();
 
+    // Epilogue: every value is computed, and every residual read issued, without
+    // a lane-dependent branch (out-of-range outputs read element 0 of the Add
+    // tensor and are not stored), so the reads are all in flight together.
     const uint32_t kp_term = 16384u * (nk * (uint32_t)BK);
     int16_t* cptr = g.c + (CONV ? 0 : (uint64_t)blockIdx.z * g.c_bs);
+    const int16_t* rptr = g.epi.add + (CONV ? 0 : (uint64_t)blockIdx.z * g.c_bs);
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
         const uint32_t cl = wcol + j * 16 + (lane & 15);
         const uint32_t col = col0 + cl;
-        if (col >= g.cols) continue;
+        const bool cok = col < g.cols;
         uint64_t coff;
         uint64_t rstride;
         if constexpr (CONV) {
@@ -586,21 +627,41 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
             rstride = g.ldc;
         }
         const uint32_t csum = s.col_sum[cl];
+        int32_t yv[TI][4];
+        uint64_t ov[TI][4];
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const uint32_t rl = wrow + i * 16 + (lane >> 4) * 4 + e;
-                const uint32_t row = row0 + rl;
-                if (row >= g.rows) continue;
+                const bool ok = cok && row0 + rl < g.rows;
                 uint32_t v = ((uint32_t)hh[i][j][e] << 16) + ((uint32_t)mid[i][j][e] << 8) +
                              (uint32_t)ll[i][j][e];
                 if constexpr (FOLD) v += (uint32_t)tot[i][j][e];
                 v += 128u * (s.row_sum[rl] + csum) - kp_term;
-                if constexpr (HAS_BIAS) v += (uint32_t)(int32_t)g.bias[row] << 8;
-                cptr[coff + (uint64_t)row * rstride] = q88::acc_to_data(v);
+                if constexpr (HAS_BIAS) v += (uint32_t)s.bias[rl];
+                ov[i][e] = ok ? coff + (uint64_t)(row0 + rl) * rstride : ~0ull;
+                yv[i][e] = q88::acc_to_data(v);
             }
         }
+        if (g.epi.add_mode == 1u) {
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    yv[i][e] = q88::add(yv[i][e], rptr[ov[i][e] == ~0ull ? 0 : ov[i][e]]);
+        } else if (g.epi.add_mode == 2u) {
+            const int32_t b = g.epi.add[cok ? col : 0u];
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) yv[i][e] = q88::add(yv[i][e], b);
+        }
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                if (ov[i][e] != ~0ull) cptr[ov[i][e]] = (int16_t)q88::epi_act(yv[i][e], g.epi.act);
     }
 }
 
@@ -647,10 +708,11 @@ int launch_gemm(GemmArgs& g, uint32_t zdim, hipStream_t s, const char* name) {
 
 int cm_matmul_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
                      uint32_t m, uint32_t batch, uint32_t a_bs, uint32_t b_bs, uint32_t c_bs,
-                     hipStream_t s) {
+                     const cm_epilogue_t* epi, hipStream_t s) {
     if (batch == 0 || n == 0 || m == 0) return CM_OK;
     GemmArgs g{};
     g.a = a; g.b = b; g.c = c; g.bias = nullptr;
+    g.epi = cm_epi_args(epi);
     g.rows = n; g.cols = m; g.k = k;
     g.lda = k; g.ldb = m; g.ldc = m;
     g.a_bs = a_bs; g.b_bs = b_bs; g.c_bs = c_bs;
@@ -671,6 +733,7 @@ int cm_matmul_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n,
         gz.a = g.a + (uint64_t)done * a_bs;
         gz.b = g.b + (uint64_t)done * b_bs;
         gz.c = g.c + (uint64_t)done * c_bs;
+        if (g.epi.add_mode == 1u) gz.epi.add = g.epi.add + (uint64_t)done * c_bs;
         const int rc = launch_gemm<B_DENSE>(gz, z, s, "matmul");
         if (rc) return rc;
         done += z;
@@ -682,7 +745,7 @@ int cm_conv_gemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias,
                         uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
                         uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
                         uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
-                        uint32_t pad_left, hipStream_t s) {
+                        uint32_t pad_left, const cm_epilogue_t* epi, hipStream_t s) {
     const uint64_t P = (uint64_t)out_h * out_w;
     const uint64_t K = (uint64_t)in_ch * kh * kw;
     const uint64_t cols = P * batch;
@@ -692,6 +755,7 @@ int cm_conv_gemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias,
         return cm_set_error(CM_ERR_RANGE, "conv: shape exceeds 32-bit indexing");
     GemmArgs g{};
     g.a = w; g.b = x; g.c = y; g.bias = bias;
+    g.epi = cm_epi_args(epi);
     g.rows = out_ch; g.cols = (uint32_t)cols; g.k = (uint32_t)K;
     g.lda = K;
     g.a_vec = aligned(w, 16) && K % 8 == 0;
@@ -700,22 +764,25 @@ int cm_conv_gemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias,
     g.kh = kh; g.kw = kw; g.sh = sh; g.sw = sw; g.dh = dh; g.dw = dw; g.pt = pad_top; g.pl = pad_left;
     g.x_img = x_img;
     g.y_img = (uint64_t)out_ch * P;
-    // the k table holds byte offsets < 2^31 and dy, dx < 2^16
     const uint64_t x_bytes = 2 * x_img * batch;
     g.x_bytes = (uint32_t)(x_bytes < 0x80000000ull ? x_bytes : 0);
-    const bool table = K <= kTabMax && (uint64_t)(kh - 1) * dh < 65536u &&
-                       (uint64_t)(kw - 1) * dw < 65536u && x_bytes < 0x80000000ull;
+    // table mode: at most 31 taps (one bit each), byte offsets of the window
+    // below 2^31
+    const bool table = ((K + BK - 1) / BK + 2) * BK <= kTabMax && (uint64_t)kh * kw <= 31u &&
+                       x_bytes < 0x80000000ull &&
+                       ((uint64_t)(kh - 1) * dh * in_w + (uint64_t)(kw - 1) * dw) < (1ull << 29);
     if (table) return launch_gemm<B_CONV_TAB>(g, 1, s, "conv_gemm");
     return launch_gemm<B_CONV_INC>(g, 1, s, "conv_gemm");
 }
 
 int cm_conv_pointwise_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
                              uint32_t batch, uint32_t in_ch, uint32_t out_ch, uint32_t hw,
-                             hipStream_t s) {
+                             const cm_epilogue_t* epi, hipStream_t s) {
     // 1x1, stride 1, no padding: y[n] = W[out_ch][in_ch] x X[n][in_ch][hw] (+ bias)
     if (batch == 0 || out_ch == 0 || hw == 0) return CM_OK;
     GemmArgs g{};
     g.a = w; g.b = x; g.c = y; g.bias = bias;
+    g.epi = cm_epi_args(epi);
     g.rows = out_ch; g.cols = hw; g.k = in_ch;
     g.lda = in_ch; g.ldb = hw; g.ldc = hw;
     g.a_bs = 0; g.b_bs = (uint64_t)in_ch * hw; g.c_bs = (uint64_t)out_ch * hw;
@@ -727,6 +794,7 @@ int cm_conv_pointwise_launch(const int16_t* x, const int16_t* w, const int16_t* 
         GemmArgs gz = g;
         gz.b = x + (uint64_t)done * g.b_bs;
         gz.c = y + (uint64_t)done * g.c_bs;
+        if (g.epi.add_mode == 1u) gz.epi.add = g.epi.add + (uint64_t)done * g.c_bs;
         const int rc = launch_gemm<B_DENSE>(gz, z, s, "conv_pointwise");
         if (rc) return rc;
         done += z;

@@ -70,6 +70,11 @@ __device__ __forceinline__ int32_t relu6(int32_t a) {
     return a < 0 ? 0 : (a > 1536 ? 1536 : a);
 }
 
+// Fused epilogue activation (cm_epilogue_t act): 1 = RELU, 2 = RELU6, else none.
+__device__ __forceinline__ int32_t epi_act(int32_t y, uint32_t act) {
+    return act == 1u ? relu(y) : (act == 2u ? relu6(y) : y);
+}
+
 // (float)AccData_t: nearest-even rounding of raw, then exact scale by 2^-16.
 __device__ __forceinline__ float acc_to_float(uint32_t acc) {
     return mul_rn((float)(int32_t)acc, 1.0f / 65536.0f);   // v_cvt_f32_i32 rounds to nearest even

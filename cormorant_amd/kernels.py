@@ -64,9 +64,30 @@ def VectorOPKernel(a, b, c, size, op, outer=1, a_inc=0, b_inc=0, stream=None) ->
     _native.call("cm_vectorop", pa, pb, pc, size, op, outer, a_inc, b_inc, _stream(stream))
 
 
+ACT_NONE, ACT_RELU, ACT_RELU6 = 0, 1, 2
+
+
+def _epilogue(add, column: bool, act: int, need: int):
+    """cm_epilogue_t for a fused Add (same layout as the output, or one value per
+    output column) and activation; None when neither is requested."""
+    if add is None and not act:
+        return None
+    if act not in (ACT_NONE, ACT_RELU, ACT_RELU6):
+        raise ValueError(f"act={act} is not ACT_NONE / ACT_RELU / ACT_RELU6")
+    e = _native.CmEpilogue()
+    e.act = act
+    if add is not None:
+        e.add = _dev_ptr(add, need, "add")
+        e.add_mode = _native.CM_EPI_ADD_COLUMN if column else _native.CM_EPI_ADD_SAME
+    return e
+
+
 def MatmulKernel(a, b, c, n, k, m, batch=1, a_batch_stride=0, b_batch_stride=0,
-                 c_batch_stride=0, stream=None) -> None:
-    """C_bi = sat16(wrap32(A_bi @ B_bi) >> 8), A_bi = a + bi*a_batch_stride, ..."""
+                 c_batch_stride=0, stream=None, add=None, add_column=False, act=ACT_NONE) -> None:
+    """C_bi = sat16(wrap32(A_bi @ B_bi) >> 8), A_bi = a + bi*a_batch_stride, ...
+
+    Optional fused epilogue: C = act(sat16(C + add)) with `add` laid out like C
+    (or, with add_column, one value per column j), act = ACT_RELU / ACT_RELU6."""
     n, k, m, batch = (_u32(x, v) for x, v in (("n", n), ("k", k), ("m", m), ("batch", batch)))
     a_bs, b_bs, c_bs = (_u32(x, v) for x, v in (("a_batch_stride", a_batch_stride),
                                                   ("b_batch_stride", b_batch_stride),
@@ -76,13 +97,20 @@ def MatmulKernel(a, b, c, n, k, m, batch=1, a_batch_stride=0, b_batch_stride=0,
     pa = _dev_ptr(a, (batch - 1) * a_bs + n * k, "a")
     pb = _dev_ptr(b, (batch - 1) * b_bs + k * m, "b")
     pc = _dev_ptr(c, (batch - 1) * c_bs + n * m, "c")
-    _native.call("cm_matmul", pa, pb, pc, n, k, m, batch, a_bs, b_bs, c_bs, _stream(stream))
+    epi = _epilogue(add, add_column, act, m if add_column else (batch - 1) * c_bs + n * m)
+    if epi is None:
+        _native.call("cm_matmul", pa, pb, pc, n, k, m, batch, a_bs, b_bs, c_bs, _stream(stream))
+    else:
+        _native.call("cm_matmul_ex", pa, pb, pc, n, k, m, batch, a_bs, b_bs, c_bs,
+                     ctypes.byref(epi), _stream(stream))
 
 
 def ConvKernel(x, weight, bias, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw,
                stride_h=1, stride_w=1, dilation_h=1, dilation_w=1, pad_top=0, pad_left=0,
-               has_bias=0, is_depthwise=0, stream=None) -> None:
-    """ONNX Conv (group 1 or depthwise), NCHW, implicit bottom/right padding."""
+               has_bias=0, is_depthwise=0, stream=None, add=None, act=ACT_NONE) -> None:
+    """ONNX Conv (group 1 or depthwise), NCHW, implicit bottom/right padding.
+
+    Optional fused epilogue: y = act(sat16(y + add)), add shaped like y."""
     args = [batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w,
             dilation_h, dilation_w, pad_top, pad_left, int(bool(has_bias)), int(bool(is_depthwise))]
     args = [_u32("conv arg", v) for v in args]
@@ -94,7 +122,11 @@ def ConvKernel(x, weight, bias, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_
     pw = _dev_ptr(weight, out_ch * (1 if is_depthwise else in_ch) * kh * kw, "weight")
     pbias = _dev_ptr(bias, out_ch, "bias") if has_bias else None
     py = _dev_ptr(y, batch * out_ch * out_h * out_w, "y")
-    _native.call("cm_conv", px, pw, pbias, py, *args, _stream(stream))
+    epi = _epilogue(add, False, act, batch * out_ch * out_h * out_w)
+    if epi is None:
+        _native.call("cm_conv", px, pw, pbias, py, *args, _stream(stream))
+    else:
+        _native.call("cm_conv_ex", px, pw, pbias, py, *args, ctypes.byref(epi), _stream(stream))
 
 
 def PoolingKernel(x, y, batch, channels, in_h, in_w, out_h, out_w, pool_h, pool_w,

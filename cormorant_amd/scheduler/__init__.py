@@ -5,6 +5,7 @@ op dispatch (graph.py, nodes.py), buffer plan (codegen/_core.py) and Gemm /
 Reshape handling, with a HIP backend (``InferenceSession``) in place of the
 generated KV260 C project.
 """
+from . import fuse
 from .graph import ALL_SUPPORTED_OP_TYPES, OnnxGraph, split_gemms
 from .nodes import (OP_ADD, OP_DIV, OP_MUL, OP_RELU, OP_RELU6, OP_SUB, POOL_AVG, POOL_LP,
                     POOL_MAX, ConvNode, KernelCall, MatmulNode, PoolNode, ReshapeNode,

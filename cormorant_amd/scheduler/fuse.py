@@ -1,0 +1,228 @@
+"""Epilogue fusion for the GPU backend.
+
+The reference scheduler emits one kernel call per ONNX node, so a Conv followed
+by Clip(0,6) is a run_conv writing an intermediate and a run_op reading it back
+(inference-scheduler/src/nodes.py:227-453, 828-1119).  On the GPU the second
+call costs a launch and a round trip of the intermediate through memory.  This
+pass finds, in a buffer plan's call list, a MatMul / Conv call whose output is
+read by nothing but the immediately following VectorOP call(s) and folds those
+into the MatMul / Conv epilogue (``cm_matmul_ex`` / ``cm_conv_ex``):
+
+    conv | matmul  ->  Add (same-shaped tensor)           [-> Relu | Clip(0,6)]
+    matmul         ->  Add (bias row broadcast per column) [-> Relu | Clip(0,6)]
+    conv | matmul  ->  Relu | Clip(0,6)
+
+The fused epilogue computes exactly what the unfused calls compute (the same
+saturating Add and clamp applied to the same saturated value), so the graph's
+outputs are bit-identical; only the intermediate is never materialised.
+
+A fused call writes its final output while it still reads its inputs, so that
+output must not share memory with them.  ``live_from`` gives each fused
+output's new first-use node (the MatMul / Conv node) for the pool layout, which
+then never places it in a slot its inputs occupy; ``fusions`` re-checks the
+actual storage of every fused group and drops any group that overlaps.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Dict, List, Optional, Set, Tuple
+
+from .nodes import OP_ADD, OP_RELU, OP_RELU6, KernelCall
+
+ADD_NONE, ADD_SAME, ADD_COLUMN = 0, 1, 2
+ACT_NONE, ACT_RELU, ACT_RELU6 = 0, 1, 2
+_ACT_OF_OP = {OP_RELU: ACT_RELU, OP_RELU6: ACT_RELU6}
+
+
+@dataclass(frozen=True)
+class FusedCall:
+    """A MatMul / Conv call with the VectorOP calls folded into its epilogue."""
+    call: KernelCall                 # the MatMul / Conv call (its output tensor is bypassed)
+    absorbed: Tuple[KernelCall, ...]  # the VectorOP calls it replaces, in order
+    out: str                         # tensor the fused call writes (last absorbed call's output)
+    add: Optional[str]               # tensor added in the epilogue
+    add_mode: int
+    act: int
+
+    def __str__(self) -> str:
+        return " + ".join(str(c) for c in (self.call,) + self.absorbed)
+
+
+def _reads(call: KernelCall) -> List[str]:
+    t = call.tensors
+    if call.kernel == "op":
+        names = [t[0], t[1]] if call.args[1] < OP_RELU else [t[0]]
+    elif call.kernel in ("matmul", "matmul_at"):
+        names = [t[0], t[1]]
+    elif call.kernel == "conv":
+        names = [t[0], t[1], t[2]]
+    elif call.kernel == "pool":
+        names = [t[0]]
+    else:
+        raise ValueError(f"unknown kernel '{call.kernel}'")
+    return [n for n in names if n is not None]
+
+
+def _writes(call: KernelCall) -> str:
+    return call.tensors[3] if call.kernel == "conv" else call.tensors[-1]
+
+
+def _written_count(call: KernelCall) -> Optional[int]:
+    """Elements of one contiguous block the call writes from its output base, or
+    None when the output has gaps (strided batches) or an element offset."""
+    if call.kernel == "conv":
+        nb, _c, _h, _w, mo, oh, ow = call.args[:7]
+        return nb * mo * oh * ow
+    n, _k, m, batch, _a, _b, c_bs = call.args
+    if call.offsets and call.offsets[2]:
+        return None
+    if batch == 1 or c_bs == 0:
+        return n * m
+    return batch * n * m if c_bs == n * m else None
+
+
+class _Graph:
+    """Readers / writers of every tensor root (reshape aliases resolved)."""
+
+    def __init__(self, plan) -> None:
+        self.plan = plan
+        self.calls = [c for _, c in plan.calls]
+        self.readers: Dict[str, Set[int]] = {}
+        self.writers: Dict[str, Set[int]] = {}
+        for i, c in enumerate(self.calls):
+            for n in _reads(c):
+                self.readers.setdefault(self.root(n), set()).add(i)
+            self.writers.setdefault(self.root(_writes(c)), set()).add(i)
+        self.outputs = {self.root(t.onnx_name) for t in plan.graph.output_tensors}
+
+    def root(self, name: str) -> str:
+        seen = 0
+        while name in self.plan.aliases and seen <= len(self.plan.aliases):
+            name = self.plan.aliases[name]
+            seen += 1
+        return name
+
+    def private(self, name: str, writer: int, reader: int) -> bool:
+        """`name` is written only by call `writer`, read only by call `reader`,
+        and is not (a view of) a graph output."""
+        r = self.root(name)
+        return (name not in self.plan.redirect and r not in self.outputs and
+                self.writers.get(r) == {writer} and self.readers.get(r) == {reader})
+
+
+def _match(g: _Graph, k: int) -> Optional[FusedCall]:
+    calls = g.calls
+    c = calls[k]
+    if c.kernel not in ("matmul", "matmul_at", "conv") or k + 1 >= len(calls):
+        return None
+    count = _written_count(c)
+    t = _writes(c)
+    nxt = calls[k + 1]
+    if nxt.kernel != "op" or not g.private(t, k, k + 1):
+        return None
+    size, op, outer, a_inc, b_inc = nxt.args
+    a, b, y = nxt.tensors
+    if op in _ACT_OF_OP:
+        if a != t or outer != 1 or size != count:
+            return None
+        return FusedCall(c, (nxt,), y, None, ADD_NONE, _ACT_OF_OP[op])
+    if op != OP_ADD or (a == t) == (b == t):
+        return None
+    other = b if a == t else a
+    if count is not None and outer == 1 and size == count:
+        mode = ADD_SAME
+    elif c.kernel != "conv" and _column_add(c, size, outer, a_inc if a == t else b_inc,
+                                            b_inc if a == t else a_inc):
+        mode = ADD_COLUMN   # MatMul rows + bias[m] broadcast over them
+        count = outer * size if (a_inc if a == t else b_inc) == size else None
+    else:
+        return None
+    fused = FusedCall(c, (nxt,), y, other, mode, ACT_NONE)
+    if k + 2 < len(calls) and count is not None:
+        act = calls[k + 2]
+        if act.kernel == "op":
+            size2, op2, outer2, _, _ = act.args
+            if (op2 in _ACT_OF_OP and act.tensors[0] == y and outer2 == 1 and
+                    size2 == count and g.private(y, k + 1, k + 2)):
+                fused = FusedCall(c, (nxt, act), act.tensors[2], other, mode, _ACT_OF_OP[op2])
+    return fused
+
+
+def _column_add(c: KernelCall, size: int, outer: int, t_inc: int, o_inc: int) -> bool:
+    """The broadcast Add walks the MatMul's output rows in order (row stride
+    t_inc, the same stride for its own output) adding one row vector: each
+    output row r of batch z sits at z*c_stride + r*m."""
+    n, _k, m, batch, _a, _b, c_bs = c.args
+    if o_inc != 0 or size != m or (c.offsets and c.offsets[2]):
+        return False
+    if batch == 1:
+        return outer == n and t_inc == m
+    return n == 1 and outer == batch and t_inc == c_bs
+
+
+def candidates(plan) -> List[Tuple[int, FusedCall]]:
+    """(index of the MatMul / Conv call in plan.calls, fused group) for every
+    group the call structure allows, without looking at storage."""
+    g = _Graph(plan)
+    out: List[Tuple[int, FusedCall]] = []
+    k = 0
+    while k < len(g.calls):
+        f = _match(g, k)
+        if f is not None:
+            out.append((k, f))
+            k += 1 + len(f.absorbed)
+        else:
+            k += 1
+    return out
+
+
+def live_from(plan) -> Dict[str, int]:
+    """{fused output tensor: node index of its MatMul / Conv} for the pool layout."""
+    node_of = [idx for idx, _ in plan.calls]
+    return {f.out: node_of[k] for k, f in candidates(plan)}
+
+
+def _span(plan, call: KernelCall, name: str) -> Tuple[str, str, int, int]:
+    """(allocation kind, key, first element, end element) a call touches of `name`."""
+    st = plan.storage[name]
+    i = call.tensors.index(name)
+    off = st.offset + (call.offsets[i] if call.offsets else 0)
+    return st.kind, st.key, off, st.offset + call.extents()[name]
+
+
+def _overlap(x, y) -> bool:
+    return x[0] == y[0] and x[1] == y[1] and x[2] < y[3] and y[2] < x[3]
+
+
+def fusions(plan) -> List[Tuple[int, FusedCall]]:
+    """The candidate groups whose fused output does not overlap anything the
+    fused call reads (an Add operand may coincide with it exactly: in place)."""
+    ok = []
+    for k, f in candidates(plan):
+        last = f.absorbed[-1]
+        out = _span(plan, last, f.out)
+        inputs = [_span(plan, f.call, n) for n in _reads(f.call)]
+        if any(_overlap(out, s) for s in inputs):
+            continue
+        if f.add is not None:
+            add = _span(plan, f.absorbed[0], f.add)
+            if _overlap(out, add) and not (f.add_mode == ADD_SAME and add[2] == out[2]):
+                continue
+        ok.append((k, f))
+    return ok
+
+
+def launch_list(plan) -> List[object]:
+    """plan.calls with every fusable group replaced by its FusedCall."""
+    groups = dict(fusions(plan))
+    seq: List[object] = []
+    k = 0
+    calls = [c for _, c in plan.calls]
+    while k < len(calls):
+        if k in groups:
+            seq.append(groups[k])
+            k += 1 + len(groups[k].absorbed)
+        else:
+            seq.append(calls[k])
+            k += 1
+    return seq

@@ -151,8 +151,12 @@ def reshape_aliases(graph: OnnxGraph) -> Dict[str, str]:
             for sn in graph.nodes if isinstance(sn, ReshapeNode)}
 
 
-def live_intervals(graph: OnnxGraph) -> Dict[str, Tuple[int, int]]:
-    """(producing node index, last consuming node index) of each non-alias intermediate."""
+def live_intervals(graph: OnnxGraph, live_from: Optional[Dict[str, int]] = None
+                   ) -> Dict[str, Tuple[int, int]]:
+    """(producing node index, last consuming node index) of each non-alias intermediate.
+
+    ``live_from`` moves the start of some intermediates earlier (a backend that
+    writes a tensor from an earlier node, e.g. a fused epilogue)."""
     aliases = reshape_aliases(graph)
     names = {t.onnx_name for t in graph.intermediate_tensors if t.onnx_name not in aliases}
     first: Dict[str, int] = {}
@@ -163,11 +167,15 @@ def live_intervals(graph: OnnxGraph) -> Dict[str, Tuple[int, int]]:
         for t in sn.inputs:
             if t.onnx_name in names:
                 last[t.onnx_name] = i
+    if live_from:
+        for n, i in live_from.items():
+            if n in first:
+                first[n] = min(first[n], i)
     return {n: (first[n], last.get(n, first[n])) for n in names if n in first}
 
 
-def pool_layout(graph: OnnxGraph, layouts: Dict[str, TensorLayout]
-                ) -> Tuple[List[Tuple[str, int, int]], int]:
+def pool_layout(graph: OnnxGraph, layouts: Dict[str, TensorLayout],
+                live_from: Optional[Dict[str, int]] = None) -> Tuple[List[Tuple[str, int, int]], int]:
     """([(tensor, offset, alloc)], total elements) of the one pool allocation.
 
     Weights come first, each in its own slot.  Intermediates are sorted by
@@ -185,7 +193,7 @@ def pool_layout(graph: OnnxGraph, layouts: Dict[str, TensorLayout]
         a = layouts[t.onnx_name].alloc
         entries.append((t.onnx_name, off, a))
         off += up(a)
-    iv = live_intervals(graph)
+    iv = live_intervals(graph, live_from)
     cands = [t.onnx_name for t in graph.intermediate_tensors if t.onnx_name not in aliases]
     timed = sorted(((n, iv[n]) for n in cands if n in iv),
                    key=lambda kv: (kv[1][0], -layouts[kv[0]].alloc))
@@ -226,10 +234,10 @@ class Storage:
 class BufferPlan:
     """Everything the backend needs to run the graph on one device."""
 
-    def __init__(self, graph: OnnxGraph) -> None:
+    def __init__(self, graph: OnnxGraph, live_from: Optional[Dict[str, int]] = None) -> None:
         self.graph = graph
         self.layouts = compute_tensor_layouts(graph)
-        self.pool_entries, self.pool_elems = pool_layout(graph, self.layouts)
+        self.pool_entries, self.pool_elems = pool_layout(graph, self.layouts, live_from)
         self.aliases = reshape_aliases(graph)
         inputs = {t.onnx_name for t in graph.input_tensors}
         outputs = {t.onnx_name for t in graph.output_tensors}

@@ -13,8 +13,11 @@ libcormorant_amd.so:
 
 Reshape / Squeeze / Unsqueeze / Dropout outputs are the same device address
 as their source; a graph output at the end of a reshape chain is written
-directly by the producing kernel.  There is no CPU execution path: without the
-native library the constructor raises.
+directly by the producing kernel.  With ``fuse=True`` (default) an Add /
+Relu / Clip(0,6) call that is the sole reader of a MatMul / Conv output runs
+in that call's epilogue (``fuse.py``); results are bit-identical either way.
+There is no CPU execution path: without the native library the constructor
+raises.
 """
 from __future__ import annotations
 
@@ -24,6 +27,7 @@ from typing import Dict, List, Optional, Tuple
 import numpy as np
 
 from .. import _native
+from . import fuse as _fuse
 from .graph import OnnxGraph
 from .nodes import KernelCall
 from .plan import BufferPlan
@@ -35,9 +39,16 @@ _FUNCS = {"op": "cm_vectorop", "matmul": "cm_matmul", "matmul_at": "cm_matmul",
 class InferenceSession:
     """Device-resident instance of one model (weights loaded, buffers allocated)."""
 
-    def __init__(self, model, stream: int = 0) -> None:
+    def __init__(self, model, stream: int = 0, fuse: bool = True) -> None:
         self.graph = model if isinstance(model, OnnxGraph) else OnnxGraph(model)
         self.plan = BufferPlan(self.graph)
+        if fuse:
+            starts = _fuse.live_from(self.plan)
+            if starts:
+                self.plan = BufferPlan(self.graph, starts)
+            self.launch_list = _fuse.launch_list(self.plan)
+        else:
+            self.launch_list = [c for _, c in self.plan.calls]
         self._lib = _native.load()
         self.stream = int(stream)
         _native.call("cm_buf_pool_init")
@@ -52,7 +63,7 @@ class InferenceSession:
             for t in self.graph.output_tensors:
                 self._alloc(("output", t.onnx_name), self.plan.layouts[t.onnx_name].alloc)
             _native.call("cm_sync", None)
-            self._launches = [self._prepare(c) for _, c in self.plan.calls]
+            self._launches = [self._prepare(c) for c in self.launch_list]
         except Exception:
             self.close()
             raise
@@ -79,8 +90,7 @@ class InferenceSession:
         buf = self._bufs[(st.kind, st.key)]
         return int(buf.contents.dev) + 2 * st.offset
 
-    def _prepare(self, call: KernelCall):
-        fn = getattr(self._lib, _FUNCS[call.kernel])
+    def _pointers(self, call: KernelCall):
         ptrs = []
         for i, name in enumerate(call.tensors):
             if name is None:
@@ -90,7 +100,23 @@ class InferenceSession:
             if call.offsets:
                 p += 2 * call.offsets[i]
             ptrs.append(p)
-        return fn, _FUNCS[call.kernel], tuple(ptrs) + tuple(call.args)
+        return ptrs
+
+    def _prepare(self, item):
+        if isinstance(item, _fuse.FusedCall):
+            call = item.call
+            name = "cm_conv_ex" if call.kernel == "conv" else "cm_matmul_ex"
+            ptrs = self._pointers(call)
+            ptrs[-1] = self.device_ptr(item.out)   # the output of the last absorbed call
+            epi = _native.CmEpilogue()
+            epi.add = self.device_ptr(item.add) if item.add is not None else None
+            epi.add_mode = item.add_mode
+            epi.act = item.act
+            # the epilogue object rides along in the tuple so it outlives the pointer
+            return getattr(self._lib, name), name, tuple(ptrs) + tuple(call.args) + (
+                ctypes.byref(epi),), epi
+        fn = getattr(self._lib, _FUNCS[item.kernel])
+        return fn, _FUNCS[item.kernel], tuple(self._pointers(item)) + tuple(item.args), None
 
     # ------------------------------------------------------------------ running
 
@@ -98,7 +124,7 @@ class InferenceSession:
         """Enqueue every kernel of the graph (inputs must already be on the device)."""
         s = self.stream if stream is None else int(stream)
         s = s or None
-        for fn, name, args in self._launches:
+        for fn, name, args, _keep in self._launches:
             rc = fn(*args, s)
             if rc:
                 raise _native.CmError(name, rc, _native.last_error())

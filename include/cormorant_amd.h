@@ -103,6 +103,45 @@ int cm_pool(const int16_t *x, int16_t *y, uint32_t batch, uint32_t channels, uin
             uint32_t dil_h, uint32_t dil_w, uint32_t pool_type, uint32_t lp_order,
             uint32_t count_include_pad, hipStream_t stream);
 
+/* ---------------------------------------------------------- fused epilogues */
+
+/* Element-wise epilogue applied by a MatMul / Conv call to each output value y
+ * (the saturated Q8.8 result) before it is stored:
+ *   add_mode CM_EPI_ADD_SAME:   y = sat16(y + add[i]), add laid out exactly like
+ *                               the output (same strides; add == output is allowed);
+ *   add_mode CM_EPI_ADD_COLUMN: y = sat16(y + add[j]) for output column j
+ *                               (MatMul only: a bias row broadcast over rows and batches);
+ *   then act CM_EPI_ACT_RELU:   y = max(y, 0);  CM_EPI_ACT_RELU6: y = clamp(y, 0, 1536).
+ * The stored value equals what run_op(ADD) and then run_op(RELU / RELU6) would
+ * leave when applied to the unfused output (VectorOP.cpp:8-35).  add must not
+ * overlap the call's inputs or any other part of its output. */
+#define CM_EPI_ADD_NONE   0u
+#define CM_EPI_ADD_SAME   1u
+#define CM_EPI_ADD_COLUMN 2u
+#define CM_EPI_ACT_NONE   0u
+#define CM_EPI_ACT_RELU   1u
+#define CM_EPI_ACT_RELU6  2u
+
+typedef struct cm_epilogue {
+    const int16_t *add;   /* NULL when add_mode == CM_EPI_ADD_NONE */
+    uint32_t add_mode;
+    uint32_t act;
+} cm_epilogue_t;
+
+/* cm_matmul / cm_conv with an epilogue (epi may be NULL = none).  No reference
+ * counterpart: they let a caller such as the scheduler's GPU backend fold the
+ * run_op Add / Relu / Clip(0,6) that follows a run_matmul / run_conv into that
+ * call, saving a launch and a round trip of the intermediate through memory. */
+int cm_matmul_ex(const int16_t *a, const int16_t *b, int16_t *c, uint32_t n, uint32_t k,
+                 uint32_t m, uint32_t batch, uint32_t a_stride, uint32_t b_stride,
+                 uint32_t c_stride, const cm_epilogue_t *epi, hipStream_t stream);
+int cm_conv_ex(const int16_t *x, const int16_t *weight, const int16_t *bias, int16_t *y,
+               uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
+               uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
+               uint32_t stride_w, uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
+               uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise,
+               const cm_epilogue_t *epi, hipStream_t stream);
+
 /* ------------------------------------------------------------------ buffers */
 
 /* Mirrors inference_buf_t (bench_src/inference.h:12-21): an owning allocation

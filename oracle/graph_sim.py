@@ -64,8 +64,14 @@ def simulate_raw(graph, feeds_raw: Dict[str, np.ndarray]) -> Dict[str, np.ndarra
     return {t.onnx_name: ns.to_raw(arrays[t.onnx_name]) for t in graph.output_tensors}
 
 
-def run_plan(plan, feeds_raw: Dict[str, np.ndarray], threads: bool = True) -> Dict[str, np.ndarray]:
-    """Execute plan.calls with the C-simulation kernels; graph outputs as raw int16."""
+def run_plan(plan, feeds_raw: Dict[str, np.ndarray], threads: bool = True,
+             launches=None) -> Dict[str, np.ndarray]:
+    """Execute plan.calls with the C-simulation kernels; graph outputs as raw int16.
+
+    ``launches`` (a backend launch list: calls and fused groups) is executed
+    instead when given: a fused group runs its calls in order with every
+    intermediate of the group in a private scratch array, i.e. never in the
+    plan's storage -- what the fused GPU epilogue does."""
     bufs = {("pool", ""): plan.pool_image() if plan.pool_elems else np.zeros(1, np.int16)}
     for t in plan.graph.input_tensors:
         b = np.zeros(plan.layouts[t.onnx_name].alloc, dtype=np.int16)
@@ -82,7 +88,7 @@ def run_plan(plan, feeds_raw: Dict[str, np.ndarray], threads: bool = True) -> Di
         start = st.offset + extra
         return base[start:start + max(st.capacity - extra, 0)]
 
-    for _, call in plan.calls:
+    def execute(call, view):
         offs = call.offsets or (0,) * len(call.tensors)
         v = [view(n, o) for n, o in zip(call.tensors, offs)]
         a = call.args
@@ -96,5 +102,20 @@ def run_plan(plan, feeds_raw: Dict[str, np.ndarray], threads: bool = True) -> Di
             _ora.pool(v[0], v[1], *a, threads=threads)
         else:
             raise ValueError(call.kernel)
+
+    for item in ([c for _, c in plan.calls] if launches is None else launches):
+        if not hasattr(item, "absorbed"):
+            execute(item, view)
+            continue
+        chain = (item.call,) + tuple(item.absorbed)
+        scratch = {}
+        for c in chain[:-1]:
+            out = c.tensors[3] if c.kernel == "conv" else c.tensors[-1]
+            scratch[out] = np.full(plan.storage[out].capacity, 0x5A5A, np.int16)
+
+        def fused_view(name, extra=0, scratch=scratch):
+            return scratch[name][extra:] if name in scratch else view(name, extra)
+        for c in chain:
+            execute(c, fused_view)
     return {t.onnx_name: plan.gather(t.onnx_name, bufs[("output", t.onnx_name)])
             for t in plan.graph.output_tensors}

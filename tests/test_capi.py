@@ -49,6 +49,32 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.cm_run_op(None, None, None, 8, 0, 1, 0, 0) == _native.CM_ERR_INVALID
 
 
+def test_bad_epilogues_are_rejected_before_any_launch():
+    """cm_matmul_ex / cm_conv_ex validate the epilogue before launching (the
+    pointers below are never dereferenced: every call returns CM_ERR_INVALID)."""
+    lib = _native.load()
+    fake = 4096
+
+    def epi(add, mode, act):
+        e = _native.CmEpilogue()
+        e.add, e.add_mode, e.act = add, mode, act
+        return ctypes.byref(e)
+
+    def mm(e):
+        return lib.cm_matmul_ex(fake, fake, fake, 2, 2, 2, 1, 0, 0, 0, e, None)
+
+    def conv(e):
+        return lib.cm_conv_ex(fake, fake, None, fake, *([1] * 15), 0, 0, e, None)
+
+    assert mm(epi(fake, 3, 0)) == _native.CM_ERR_INVALID
+    assert mm(epi(fake, _native.CM_EPI_ADD_SAME, 3)) == _native.CM_ERR_INVALID
+    assert mm(epi(None, _native.CM_EPI_ADD_COLUMN, 0)) == _native.CM_ERR_INVALID
+    assert "null add" in _native.last_error()
+    assert conv(epi(fake, _native.CM_EPI_ADD_COLUMN, 0)) == _native.CM_ERR_INVALID
+    assert "add_mode" in _native.last_error()
+    assert conv(epi(None, _native.CM_EPI_ADD_SAME, 0)) == _native.CM_ERR_INVALID
+
+
 def test_missing_library_fails_loudly(tmp_path):
     with pytest.raises(_native.NativeLibraryError):
         saved = _native._lib

@@ -19,8 +19,8 @@ from tests.test_scheduler import GRAPH_CASES, SAT_EXPECT, feeds_for
 pytestmark = pytest.mark.gpu
 
 
-def check_session(g, feeds, sim=True):
-    sess = InferenceSession(g)
+def check_session(g, feeds, sim=True, fuse=True):
+    sess = InferenceSession(g, fuse=fuse)
     try:
         got = sess.run(feeds)
     finally:
@@ -36,11 +36,12 @@ def check_session(g, feeds, sim=True):
     return got
 
 
+@pytest.mark.parametrize("fuse", [True, False], ids=["fused", "unfused"])
 @pytest.mark.parametrize("name", sorted(GRAPH_CASES))
-def test_reference_graphs(name):
-    say(f"scheduler graph {name}")
+def test_reference_graphs(name, fuse):
+    say(f"scheduler graph {name} fuse={fuse}")
     g = OnnxGraph(ox.encode_model(GRAPH_CASES[name]()))
-    check_session(g, feeds_for(g, len(name)))
+    check_session(g, feeds_for(g, len(name)), fuse=fuse)
 
 
 @pytest.mark.parametrize("kind", om.SAT_KINDS)
@@ -74,11 +75,12 @@ def test_session_reuse_and_input_copy():
         sess.close()
 
 
-def test_mlp_full_size():
+@pytest.mark.parametrize("fuse", [True, False], ids=["fused", "unfused"])
+def test_mlp_full_size(fuse):
     """2-layer MLP, batch 64 (Gemm 784->256, Relu, Gemm 256->10)."""
-    say("scheduler MLP b64")
+    say(f"scheduler MLP b64 fuse={fuse}")
     g = OnnxGraph(ox.encode_model(wl.mlp_model()))
-    check_session(g, {"X": wl.mlp_input()})
+    check_session(g, {"X": wl.mlp_input()}, fuse=fuse)
 
 
 def test_mobilenet_like_full_size():
@@ -87,6 +89,12 @@ def test_mobilenet_like_full_size():
     g = OnnxGraph(ox.encode_model(wl.mobilenet_model()))
     y = check_session(g, {"X": wl.mobilenet_input()})["Y"]
     assert np.count_nonzero(y) > 0.9 * y.size
+
+
+def test_mobilenet_like_small_unfused():
+    say("scheduler MobileNetV2-like b2 32 unfused")
+    g = OnnxGraph(ox.encode_model(wl.mobilenet_model(batch=2, hw=32)))
+    check_session(g, {"X": wl.mobilenet_input(2, 32)}, fuse=False)
 
 
 def test_run_helpers_reject_short_buffers():

@@ -11,6 +11,7 @@ gen_matmul_models.py docstrings) for the same graph structures.
 from __future__ import annotations
 
 import os
+from collections import Counter
 
 import numpy as np
 import pytest
@@ -18,7 +19,7 @@ import pytest
 import oracle
 from oracle import graph_sim as gs
 from cormorant_amd import workloads as wl
-from cormorant_amd.scheduler import (BufferPlan, OnnxGraph, SchedulerError, live_intervals,
+from cormorant_amd.scheduler import (BufferPlan, OnnxGraph, SchedulerError, fuse, live_intervals,
                                      onnx_io as ox)
 from cormorant_amd.scheduler.nodes import (OP_ADD, OP_RELU6, ConvNode, MatmulNode, PoolNode,
                                            ReshapeNode, ScheduledNode)
@@ -497,3 +498,114 @@ def test_mobilenet_like_small_oracles_agree():
     got = gs.run_plan(BufferPlan(g), {"X": x})["Y"]
     np.testing.assert_array_equal(got, gs.simulate_raw(g, {"X": x})["Y"])
     assert np.count_nonzero(got) > 0.9 * got.size
+
+
+# --------------------------------------------------------------------------- epilogue fusion
+
+def fused_plan(g):
+    plan = BufferPlan(g, fuse.live_from(BufferPlan(g)))
+    return plan, fuse.launch_list(plan)
+
+
+def test_fusion_mobilenet_groups():
+    """Every Clip(0,6) and residual Add of the MobileNetV2-like graph, and the
+    classifier's bias Add, run in a convolution / MatMul epilogue."""
+    g = graph(wl.mobilenet_model(batch=2, hw=32))
+    plan, seq = fused_plan(g)
+    assert len(plan.calls) == 68 and len(seq) == 38
+    groups = [x for x in seq if isinstance(x, fuse.FusedCall)]
+    kinds = Counter((x.add_mode, x.act) for x in groups)
+    assert kinds == {(fuse.ADD_NONE, fuse.ACT_RELU6): 19, (fuse.ADD_SAME, fuse.ACT_NONE): 10,
+                     (fuse.ADD_COLUMN, fuse.ACT_NONE): 1}
+    assert not any(getattr(x, "kernel", None) == "op" for x in seq)
+    # the group's string form keeps the reference call syntax of every member
+    assert str(groups[0]).startswith("run_conv(X, conv0_w, conv0_b, conv0_y, 2, 3, 32, 32, 32,")
+    assert str(groups[0]).endswith("+ run_op(conv0_y, NULL, conv0_y_r6, 16384, RELU6, 1, 0, 0)")
+
+
+def test_fusion_mlp_chains_bias_and_relu():
+    plan, seq = fused_plan(graph(wl.mlp_model()))
+    assert [type(x).__name__ for x in seq] == ["FusedCall", "FusedCall"]
+    assert (seq[0].add, seq[0].add_mode, seq[0].act, seq[0].out) == \
+        ("B1", fuse.ADD_COLUMN, fuse.ACT_RELU, "R")
+    # second layer: batch-64 single-row MatMul with 16-element row stride + bias
+    assert seq[1].call.args == (1, 256, 10, 64, 256, 0, 16)
+    assert (seq[1].add, seq[1].add_mode, seq[1].act, seq[1].out) == \
+        ("B2", fuse.ADD_COLUMN, fuse.ACT_NONE, "Y")
+
+
+def _conv_then(nodes_after, outputs, extra_inputs=()):
+    N = ox.make_node
+    inits = [ox.from_array(np.full((4, 3, 1, 1), 0.25, np.float32), "W")]
+    nodes = [N("Conv", ["X", "W"], ["c"], kernel_shape=[1, 1])] + nodes_after
+    ins = [ox.value_info("X", [1, 3, 4, 4])] + [ox.value_info(n, s) for n, s in extra_inputs]
+    g = ox.make_graph(nodes, "conv_then", ins, [ox.value_info(n, s) for n, s in outputs], inits)
+    return graph(ox.make_model(g))
+
+
+def test_fusion_rejections():
+    N = ox.make_node
+    shape = [1, 4, 4, 4]
+    # the conv output has a second reader
+    g = _conv_then([N("Relu", ["c"], ["r"]), N("Add", ["c", "r"], ["Y"])], [("Y", shape)])
+    assert not fuse.candidates(BufferPlan(g))
+    # the conv output is itself a graph output
+    g = _conv_then([N("Relu", ["c"], ["Y"])], [("c", shape), ("Y", shape)])
+    assert not fuse.candidates(BufferPlan(g))
+    # Sub is not an epilogue operation
+    g = _conv_then([N("Sub", ["c", "Z"], ["Y"])], [("Y", shape)], [("Z", shape)])
+    assert not fuse.candidates(BufferPlan(g))
+    # a broadcast Add repeating a [2, 8] block over MatMul batches is not a column add
+    mm = ox.make_graph([N("MatMul", ["X", "W"], ["m"]), N("Add", ["m", "Z"], ["Y"])], "mm_bcast",
+                       [ox.value_info("X", [2, 2, 4]), ox.value_info("Z", [2, 8])],
+                       [ox.value_info("Y", [2, 2, 8])],
+                       [ox.from_array(np.full((4, 8), 0.5, np.float32), "W")])
+    p = BufferPlan(graph(ox.make_model(mm)))
+    assert str(p.calls[1][1]) == "run_op(m, Z, Y, 16, ADD, 2, 16, 0)"
+    assert not fuse.candidates(p)
+    # accepted: same-shape Add then Clip(0,6) through a reshape of the sum
+    g = _conv_then([N("Add", ["c", "Z"], ["s"]), N("Relu", ["s"], ["Y"])], [("Y", shape)],
+                   [("Z", shape)])
+    (k, f), = fuse.candidates(BufferPlan(g))
+    assert (k, f.add, f.add_mode, f.act, f.out) == (0, "Z", fuse.ADD_SAME, fuse.ACT_RELU, "Y")
+
+
+def test_fusion_storage_checks():
+    """With the reference pool layout a fused output may share a slot with its
+    MatMul / Conv input; those groups are dropped, and ``live_from`` gives a
+    layout in which none is."""
+    g = graph(wl.mobilenet_model(batch=2, hw=32))
+    p0 = BufferPlan(g)
+    cands, ok = fuse.candidates(p0), dict(fuse.fusions(p0))
+    assert 0 < len(ok) < len(cands)
+    for k, f in cands:
+        if k in ok:
+            continue
+        out = fuse._span(p0, f.absorbed[-1], f.out)
+        ins = [fuse._span(p0, f.call, n) for n in fuse._reads(f.call)]
+        assert any(fuse._overlap(out, s) for s in ins), str(f)
+    p1, _ = fused_plan(g)
+    assert len(fuse.fusions(p1)) == len(fuse.candidates(p1)) == 30
+
+
+@pytest.mark.parametrize("name", ["gemm_chain", "gemm_with_bias", "conv_relu_chain",
+                                  "mixed_all_kernels", "residual_chain"])
+def test_fused_launches_match_simulation(name):
+    """The fused launch list, executed on the oracle with every group's
+    intermediates kept out of the plan's storage, gives the graph's outputs."""
+    g = graph(GRAPH_CASES[name]())
+    plan, seq = fused_plan(g)
+    feeds = feeds_for(g, 3)
+    got = gs.run_plan(plan, feeds, threads=False, launches=seq)
+    want = gs.simulate_raw(g, feeds)
+    for k in want:
+        np.testing.assert_array_equal(got[k], want[k], err_msg=k)
+
+
+def test_fused_launches_mobilenet_small():
+    g = graph(wl.mobilenet_model(batch=2, hw=32))
+    plan, seq = fused_plan(g)
+    x = wl.mobilenet_input(2, 32)
+    oracle.set_threads(min(os.cpu_count() or 1, 8))
+    got = gs.run_plan(plan, {"X": x}, launches=seq)["Y"]
+    np.testing.assert_array_equal(got, gs.run_plan(BufferPlan(g), {"X": x})["Y"])
