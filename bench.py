@@ -63,7 +63,9 @@ def time_launches(calls, steps: int) -> float:
 def time_graph(calls, steps: int) -> float:
     """Mean duration (ms) of one launch with host overhead removed: `steps`
     launches (cycling through `calls`) are captured into one HIP graph, which is
-    replayed once untimed and then once between HIP events."""
+    replayed once untimed and then once between HIP events.  The calls run once
+    eagerly on the capture stream first (per-stream split-K workspaces are
+    allocated there; nothing is allocated during capture)."""
     import torch
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -73,7 +75,7 @@ def time_graph(calls, steps: int) -> float:
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=side):
         for i in range(steps):
             calls[i % len(calls)]()
     graph.replay()

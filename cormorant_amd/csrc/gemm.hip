@@ -27,7 +27,11 @@
 // banks).  The next tile's loads are issued before the MFMA phase; loads are
 // unconditional (out-of-range elements are zeroed by the buffer range check
 // or by a select), so all of a tile's loads are in flight at once.
+#include <map>
+#include <mutex>
 #include <type_traits>
+#include <utility>
+#include <vector>
 
 #include "cm_internal.h"
 #include "q88.h"
@@ -46,6 +50,28 @@ constexpr int kFoldIters = 512;      // fold MFMA partials every 512*64 = 32768 
 constexpr int TI = 4, TJ = 2;        // MFMA tiles per wave: 4 row tiles x 2 column tiles
 constexpr uint32_t kTabMax = 2048;   // largest K of the table-driven convolution gather
 
+// Division of any n < 2^31 by a fixed d >= 1 as a multiply and shift
+// (Granlund-Montgomery, the round-up variant): l = ceil(log2 d), p = 31 + l,
+// m = ceil(2^p / d) < 2^33; then n / d = (n * m) >> p exactly, since the
+// error term n*(m*d - 2^p) / (d*2^p) stays below 2^-l <= 1/d.
+struct FastDiv {
+    uint32_t m_lo, m_hi, p;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+    if (d == 0) d = 1;
+    uint32_t l = 0;
+    while (l < 32 && (1ull << l) < d) ++l;
+    const uint32_t p = 31 + l;
+    const unsigned __int128 m = (((unsigned __int128)1 << p) + d - 1) / d;
+    return FastDiv{(uint32_t)m, (uint32_t)(m >> 32), p};
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+    const uint64_t t = (uint64_t)n * f.m_lo + (f.m_hi ? (uint64_t)n << 32 : 0ull);
+    return (uint32_t)(t >> f.p);
+}
+
 struct GemmArgs {
     const int16_t* a;     // [rows][k], row stride lda (weights for conv)
     const int16_t* b;     // dense: [k][cols], row stride ldb; conv: x (NCHW)
@@ -58,8 +84,13 @@ struct GemmArgs {
     // implicit GEMM: column = n*P + p, k = (c*kh + khi)*kw + kwi
     uint32_t C, H, W, OW, P, kh, kw, sh, sw, dh, dw, pt, pl;
     uint64_t x_img, y_img;
+    FastDiv div_p, div_ow, div_kk, div_kw;   // divisions by P, OW, kh*kw, kw
     uint32_t x_bytes;            // table mode: size of the whole input tensor, < 2^31
     EpiArgs epi;                 // fused Add / Relu / Clip; add_mode 1 follows C's layout
+    // split-K: blockIdx.z selects k steps [z*split_steps, +split_steps) and the
+    // block stores its partial sums (no bias) to ws[z][row][col]; 0 = no split
+    uint32_t split_steps;
+    uint32_t* ws;
 };
 
 // Raw buffer resource word 3 for gfx950 (32-bit data, no swizzle): loads past
@@ -105,6 +136,7 @@ struct Smem {
     uint32_t row_sum[BM];
     uint32_t col_sum[BN];
     int32_t bias[BM];      // bias << 8 of the block's rows (0 past the last row)
+    uint64_t coff[BN];     // convolution: output offset n*y_img + p of each column
 };
 
 // Splits 16 int16 values (8 packed words, k order) into 16 high and 16 low
@@ -318,9 +350,9 @@ struct ConvBTile {
     __device__ __forceinline__ void init(const GemmArgs& g, uint32_t col0) {
         const uint32_t col = col0 + (threadIdx.x & 127);
         col_ok = col < g.cols;
-        const uint32_t n = col_ok ? col / g.P : 0;
+        const uint32_t n = col_ok ? fdiv(col, g.div_p) : 0;
         const uint32_t p = col_ok ? col - n * g.P : 0;
-        const uint32_t oh = p / g.OW, ow = p - (p / g.OW) * g.OW;
+        const uint32_t oh = fdiv(p, g.div_ow), ow = p - oh * g.OW;
         // a column past the end gets a window origin no tap can reach, so the
         // per-tap bounds test alone rejects it (a separate lane-varying test
         // would let the compiler branch around the gather and serialise it)
@@ -366,9 +398,9 @@ struct ConvBTile {
     __device__ __forceinline__ void load(const GemmArgs& g, uint32_t k0) {
         const uint32_t ks = k0 + (threadIdx.x >> 7) * 16;
         const uint32_t kk = g.kh * g.kw;
-        uint32_t c = ks / kk;
+        uint32_t c = fdiv(ks, g.div_kk);
         uint32_t r = ks - c * kk;
-        uint32_t khi = r / g.kw;
+        uint32_t khi = fdiv(r, g.div_kw);
         uint32_t kwi = r - khi * g.kw;
         const uint32_t hw = g.H * g.W;
 #pragma unroll
@@ -419,6 +451,11 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
         const uint32_t r = row0 + threadIdx.x;
         s.bias[threadIdx.x] = r < g.rows ? (int32_t)g.bias[r] * 256 : 0;
     }
+    if (CONV && threadIdx.x >= BM && threadIdx.x < BM + BN) {
+        const uint32_t col = col0 + threadIdx.x - BM;
+        const uint32_t n = fdiv(col, g.div_p);
+        s.coff[threadIdx.x - BM] = (uint64_t)n * g.y_img + (col - n * g.P);
+    }
     const int2* tab = nullptr;
     if constexpr (MODE == B_CONV_TAB) {
         // one entry per k the main loop loads: its k steps plus the two past
@@ -427,8 +464,8 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
         const uint32_t kk = g.kh * g.kw, hw = g.H * g.W;
         const uint32_t kend = ((g.k + BK - 1) / BK + 2) * BK;
         for (uint32_t k = threadIdx.x; k < kend; k += kThreads) {
-            const uint32_t c = k / kk, r = k - (k / kk) * kk;
-            const uint32_t khi = r / g.kw, kwi = r - (r / g.kw) * g.kw;
+            const uint32_t c = fdiv(k, g.div_kk), r = k - c * kk;
+            const uint32_t khi = fdiv(r, g.div_kw), kwi = r - khi * g.kw;
             const uint32_t dy = khi * g.dh, dx = kwi * g.dw;
             ktab[k] = k < g.k ? int2{(int)(2 * (c * hw + dy * g.W + dx)), (int)r} : int2{0, 31};
         }
@@ -562,9 +599,14 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
         }
     };
 
-    const uint32_t nk = (g.k + BK - 1) / BK;
-    load_tile(at[0], bt[0], 0);
-    load_tile(at[1], bt[1], BK);
+    // this block's k steps: all of them, or its split's share (sums over any
+    // k range obey the limb identity with that range's row / column sums and Kp)
+    const uint32_t nk_all = (g.k + BK - 1) / BK;
+    const uint32_t s0 = g.split_steps ? blockIdx.z * g.split_steps : 0u;
+    const uint32_t nk = g.split_steps ? min(g.split_steps, nk_all - s0) : nk_all;
+    const uint32_t kbase = s0 * BK;
+    load_tile(at[0], bt[0], kbase);
+    load_tile(at[1], bt[1], kbase + BK);
     stage_tile(at[0], bt[0], s.st[0], true);
     __syncthreads();
     // Steps go in pairs (it, it + 1).  Step it computes on planes 0 while the
@@ -578,13 +620,13 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     // loop from planes 0.
     uint32_t it = 0;
     for (; it + 2 <= nk; it += 2) {
-        load_tile(at[0], bt[0], (it + 2) * BK);
+        load_tile(at[0], bt[0], kbase + (it + 2) * BK);
         __builtin_amdgcn_sched_barrier(0);   // keep the loads ahead of this step's work
         mfma_step(s.st[0], it);
         stage_tile(at[1], bt[1], s.st[1], true);
         interleave();
         __syncthreads();
-        load_tile(at[1], bt[1], (it + 3) * BK);
+        load_tile(at[1], bt[1], kbase + (it + 3) * BK);
         __builtin_amdgcn_sched_barrier(0);
         mfma_step(s.st[1], it + 1);
         stage_tile(at[0], bt[0], s.st[0], it + 2 < nk);
@@ -611,26 +653,38 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     const uint32_t kp_term = 16384u * (nk * (uint32_t)BK);
     int16_t* cptr = g.c + (CONV ? 0 : (uint64_t)blockIdx.z * g.c_bs);
     const int16_t* rptr = g.epi.add + (CONV ? 0 : (uint64_t)blockIdx.z * g.c_bs);
+    // MFMA tiles wholly past the last row or column are skipped (wave-uniform)
 #pragma unroll
     for (int j = 0; j < TJ; ++j) {
+        if (col0 + wcol + j * 16 >= g.cols) continue;
         const uint32_t cl = wcol + j * 16 + (lane & 15);
         const uint32_t col = col0 + cl;
         const bool cok = col < g.cols;
-        uint64_t coff;
-        uint64_t rstride;
-        if constexpr (CONV) {
-            const uint32_t n = col / g.P;
-            coff = (uint64_t)n * g.y_img + (col - n * g.P);
-            rstride = g.P;
-        } else {
-            coff = col;
-            rstride = g.ldc;
-        }
+        const uint64_t coff = CONV ? s.coff[cl] : (uint64_t)col;
+        const uint64_t rstride = CONV ? (uint64_t)g.P : g.ldc;
         const uint32_t csum = s.col_sum[cl];
-        int32_t yv[TI][4];
-        uint64_t ov[TI][4];
+        if (g.ws) {   // split-K partial: raw sums, bias and epilogue in split_reduce
+            uint32_t* wp = g.ws + (uint64_t)blockIdx.z * g.rows * g.cols + col;
+#pragma unroll
+            for (int i = 0; i < TI; ++i) {
+                if (row0 + wrow + i * 16 >= g.rows) continue;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t rl = wrow + i * 16 + (lane >> 4) * 4 + e;
+                    uint32_t v = ((uint32_t)hh[i][j][e] << 16) + ((uint32_t)mid[i][j][e] << 8) +
+                                 (uint32_t)ll[i][j][e];
+                    v += 128u * (s.row_sum[rl] + csum) - kp_term;
+                    if (cok && row0 + rl < g.rows) wp[(uint64_t)(row0 + rl) * g.cols] = v;
+                }
+            }
+            continue;
+        }
+        const int32_t cadd = g.epi.add_mode == 2u ? (int32_t)g.epi.add[cok ? col : 0u] : 0;
 #pragma unroll
         for (int i = 0; i < TI; ++i) {
+            if (row0 + wrow + i * 16 >= g.rows) continue;
+            int32_t yv[4];
+            uint64_t ov[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const uint32_t rl = wrow + i * 16 + (lane >> 4) * 4 + e;
@@ -640,40 +694,131 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
                 if constexpr (FOLD) v += (uint32_t)tot[i][j][e];
                 v += 128u * (s.row_sum[rl] + csum) - kp_term;
                 if constexpr (HAS_BIAS) v += (uint32_t)s.bias[rl];
-                ov[i][e] = ok ? coff + (uint64_t)(row0 + rl) * rstride : ~0ull;
-                yv[i][e] = q88::acc_to_data(v);
+                ov[e] = ok ? coff + (uint64_t)(row0 + rl) * rstride : ~0ull;
+                yv[e] = q88::acc_to_data(v);
             }
-        }
-        if (g.epi.add_mode == 1u) {
+            if (g.epi.add_mode == 1u) {
 #pragma unroll
-            for (int i = 0; i < TI; ++i)
+                for (int e = 0; e < 4; ++e) yv[e] = q88::add(yv[e], rptr[ov[e] == ~0ull ? 0 : ov[e]]);
+            } else if (g.epi.add_mode == 2u) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    yv[i][e] = q88::add(yv[i][e], rptr[ov[i][e] == ~0ull ? 0 : ov[i][e]]);
-        } else if (g.epi.add_mode == 2u) {
-            const int32_t b = g.epi.add[cok ? col : 0u];
-#pragma unroll
-            for (int i = 0; i < TI; ++i)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) yv[i][e] = q88::add(yv[i][e], b);
-        }
-#pragma unroll
-        for (int i = 0; i < TI; ++i)
+                for (int e = 0; e < 4; ++e) yv[e] = q88::add(yv[e], cadd);
+            }
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-                if (ov[i][e] != ~0ull) cptr[ov[i][e]] = (int16_t)q88::epi_act(yv[i][e], g.epi.act);
+                if (ov[e] != ~0ull) cptr[ov[e]] = (int16_t)q88::epi_act(yv[e], g.epi.act);
+        }
     }
+}
+
+// Split-K second pass: sums the partials of one output element over the
+// splits, adds the bias, saturates, applies the epilogue and stores the value
+// in the MatMul ([rows][ldc]) or convolution (NCHW) output layout.
+constexpr int kReduceThreads = 256;
+
+__global__ __launch_bounds__(kReduceThreads) void split_reduce(
+        const uint32_t* __restrict__ ws, uint32_t splits, uint32_t rows, uint32_t cols,
+        const int16_t* __restrict__ bias, int16_t* __restrict__ y, uint32_t conv, uint32_t P,
+        uint64_t y_img, uint64_t ldc, EpiArgs epi) {
+    const uint64_t n = (uint64_t)rows * cols;
+    for (uint64_t idx = (uint64_t)blockIdx.x * kReduceThreads + threadIdx.x; idx < n;
+         idx += (uint64_t)gridDim.x * kReduceThreads) {
+        const uint32_t row = (uint32_t)(idx / cols);
+        const uint32_t col = (uint32_t)(idx - (uint64_t)row * cols);
+        uint32_t v = 0;
+        for (uint32_t z = 0; z < splits; ++z) v += ws[z * n + idx];
+        if (bias) v += (uint32_t)(int32_t)bias[row] << 8;
+        uint64_t o;
+        if (conv) {
+            const uint32_t img = col / P;
+            o = (uint64_t)img * y_img + (uint64_t)row * P + (col - img * P);
+        } else {
+            o = (uint64_t)row * ldc + col;
+        }
+        int32_t yv = q88::acc_to_data(v);
+        if (epi.add_mode == 1u) yv = q88::add(yv, epi.add[o]);
+        else if (epi.add_mode == 2u) yv = q88::add(yv, epi.add[col]);
+        y[o] = (int16_t)q88::epi_act(yv, epi.act);
+    }
+}
+
+// Per-(device, stream) split-K workspace.  It only grows, and a replaced
+// buffer is kept until the process ends, since a captured HIP graph may still
+// hold its address; calls on one stream are ordered, so they share it safely.
+// Inside a stream capture nothing is allocated: the call then runs unsplit.
+struct SplitWorkspace {
+    uint32_t* ptr = nullptr;
+    size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+std::map<std::pair<int, hipStream_t>, SplitWorkspace> g_ws;
+std::vector<uint32_t*> g_ws_retired;
+constexpr size_t kWsMin = 8u << 20, kWsMax = 64u << 20;
+
+uint32_t* split_workspace(hipStream_t s, size_t bytes) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
+    std::lock_guard<std::mutex> lock(g_ws_mutex);
+    SplitWorkspace& w = g_ws[{dev, s}];
+    if (w.bytes >= bytes) return w.ptr;
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    const size_t nb = bytes > kWsMin ? bytes : kWsMin;
+    uint32_t* p = nullptr;
+    if (hipMalloc((void**)&p, nb) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    if (w.ptr) g_ws_retired.push_back(w.ptr);
+    w.ptr = p;
+    w.bytes = nb;
+    return p;
+}
+
+// Number of k splits for a launch of `tiles` blocks over nk_all k steps: enough
+// blocks for every CU when the tile grid alone leaves most of the chip idle,
+// at least two k steps per split, at most 16 splits.
+uint32_t choose_splits(uint32_t tiles, uint32_t nk_all) {
+    if (tiles >= 160 || nk_all < 4) return 1;
+    uint32_t want = (256 + tiles - 1) / tiles;
+    uint32_t sp = want < nk_all / 2 ? want : nk_all / 2;
+    if (sp > 16) sp = 16;
+    return sp < 2 ? 1 : sp;
 }
 
 inline bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p & (n - 1)) == 0; }
 
 template <int MODE>
-int launch_gemm(GemmArgs& g, uint32_t zdim, hipStream_t s, const char* name) {
-    const dim3 grid((g.cols + BN - 1) / BN, (g.rows + BM - 1) / BM, zdim);
+int launch_gemm(GemmArgs& g0, uint32_t zdim, hipStream_t s, const char* name) {
+    GemmArgs g = g0;
+    dim3 grid((g.cols + BN - 1) / BN, (g.rows + BM - 1) / BM, zdim);
     if (grid.y > 65535u || grid.z > 65535u || grid.x > 0x7FFFFFFFu)
         return cm_set_error(CM_ERR_RANGE, "%s: grid too large", name);
     const bool fold = g.k > (uint32_t)(kFoldIters * BK);
-    const bool bias = g.bias != nullptr;
+    // split-K when the output tiles cannot fill the chip (single launch, no fold)
+    uint32_t splits = 1;
+    if (zdim == 1 && !fold) {
+        const uint32_t nk_all = (g.k + BK - 1) / BK;
+        splits = choose_splits(grid.x * grid.y, nk_all);
+        if (splits > 1) {
+            const uint32_t sps = (nk_all + splits - 1) / splits;
+            splits = (nk_all + sps - 1) / sps;
+            const size_t bytes = (size_t)splits * g.rows * g.cols * 4u;
+            uint32_t* ws = bytes <= kWsMax ? split_workspace(s, bytes) : nullptr;
+            if (ws) {
+                g.split_steps = sps;
+                g.ws = ws;
+                g.a_bs = g.b_bs = g.c_bs = 0;
+                grid.z = splits;
+            } else {
+                splits = 1;
+            }
+        }
+    }
+    const bool bias = g.bias != nullptr && splits == 1;
     // Buffer loads need each per-block resource below 2^31 bytes: 128 rows of A
     // and 64 k rows of dense B.  The table-gather conv always satisfies it.
     const bool buf = MODE == B_CONV_TAB ||
@@ -701,7 +846,14 @@ int launch_gemm(GemmArgs& g, uint32_t zdim, hipStream_t s, const char* name) {
     }
 #undef CM_GEMM_BIAS
 #undef CM_GEMM_LAUNCH
-    return cm_check_launch(name);
+    if (splits == 1) return cm_check_launch(name);
+    const int rc = cm_check_launch(name);
+    if (rc) return rc;
+    const uint64_t n = (uint64_t)g.rows * g.cols;
+    const uint32_t blocks = (uint32_t)cm_grid_blocks(n, kReduceThreads, 4096);
+    hipLaunchKernelGGL(split_reduce, dim3(blocks), dim3(kReduceThreads), 0, s, g.ws, splits, g.rows,
+                       g.cols, g.bias, g.c, (uint32_t)(MODE != B_DENSE), g.P, g.y_img, g.ldc, g.epi);
+    return cm_check_launch("split_reduce");
 }
 
 }  // namespace
@@ -764,6 +916,10 @@ int cm_conv_gemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias,
     g.kh = kh; g.kw = kw; g.sh = sh; g.sw = sw; g.dh = dh; g.dw = dw; g.pt = pad_top; g.pl = pad_left;
     g.x_img = x_img;
     g.y_img = (uint64_t)out_ch * P;
+    g.div_p = make_fastdiv((uint32_t)P);
+    g.div_ow = make_fastdiv(out_w);
+    g.div_kk = make_fastdiv(kh * kw);
+    g.div_kw = make_fastdiv(kw);
     const uint64_t x_bytes = 2 * x_img * batch;
     g.x_bytes = (uint32_t)(x_bytes < 0x80000000ull ? x_bytes : 0);
     // table mode: at most 31 taps (one bit each), byte offsets of the window

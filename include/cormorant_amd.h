@@ -19,7 +19,15 @@
  *     calling thread.  Where the reference has undefined behaviour (shapes
  *     beyond its compile-time kMax* limits) this library computes the exact
  *     result instead, or returns CM_ERR_RANGE if a size exceeds its indexing.
- *   - The caller owns every buffer; kernels never allocate.
+ *   - The caller owns every buffer it passes.  The one allocation the library
+ *     makes itself is a split-K workspace: a MatMul / Conv call whose output
+ *     tiles are too few to fill the GPU splits its k range over extra blocks
+ *     and adds the partial sums in a second pass, through a workspace owned by
+ *     the library, one per (device, stream), allocated by the first such call
+ *     on that stream (8-64 MiB, kept until the process ends).  Inside a stream
+ *     capture nothing is allocated: if the stream has no workspace yet the
+ *     call runs unsplit (same result, slower), so run a call once on the
+ *     capture stream before capturing it.
  *
  * Reference interfaces replaced (paths relative to the reference root):
  *   kernels/vectorop/include/VectorOP.h:86-95        VectorOPKernel

@@ -115,3 +115,33 @@ def test_run_helpers_reject_short_buffers():
     finally:
         for x in (a, b, c):
             lib.cm_buf_free(x)
+
+
+def test_session_graph_replay_matches_eager():
+    """The session's launch list (fused epilogues, split-K layers) captured in
+    a HIP graph on a warmed-up stream: every replay, with eager work and
+    synchronisations in between, reproduces the eager output."""
+    import torch
+    say("scheduler MobileNetV2-like b2 32 graph replay")
+    g = OnnxGraph(ox.encode_model(wl.mobilenet_model(batch=2, hw=32)))
+    x = wl.mobilenet_input(2, 32)
+    sess = InferenceSession(g)
+    try:
+        want = sess.run({"X": x})["Y"]
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            sess.launch(side.cuda_stream)       # eager run on the capture stream
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            sess.launch(side.cuda_stream)
+        for rep in range(3):
+            junk = torch.randint(-100, 100, (1 << 20,), dtype=torch.int16, device="cuda")
+            junk.mul_(3)                           # unrelated eager work between replays
+            torch.cuda.synchronize()
+            graph.replay()
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(sess.read_output("Y"), want, err_msg=f"replay {rep}")
+    finally:
+        sess.close()

@@ -1,0 +1,90 @@
+"""GPU parity of split-K launches: MatMul / Conv calls whose output tiles
+cannot fill the GPU are computed as k-split partial sums plus a reduction pass
+(the partials of every k range obey the same limb identity, and the uint32
+sum of the partials is the wrapping accumulator).  Compared bit for bit with
+the oracle, including full-range operands whose sums wrap."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from cormorant_amd import kernels as K
+from cormorant_amd import workloads as wl
+from tests.gpu_util import dev, empty_dev, host, oracle_threads, say
+from tests.test_gpu_epilogue import apply_epilogue, full_range
+
+pytestmark = pytest.mark.gpu
+
+MM = [
+    # name, n, k, m, operand range (None = full int16 range)
+    ("one_tile_k5000", 100, 5000, 60, 2.0),
+    ("fc_16x1280x1000", 16, 1280, 1000, 1.0),
+    ("odd_steps_k449", 130, 449, 70, 4.0),
+    ("wrap_full_range", 64, 4096, 96, None),
+    ("k256_two_tiles", 200, 256, 100, 8.0),
+]
+
+
+@pytest.mark.parametrize("case", MM, ids=[c[0] for c in MM])
+def test_matmul_split(case):
+    name, n, k, m, rng_ = case
+    say(f"split-K matmul {name}")
+    g = wl.rng(910, n, k, m)
+    if rng_ is None:
+        a, b = full_range(g, n * k), full_range(g, k * m)
+    else:
+        a = wl.uniform_q88(g, n * k, -rng_, rng_)
+        b = wl.uniform_q88(g, k * m, -rng_, rng_)
+    c = empty_dev(n * m)
+    K.MatmulKernel(dev(a), dev(b), c, n, k, m)
+    want = np.zeros(n * m, np.int16)
+    oracle.set_threads(oracle_threads())
+    oracle.matmul(a, b, want, n, k, m, threads=True)
+    np.testing.assert_array_equal(host(c), want)
+
+
+@pytest.mark.parametrize("act", [K.ACT_NONE, K.ACT_RELU6])
+def test_matmul_split_column_add(act):
+    say(f"split-K matmul column add act {act}")
+    n, k, m = 16, 1280, 1000
+    g = wl.rng(911, act)
+    a = wl.uniform_q88(g, n * k, -1.0, 1.0)
+    b = wl.uniform_q88(g, k * m, -0.5, 0.5)
+    bias = full_range(g, m)
+    c = empty_dev(n * m)
+    K.MatmulKernel(dev(a), dev(b), c, n, k, m, add=dev(bias), add_column=True, act=act)
+    y = np.zeros(n * m, np.int16)
+    oracle.matmul(a, b, y, n, k, m)
+    np.testing.assert_array_equal(host(c), apply_epilogue(y, bias, True, act, n, m))
+
+
+CONV = [
+    # name, N, C, H, W, M, k, s, p
+    ("7x7x160", 16, 160, 7, 7, 160, 3, 1, 1),
+    ("14x14x96_s2", 16, 96, 14, 14, 96, 3, 2, 1),
+    ("14x14x64", 16, 64, 14, 14, 64, 3, 1, 1),
+    ("5x5_kernel_c40", 2, 40, 9, 9, 50, 5, 1, 2),
+]
+
+
+@pytest.mark.parametrize("case", CONV, ids=[c[0] for c in CONV])
+def test_conv_split(case):
+    name, N, C, H, W, M, k, s, p = case
+    say(f"split-K conv {name}")
+    g = wl.rng(912, N, C, M)
+    OH = (H + 2 * p - k) // s + 1
+    x = wl.uniform_q88(g, N * C * H * W, -4.0, 4.0)
+    w = full_range(g, M * C * k * k)
+    bias = full_range(g, M)
+    res = full_range(g, N * M * OH * OH)
+    args = (N, C, H, W, M, OH, OH, k, k, s, s, 1, 1, p, p, 1, 0)
+    y = np.zeros(N * M * OH * OH, np.int16)
+    oracle.set_threads(oracle_threads())
+    oracle.conv(x, w, bias, y, *args, threads=True)
+    out = empty_dev(y.size)
+    K.ConvKernel(dev(x), dev(w), dev(bias), out, *args)
+    np.testing.assert_array_equal(host(out), y)
+    out2 = empty_dev(y.size)
+    K.ConvKernel(dev(x), dev(w), dev(bias), out2, *args, add=dev(res), act=K.ACT_RELU)
+    np.testing.assert_array_equal(host(out2), apply_epilogue(y, res, False, K.ACT_RELU, 0, 0))
