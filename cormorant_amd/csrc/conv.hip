@@ -1,8 +1,9 @@
 // conv.hip -- ConvKernel for gfx950 (kernels/conv/kernel/ConvKernel.cpp:46-343).
 //
 // Dispatch:
-//   * standard conv, 1x1 / stride 1 / no padding: batched GEMM
-//     Y[n] = W[out_ch][in_ch] x X[n][in_ch][h*w] on the int8-limb MFMA core;
+//   * standard conv, 1x1 / stride 1 / no padding, planes that fill 128-column
+//     tiles: batched GEMM Y[n] = W[out_ch][in_ch] x X[n][in_ch][h*w] on the
+//     int8-limb MFMA core;
 //   * any other standard conv: implicit GEMM on the same core, im2col gathered
 //     straight from NCHW x while the B tile is built (no im2col buffer);
 //   * depthwise (is_depthwise = 1, weights [out_ch][1][kh][kw]): direct kernel,
@@ -82,9 +83,14 @@ int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int1
         else hipLaunchKernelGGL(conv_depthwise<false>, grid, dim3(kThreads), 0, s, x, w, b, y, g, total, ea);
         return cm_check_launch("conv_depthwise");
     }
+    // 1x1 / stride 1 / no padding as one GEMM per image, when an image's
+    // pixels fill its 128-column tiles to at least 80 %; small planes (e.g.
+    // 7x7, 14x14) go through the gather path, whose columns run across images
+    const uint64_t hw = (uint64_t)in_h * in_w;
+    const uint64_t tiles = (hw + 127) / 128;
     if (kh == 1 && kw == 1 && sh == 1 && sw == 1 && pad_top == 0 && pad_left == 0 &&
-        out_h == in_h && out_w == in_w && (uint64_t)in_h * in_w <= 0x7FFFFFFFull)
-        return cm_conv_pointwise_launch(x, w, b, y, batch, in_ch, out_ch, in_h * in_w, epi, s);
+        out_h == in_h && out_w == in_w && hw <= 0x7FFFFFFFull && (tiles * 128 - hw) * 5 <= tiles * 128)
+        return cm_conv_pointwise_launch(x, w, b, y, batch, in_ch, out_ch, (uint32_t)hw, epi, s);
     return cm_conv_gemm_launch(x, w, b, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw,
                                sh, sw, dh, dw, pad_top, pad_left, epi, s);
 }

@@ -715,9 +715,13 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
 // splits, adds the bias, saturates, applies the epilogue and stores the value
 // in the MatMul ([rows][ldc]) or convolution (NCHW) output layout.
 constexpr int kReduceThreads = 256;
+constexpr uint32_t kMaxSplits = 16;
 
+// SPLITS is a template parameter so the partial loads are unrolled and all in
+// flight at once (a run-time trip count would wait for each in turn).
+template <uint32_t SPLITS>
 __global__ __launch_bounds__(kReduceThreads) void split_reduce(
-        const uint32_t* __restrict__ ws, uint32_t splits, uint32_t rows, uint32_t cols,
+        const uint32_t* __restrict__ ws, uint32_t rows, uint32_t cols,
         const int16_t* __restrict__ bias, int16_t* __restrict__ y, uint32_t conv, uint32_t P,
         uint64_t y_img, uint64_t ldc, EpiArgs epi) {
     const uint64_t n = (uint64_t)rows * cols;
@@ -725,9 +729,12 @@ __global__ __launch_bounds__(kReduceThreads) void split_reduce(
          idx += (uint64_t)gridDim.x * kReduceThreads) {
         const uint32_t row = (uint32_t)(idx / cols);
         const uint32_t col = (uint32_t)(idx - (uint64_t)row * cols);
-        uint32_t v = 0;
-        for (uint32_t z = 0; z < splits; ++z) v += ws[z * n + idx];
-        if (bias) v += (uint32_t)(int32_t)bias[row] << 8;
+        uint32_t part[SPLITS];
+#pragma unroll
+        for (uint32_t z = 0; z < SPLITS; ++z) part[z] = __builtin_nontemporal_load(ws + z * n + idx);
+        uint32_t v = bias ? (uint32_t)(int32_t)bias[row] << 8 : 0u;
+#pragma unroll
+        for (uint32_t z = 0; z < SPLITS; ++z) v += part[z];
         uint64_t o;
         if (conv) {
             const uint32_t img = col / P;
@@ -739,6 +746,18 @@ __global__ __launch_bounds__(kReduceThreads) void split_reduce(
         if (epi.add_mode == 1u) yv = q88::add(yv, epi.add[o]);
         else if (epi.add_mode == 2u) yv = q88::add(yv, epi.add[col]);
         y[o] = (int16_t)q88::epi_act(yv, epi.act);
+    }
+}
+
+template <uint32_t S>
+int launch_reduce(uint32_t splits, dim3 grid, hipStream_t s, const GemmArgs& g, uint32_t conv) {
+    if constexpr (S > kMaxSplits) {
+        return cm_set_error(CM_ERR_INVALID, "split_reduce: %u splits", splits);
+    } else {
+        if (splits != S) return launch_reduce<S + 1>(splits, grid, s, g, conv);
+        hipLaunchKernelGGL(split_reduce<S>, grid, dim3(kReduceThreads), 0, s, g.ws, g.rows, g.cols,
+                           g.bias, g.c, conv, g.P, g.y_img, g.ldc, g.epi);
+        return cm_check_launch("split_reduce");
     }
 }
 
@@ -785,7 +804,7 @@ uint32_t choose_splits(uint32_t tiles, uint32_t nk_all) {
     if (tiles >= 160 || nk_all < 4) return 1;
     uint32_t want = (256 + tiles - 1) / tiles;
     uint32_t sp = want < nk_all / 2 ? want : nk_all / 2;
-    if (sp > 16) sp = 16;
+    if (sp > kMaxSplits) sp = kMaxSplits;
     return sp < 2 ? 1 : sp;
 }
 
@@ -850,10 +869,8 @@ int launch_gemm(GemmArgs& g0, uint32_t zdim, hipStream_t s, const char* name) {
     const int rc = cm_check_launch(name);
     if (rc) return rc;
     const uint64_t n = (uint64_t)g.rows * g.cols;
-    const uint32_t blocks = (uint32_t)cm_grid_blocks(n, kReduceThreads, 4096);
-    hipLaunchKernelGGL(split_reduce, dim3(blocks), dim3(kReduceThreads), 0, s, g.ws, splits, g.rows,
-                       g.cols, g.bias, g.c, (uint32_t)(MODE != B_DENSE), g.P, g.y_img, g.ldc, g.epi);
-    return cm_check_launch("split_reduce");
+    const dim3 rgrid((uint32_t)cm_grid_blocks(n, kReduceThreads, 4096));
+    return launch_reduce<2>(splits, rgrid, s, g, (uint32_t)(MODE != B_DENSE));
 }
 
 }  // namespace
