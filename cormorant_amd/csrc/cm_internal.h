@@ -30,6 +30,28 @@ inline EpiArgs cm_epi_args(const cm_epilogue_t* e) {
 }
 int cm_check_launch(const char* what);
 
+// Division of any n < 2^31 by a fixed d >= 1 as a multiply and shift
+// (Granlund-Montgomery, the round-up variant): l = ceil(log2 d), p = 31 + l,
+// m = ceil(2^p / d) < 2^33; then n / d = (n * m) >> p exactly, since the
+// error term n*(m*d - 2^p) / (d*2^p) stays below 2^-l <= 1/d.
+struct FastDiv {
+    uint32_t m_lo, m_hi, p;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+    if (d == 0) d = 1;
+    uint32_t l = 0;
+    while (l < 32 && (1ull << l) < d) ++l;
+    const uint32_t p = 31 + l;
+    const unsigned __int128 m = (((unsigned __int128)1 << p) + d - 1) / d;
+    return FastDiv{(uint32_t)m, (uint32_t)(m >> 32), p};
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+    const uint64_t t = (uint64_t)n * f.m_lo + (f.m_hi ? (uint64_t)n << 32 : 0ull);
+    return (uint32_t)(t >> f.p);
+}
+
 inline uint64_t cm_grid_blocks(uint64_t work, uint32_t threads, uint64_t cap = 1u << 20) {
     uint64_t b = (work + threads - 1) / threads;
     if (b == 0) b = 1;

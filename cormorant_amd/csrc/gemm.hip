@@ -50,28 +50,6 @@ constexpr int kFoldIters = 512;      // fold MFMA partials every 512*64 = 32768 
 constexpr int TI = 4, TJ = 2;        // MFMA tiles per wave: 4 row tiles x 2 column tiles
 constexpr uint32_t kTabMax = 2048;   // largest K of the table-driven convolution gather
 
-// Division of any n < 2^31 by a fixed d >= 1 as a multiply and shift
-// (Granlund-Montgomery, the round-up variant): l = ceil(log2 d), p = 31 + l,
-// m = ceil(2^p / d) < 2^33; then n / d = (n * m) >> p exactly, since the
-// error term n*(m*d - 2^p) / (d*2^p) stays below 2^-l <= 1/d.
-struct FastDiv {
-    uint32_t m_lo, m_hi, p;
-};
-
-inline FastDiv make_fastdiv(uint32_t d) {
-    if (d == 0) d = 1;
-    uint32_t l = 0;
-    while (l < 32 && (1ull << l) < d) ++l;
-    const uint32_t p = 31 + l;
-    const unsigned __int128 m = (((unsigned __int128)1 << p) + d - 1) / d;
-    return FastDiv{(uint32_t)m, (uint32_t)(m >> 32), p};
-}
-
-__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
-    const uint64_t t = (uint64_t)n * f.m_lo + (f.m_hi ? (uint64_t)n << 32 : 0ull);
-    return (uint32_t)(t >> f.p);
-}
-
 struct GemmArgs {
     const int16_t* a;     // [rows][k], row stride lda (weights for conv)
     const int16_t* b;     // dense: [k][cols], row stride ldb; conv: x (NCHW)

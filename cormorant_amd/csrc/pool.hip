@@ -25,7 +25,7 @@ namespace {
 typedef short v8s __attribute__((ext_vector_type(8)));
 
 constexpr int kThreads = 256;
-constexpr uint64_t kPoolBlocks = 2048;   // 256 CUs x 8 resident blocks of 256 threads
+constexpr uint64_t kPoolBlocks = 2048;   // fallback: 256 CUs x 8 resident blocks of 256 threads
 
 struct PoolGeom {
     uint32_t in_h, in_w, out_h, out_w, ph, pw, sh, sw, pt, pl, dh, dw;
@@ -126,14 +126,22 @@ __global__ __launch_bounds__(kThreads) void pool_global(const int16_t* __restric
 // `vec` (in_w % 8 == 0, 16-byte aligned planes) selects 16-byte row copies;
 // otherwise rows are copied element by element.  KH/KW > 0 fix the window at
 // compile time (dilation 1) so the taps unroll with immediate LDS offsets.
-constexpr int kPre = 4;
+constexpr int kPre = 2;
 constexpr uint32_t kBandBytes = kPre * kThreads * 16;
+#ifndef CM_POOL_BAND_TARGET
+#define CM_POOL_BAND_TARGET (16u << 10)
+#endif
+// LDS bytes of input a band aims for: smaller bands give each persistent block
+// more items to pipeline and a shorter last item
+constexpr uint32_t kBandTarget = CM_POOL_BAND_TARGET < kBandBytes ? CM_POOL_BAND_TARGET : kBandBytes;
 constexpr uint32_t kInvTab = 64;   // AVG: 1/d for every denominator d <= 63, per block
 
 struct BandGeom {
     uint32_t band_h, n_bands, n_items;
-    uint32_t pitch, cofs, lds_rows;    // LDS tile: lds_rows x pitch elements
-    uint32_t rows_pp, vec;             // output rows per pass, 16-byte row copies
+    uint32_t pitch, cofs, lds_rows;    // LDS tile: lds_rows x pitch elements (+ slack rows)
+    uint32_t alloc_rows;               // rows allocated (slack for the last strip's reads)
+    uint32_t vec;                      // 16-byte row copies
+    FastDiv div_w;                     // division by in_w (element copies)
 };
 
 struct BandItem {
@@ -145,7 +153,7 @@ struct BandItem {
 
 __device__ __forceinline__ BandItem band_item(const PoolGeom& g, const BandGeom& b, uint32_t item) {
     BandItem it;
-    it.plane = item / b.n_bands;
+    it.plane = b.n_bands == 1 ? item : item / b.n_bands;
     const uint32_t band = item - (uint32_t)(it.plane * b.n_bands);
     it.oh0 = band * b.band_h;
     it.oh1 = min(it.oh0 + b.band_h, g.out_h);
@@ -158,24 +166,58 @@ __device__ __forceinline__ BandItem band_item(const PoolGeom& g, const BandGeom&
     return it;
 }
 
-template <int KIND, int KH, int KW>
+// Output rows per thread on the strip path (fixed window, row stride SH).
+constexpr int kStrip = 4;
+
+// KH/KW > 0: window fixed at compile time (dilation 1).  SH > 0 (with KH > 0):
+// row stride fixed too, and each thread reduces a vertical strip of kStrip
+// outputs of one column: every input row of the strip is reduced across the
+// window's columns once, and each output merges KH of those row partials
+// (max and the wrapping sums are associative, so the result is the same as
+// tap-by-tap accumulation).  Otherwise one output per thread and pass.
+template <int KIND, int KH, int KW, int SH>
 __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict__ x,
                                                       int16_t* __restrict__ y, PoolGeom g,
                                                       BandGeom b, float inv_full) {
     extern __shared__ __align__(16) int16_t lds[];
     __shared__ float inv_tab[kInvTab];
     constexpr int16_t kPadV = KIND == K_MAX ? (int16_t)-32768 : (int16_t)0;
+    constexpr bool STRIP = KH > 0 && SH > 0;
     const int32_t ph = KH > 0 ? KH : (int32_t)g.ph, pw = KW > 0 ? KW : (int32_t)g.pw;
     const int32_t dh = KH > 0 ? 1 : (int32_t)g.dh, dw = KW > 0 ? 1 : (int32_t)g.dw;
     const bool avg_tab = KIND == K_AVG && !g.cip && (uint32_t)(ph * pw) < kInvTab;
     if (KIND == K_AVG && threadIdx.x < kInvTab) inv_tab[threadIdx.x] = q88::inv_denom(threadIdx.x);
 
+    // left [0, cofs) and right [cofs + in_w, pitch) columns are padding in every
+    // row of every item (data rows only write [cofs, cofs + in_w)): filled once
+    {
+        const uint32_t rcols = b.pitch - b.cofs - g.in_w;
+        const uint32_t strip = b.cofs + rcols;
+        if (strip) {
+            const uint32_t n = b.alloc_rows * strip;
+            for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
+                const uint32_t r = i / strip, c = i - r * strip;
+                lds[r * b.pitch + (c < b.cofs ? c : c + g.in_w)] = kPadV;
+            }
+        }
+    }
+
+    // this thread's 16-byte vectors u: row (relative to the item's first real
+    // row) and vector column, the same for every item
     const uint32_t vpr = g.in_w / 8;                 // 16-byte vectors per input row (vec path)
-    const uint32_t my_r = threadIdx.x / g.out_w;     // this thread's row within a pass ...
+    uint32_t vslot[kPre];   // LDS element offset of vector u, relative to the item's row r0
+#pragma unroll
+    for (int u = 0; u < kPre; ++u) {
+        const uint32_t v = u * kThreads + threadIdx.x;
+        const uint32_t r = b.vec ? v / vpr : 0u;
+        vslot[u] = r * b.pitch + b.cofs + (v - r * vpr) * 8;
+    }
+    const uint32_t my_r = threadIdx.x / g.out_w;          // this thread's row (strip) within a pass ...
     const uint32_t my_c = threadIdx.x - my_r * g.out_w;   // ... and column (when out_w <= 256)
+    const uint32_t rows_pp = g.out_w >= (uint32_t)kThreads ? 1u : (uint32_t)kThreads / g.out_w;
     const uint32_t cstep = g.out_w > kThreads ? kThreads : g.out_w;
 
-    // fetch: the real input rows of an item into registers, vector v = u * kThreads + t
+    // fetch: the real input rows of an item into registers
     v8s pre[kPre];
     auto fetch = [&](const BandItem& it) {
         if (!b.vec) return;
@@ -197,36 +239,23 @@ __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict_
         const uint32_t next = item + gridDim.x;
         __syncthreads();                       // the previous item's LDS reads are done
         {
-            // padding: whole LDS rows outside [r0, r1), then the left [0, cofs) and
-            // right [cofs + in_w, pitch) columns of the real rows
+            // whole padding rows outside [r0, r1) (full pitch), then the data
             const uint32_t top = cur.r0 * b.pitch;
             const uint32_t bottom = (b.lds_rows - cur.r1) * b.pitch;
             for (uint32_t i = threadIdx.x; i < top; i += kThreads) lds[i] = kPadV;
             for (uint32_t i = threadIdx.x; i < bottom; i += kThreads) lds[cur.r1 * b.pitch + i] = kPadV;
-            const uint32_t rcols = b.pitch - b.cofs - g.in_w;
-            const uint32_t strip = b.cofs + rcols;
-            if (strip) {
-                const uint32_t n = (cur.r1 - cur.r0) * strip;
-                for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
-                    const uint32_t r = i / strip, c = i - r * strip;
-                    lds[(cur.r0 + r) * b.pitch + (c < b.cofs ? c : c + g.in_w)] = kPadV;
-                }
-            }
             if (b.vec) {
                 const uint32_t nv = (cur.r1 - cur.r0) * vpr;
 #pragma unroll
                 for (int u = 0; u < kPre; ++u) {
                     const uint32_t v = u * kThreads + threadIdx.x;
-                    if (v < nv) {
-                        const uint32_t r = v / vpr, q = v - r * vpr;
-                        *reinterpret_cast<v8s*>(lds + (cur.r0 + r) * b.pitch + b.cofs + q * 8) = pre[u];
-                    }
+                    if (v < nv) *reinterpret_cast<v8s*>(lds + cur.r0 * b.pitch + vslot[u]) = pre[u];
                 }
             } else {
                 const int16_t* xp = x + cur.plane * (uint64_t)g.in_h * g.in_w;
                 const uint32_t n = (cur.r1 - cur.r0) * g.in_w;
                 for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
-                    const uint32_t r = i / g.in_w, c = i - r * g.in_w;
+                    const uint32_t r = fdiv(i, b.div_w), c = i - r * g.in_w;
                     lds[(cur.r0 + r) * b.pitch + b.cofs + c] =
                         xp[(int64_t)(cur.ih_lo + (int32_t)(cur.r0 + r)) * g.in_w + c];
                 }
@@ -241,29 +270,71 @@ __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict_
         }
 
         int16_t* yp = y + cur.plane * (uint64_t)g.out_h * g.out_w;
-        for (uint32_t oh = cur.oh0 + my_r; my_r < b.rows_pp && oh < cur.oh1; oh += b.rows_pp) {
-            // LDS row of the window's first tap: oh*sh - pt - ih_lo
-            const int16_t* wrow = lds + (oh - cur.oh0) * g.sh * b.pitch + b.cofs - g.pl;
-            const int32_t ih0 = (int32_t)(oh * g.sh) - (int32_t)g.pt;
-            for (uint32_t ow = my_c; ow < g.out_w; ow += cstep) {
-                const int16_t* w0 = wrow + ow * g.sw;
-                Acc<KIND> a;
+        if constexpr (STRIP) {
+            constexpr int NR = (kStrip - 1) * SH + KH;     // input rows of one strip
+            const uint32_t nrows = cur.oh1 - cur.oh0;
+            for (uint32_t st = my_r; my_r < rows_pp && st * kStrip < nrows; st += rows_pp) {
+                const uint32_t oh_b = cur.oh0 + st * kStrip;
+                // strip rows run past the tile only for outputs that are not stored;
+                // the allocation has (kStrip - 1) * SH slack rows for them
+                const int16_t* wrow = lds + st * kStrip * SH * b.pitch + b.cofs - g.pl;
+                for (uint32_t ow = my_c; ow < g.out_w; ow += cstep) {
+                    const int16_t* w0 = wrow + ow * g.sw;
+                    uint32_t part[NR];
 #pragma unroll
-                for (int32_t khi = 0; khi < (KH > 0 ? KH : ph); ++khi) {
-                    const int16_t* rp = w0 + khi * dh * b.pitch;
+                    for (int rr = 0; rr < NR; ++rr) {
+                        Acc<KIND> a;
 #pragma unroll
-                    for (int32_t kwi = 0; kwi < (KW > 0 ? KW : pw); ++kwi) a.add(rp[kwi * dw]);
-                }
-                float inv = inv_full;
-                if constexpr (KIND == K_AVG) {
-                    if (!g.cip) {
-                        const int32_t iw0 = (int32_t)(ow * g.sw) - (int32_t)g.pl;
-                        const uint32_t d = (uint32_t)(valid_taps(ih0, ph, dh, (int32_t)g.in_h) *
-                                                      valid_taps(iw0, pw, dw, (int32_t)g.in_w));
-                        inv = avg_tab ? inv_tab[d] : q88::inv_denom(d);
+                        for (int kwi = 0; kwi < KW; ++kwi) a.add(w0[rr * b.pitch + kwi]);
+                        part[rr] = a.v;
+                    }
+#pragma unroll
+                    for (int o = 0; o < kStrip; ++o) {
+                        const uint32_t oh = oh_b + o;
+                        if (oh >= cur.oh1) break;
+                        Acc<KIND> a;
+                        a.v = part[o * SH];
+#pragma unroll
+                        for (int khi = 1; khi < KH; ++khi) a.merge(part[o * SH + khi]);
+                        float inv = inv_full;
+                        if constexpr (KIND == K_AVG) {
+                            if (!g.cip) {
+                                const int32_t ih0 = (int32_t)(oh * SH) - (int32_t)g.pt;
+                                const int32_t iw0 = (int32_t)(ow * g.sw) - (int32_t)g.pl;
+                                const uint32_t d = (uint32_t)(valid_taps(ih0, KH, 1, (int32_t)g.in_h) *
+                                                              valid_taps(iw0, KW, 1, (int32_t)g.in_w));
+                                inv = avg_tab ? inv_tab[d] : q88::inv_denom(d);
+                            }
+                        }
+                        yp[(uint64_t)oh * g.out_w + ow] = a.finish(inv);
                     }
                 }
-                yp[(uint64_t)oh * g.out_w + ow] = a.finish(inv);
+            }
+        } else {
+            for (uint32_t oh = cur.oh0 + my_r; my_r < rows_pp && oh < cur.oh1; oh += rows_pp) {
+                // LDS row of the window's first tap: oh*sh - pt - ih_lo
+                const int16_t* wrow = lds + (oh - cur.oh0) * g.sh * b.pitch + b.cofs - g.pl;
+                const int32_t ih0 = (int32_t)(oh * g.sh) - (int32_t)g.pt;
+                for (uint32_t ow = my_c; ow < g.out_w; ow += cstep) {
+                    const int16_t* w0 = wrow + ow * g.sw;
+                    Acc<KIND> a;
+#pragma unroll
+                    for (int32_t khi = 0; khi < (KH > 0 ? KH : ph); ++khi) {
+                        const int16_t* rp = w0 + khi * dh * b.pitch;
+#pragma unroll
+                        for (int32_t kwi = 0; kwi < (KW > 0 ? KW : pw); ++kwi) a.add(rp[kwi * dw]);
+                    }
+                    float inv = inv_full;
+                    if constexpr (KIND == K_AVG) {
+                        if (!g.cip) {
+                            const int32_t iw0 = (int32_t)(ow * g.sw) - (int32_t)g.pl;
+                            const uint32_t d = (uint32_t)(valid_taps(ih0, ph, dh, (int32_t)g.in_h) *
+                                                          valid_taps(iw0, pw, dw, (int32_t)g.in_w));
+                            inv = avg_tab ? inv_tab[d] : q88::inv_denom(d);
+                        }
+                    }
+                    yp[(uint64_t)oh * g.out_w + ow] = a.finish(inv);
+                }
             }
         }
         if (!more) break;
@@ -316,6 +387,20 @@ uint64_t rows_needed(const PoolGeom& g, uint32_t bh) {
     return (uint64_t)(bh - 1) * g.sh + (uint64_t)(g.ph - 1) * g.dh + 1;
 }
 
+// Blocks of kThreads threads with `lds` dynamic LDS bytes resident on the whole
+// device at once (occupancy x CU count), kPoolBlocks if the runtime cannot say.
+uint64_t resident_blocks(const void* kernel, uint32_t lds) {
+    int per_cu = 0, dev = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess ||
+        hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        per_cu <= 0 || cus <= 0) {
+        (void)hipGetLastError();
+        return kPoolBlocks;
+    }
+    return (uint64_t)per_cu * (uint64_t)cus;
+}
+
 // 1.0f / (float)d on the host: IEEE round-to-nearest-even, like the device path.
 float host_inv_denom(uint64_t d) { return d ? 1.0f / (float)d : 0.0f; }
 
@@ -363,7 +448,7 @@ int pool_launch(const int16_t* x, int16_t* y, uint64_t planes, const PoolGeom& g
         uint32_t lo = 1, hi = g.out_h;
         while (lo < hi) {
             const uint32_t mid = lo + (hi - lo + 1) / 2;
-            if (rows_needed(g, mid) * pitch * 2 <= kBandBytes) lo = mid; else hi = mid - 1;
+            if (rows_needed(g, mid) * pitch * 2 <= kBandTarget) lo = mid; else hi = mid - 1;
         }
         band_h = lo;
     }
@@ -378,19 +463,30 @@ int pool_launch(const int16_t* x, int16_t* y, uint64_t planes, const PoolGeom& g
             b.pitch = (uint32_t)pitch;
             b.cofs = (uint32_t)cofs;
             b.lds_rows = (uint32_t)rows_needed(g, band_h);
-            b.rows_pp = g.out_w >= (uint32_t)kThreads ? 1u : (uint32_t)kThreads / g.out_w;
             b.vec = (g.in_w % 8 == 0) && (((uintptr_t)x & 15u) == 0);
-            const uint32_t lds = b.lds_rows * b.pitch * 2;
-            // persistent blocks: up to 8 per CU (2048 threads) on every CU
-            const uint32_t blocks = (uint32_t)(items < kPoolBlocks ? items : kPoolBlocks);
-            const dim3 grid(blocks), block(kThreads);
+            b.div_w = make_fastdiv(g.in_w);
             const bool unit_dil = g.dh == 1 && g.dw == 1;
-            if (unit_dil && g.ph == 3 && g.pw == 3)
-                hipLaunchKernelGGL((pool_band<KIND, 3, 3>), grid, block, lds, s, x, y, g, b, inv_full);
-            else if (unit_dil && g.ph == 2 && g.pw == 2)
-                hipLaunchKernelGGL((pool_band<KIND, 2, 2>), grid, block, lds, s, x, y, g, b, inv_full);
-            else
-                hipLaunchKernelGGL((pool_band<KIND, 0, 0>), grid, block, lds, s, x, y, g, b, inv_full);
+            const uint32_t kwin = unit_dil && g.ph == g.pw && (g.ph == 2 || g.ph == 3) ? g.ph : 0;
+            const uint32_t sh = kwin && (g.sh == 1 || g.sh == 2) ? g.sh : 0;
+            b.alloc_rows = b.lds_rows + (sh ? (kStrip - 1) * sh : 0);
+            const uint32_t lds = b.alloc_rows * b.pitch * 2;
+            // persistent blocks: exactly as many as are resident at once (a block
+            // beyond that would start a second round and double the tail)
+#define CM_BAND(KW_, SH_)                                                                        \
+    do {                                                                                         \
+        const uint64_t cap = resident_blocks((const void*)pool_band<KIND, KW_, KW_, SH_>, lds);  \
+        const dim3 grid((uint32_t)(items < cap ? items : cap)), block(kThreads);                 \
+        hipLaunchKernelGGL((pool_band<KIND, KW_, KW_, SH_>), grid, block, lds, s, x, y, g, b,    \
+                           inv_full);                                                            \
+    } while (0)
+            if (kwin == 3) {
+                if (sh == 2) CM_BAND(3, 2); else if (sh == 1) CM_BAND(3, 1); else CM_BAND(3, 0);
+            } else if (kwin == 2) {
+                if (sh == 2) CM_BAND(2, 2); else if (sh == 1) CM_BAND(2, 1); else CM_BAND(2, 0);
+            } else {
+                CM_BAND(0, 0);
+            }
+#undef CM_BAND
             return cm_check_launch("pool_band");
         }
     }

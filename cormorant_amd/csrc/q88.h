@@ -80,19 +80,26 @@ __device__ __forceinline__ float acc_to_float(uint32_t acc) {
     return mul_rn((float)(int32_t)acc, 1.0f / 65536.0f);   // v_cvt_f32_i32 rounds to nearest even
 }
 
-// saturate_cast<Data_t>(AccData_t(f)): AccData_t(f) floors f to 2^-16 and wraps;
-// the >> 8 then floors to 2^-8.  For |f| < 32768 this is sat16(floor(f * 256)).
-// NaN / Inf (only reachable from a wrapped LP p=2 accumulator) give 0.
-__device__ __forceinline__ int16_t float_to_data(float f) {
+// saturate_cast<Data_t>(AccData_t(f)) for NaN / Inf / |f| >= 32768:
+// AccData_t(f) floors f to 2^-16 and wraps (keep the low 32 bits of the exact
+// value), then >> 8 and saturate.  NaN / Inf (only reachable from a wrapped
+// LP p=2 accumulator) give 0.
+__device__ __forceinline__ int16_t float_to_data_wide(float f) {
     if (!__builtin_isfinite(f)) return 0;
-    if (!(__builtin_fabsf(f) < 32768.0f)) {
-        // AP_WRAP of floor(f * 65536): keep the low 32 bits of the exact value.
-        const double s = __builtin_floor((double)f * 65536.0);
-        if (!(__builtin_fabs(s) < 9.2e18)) return 0;
-        return acc_to_data((uint32_t)(uint64_t)(int64_t)s);
-    }
-    const float s = __builtin_floorf(mul_rn(f, 256.0f));  // exact scale
-    return (int16_t)sat16((int32_t)s);
+    const double s = __builtin_floor((double)f * 65536.0);
+    if (!(__builtin_fabs(s) < 9.2e18)) return 0;
+    return acc_to_data((uint32_t)(uint64_t)(int64_t)s);
+}
+
+// saturate_cast<Data_t>(AccData_t(f)): for |f| < 32768 this is
+// sat16(floor(f * 256)) (the scale is exact); other values take the rare
+// path behind one branch, so the common case is straight-line code.
+__device__ __forceinline__ int16_t float_to_data(float f) {
+    // clamped into int32 range before the conversion (only matters off the fast path)
+    const float s = __builtin_amdgcn_fmed3f(__builtin_floorf(mul_rn(f, 256.0f)), -8388608.0f, 8388607.0f);
+    int16_t r = (int16_t)sat16((int32_t)s);
+    if (!(__builtin_fabsf(f) < 32768.0f)) r = float_to_data_wide(f);
+    return r;
 }
 
 // PoolingKernel.cpp:137, 259, 265: AccData_t((float)acc * (1.0f / denom)).
