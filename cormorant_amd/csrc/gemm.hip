@@ -194,6 +194,19 @@ struct ATile {
             }
         }
     }
+    // Vector path with per-thread offsets computed once (`base`: byte offset of
+    // vector q in the block's rows, kOob for rows past the end; `kc`: its k
+    // within the step) and the step's k0 as the load's scalar offset: per step
+    // only the k-bound test of the last, partial step costs vector work.
+    __device__ __forceinline__ void load_buf_fixed(__amdgpu_buffer_rsrc_t ra, const uint32_t (&base)[2],
+                                                   const uint32_t (&kc)[2], uint32_t k0, uint32_t krem) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const v4u v = __builtin_amdgcn_raw_buffer_load_b128(ra, kc[q] < krem ? base[q] : kOob,
+                                                                 (int)(k0 * 2u), 0);
+            w[4 * q + 0] = v[0]; w[4 * q + 1] = v[1]; w[4 * q + 2] = v[2]; w[4 * q + 3] = v[3];
+        }
+    }
     // Stores the limbs; hs / ls accumulate the sums of the high and low limbs
     // of this thread's values (sum a = 256*hs + ls + 128*count).
     __device__ __forceinline__ void store(bool vec, Planes& s, int32_t& hs, int32_t& ls) {
@@ -266,6 +279,16 @@ struct DenseBTile {
                         rb, ok ? ((kr + i) * (uint32_t)g.ldb + cr + q) * 2u : kOob, 0, 0);
                 }
             }
+        }
+    }
+    // Vector path with per-thread offsets computed once (`off`: byte offset of
+    // k row i of this thread in the step's resource, kOob past the last
+    // column); rows past K lie past the per-step resource and read as 0.
+    __device__ __forceinline__ void load_buf_fixed(__amdgpu_buffer_rsrc_t rb, const uint32_t (&off)[4]) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const v2u v = __builtin_amdgcn_raw_buffer_load_b64(rb, off[i], 0, 0);
+            w[i][0] = v[0]; w[i][1] = v[1];
         }
     }
     __device__ __forceinline__ void pack_raw() {
@@ -479,8 +502,25 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
             if constexpr (FOLD) tot[i][j] = v4i{0, 0, 0, 0};
         }
 
+    // vector buffer paths: per-thread load offsets, the same for every k step
+    uint32_t a_base[2], a_kc[2], b_off[4];
+    {
+        const uint32_t rel = threadIdx.x >> 2;
+        const bool rok = row0 + rel < g.rows;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            a_kc[q] = (threadIdx.x & 3) * 16 + q * 8;
+            a_base[q] = rok ? (rel * (uint32_t)g.lda + a_kc[q]) * 2u : kOob;
+        }
+        const uint32_t cr = (threadIdx.x >> 4) * 4, kr = (threadIdx.x & 15) * 4;
+        const bool cok = col0 + cr < g.cols;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) b_off[i] = cok ? ((kr + i) * (uint32_t)g.ldb + cr) * 2u : kOob;
+    }
     auto load_tile = [&](ATile& a, BTile& b, uint32_t k0) {
-        if constexpr (BUF) a.template load_buf<AV == 1>(g, arsrc, row0, k0);
+        if constexpr (BUF && AV == 1)
+            a.load_buf_fixed(arsrc, a_base, a_kc, k0, k0 < g.k ? g.k - k0 : 0u);
+        else if constexpr (BUF) a.template load_buf<false>(g, arsrc, row0, k0);
         else a.load(g, abase, row0, k0);
         if constexpr (MODE == B_CONV_TAB) {
             b.load_tab(g, k0, tab, xrsrc);
@@ -490,10 +530,10 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
             // k0 may lie past the last step (see the main loop): an empty resource
             const uint32_t kr = k0 >= g.k ? 0u : (g.k - k0 < (uint32_t)BK ? g.k - k0 : (uint32_t)BK);
             const uint32_t cr = g.cols - col0 < (uint32_t)BN ? g.cols - col0 : (uint32_t)BN;
-            b.template load_buf<BV == 1>(
-                g, make_rsrc(bbase + (uint64_t)(kr ? k0 : 0u) * g.ldb + col0,
-                             kr ? ((kr - 1) * (uint32_t)g.ldb + cr) * 2u : 0u),
-                col0, k0);
+            const __amdgpu_buffer_rsrc_t rb = make_rsrc(bbase + (uint64_t)(kr ? k0 : 0u) * g.ldb + col0,
+                                                        kr ? ((kr - 1) * (uint32_t)g.ldb + cr) * 2u : 0u);
+            if constexpr (BV == 1) b.load_buf_fixed(rb, b_off);
+            else b.template load_buf<false>(g, rb, col0, k0);
         } else {
             b.load(g, bbase, col0, k0);
         }
