@@ -155,18 +155,33 @@ def live_intervals(graph: OnnxGraph, live_from: Optional[Dict[str, int]] = None
                    ) -> Dict[str, Tuple[int, int]]:
     """(producing node index, last consuming node index) of each non-alias intermediate.
 
+    A read of a reshape alias (Reshape / Squeeze / Unsqueeze / Dropout output)
+    counts as a read of the tensor it aliases: the alias IS that storage.  The
+    reference's interval (_core.py:270-296) counts only direct readers, so a
+    tensor produced between the reshape and the alias's reader may be given the
+    source's slot and overwrite it; extending the interval keeps that from
+    happening (it only changes slot offsets, never a kernel argument).
+
     ``live_from`` moves the start of some intermediates earlier (a backend that
     writes a tensor from an earlier node, e.g. a fused epilogue)."""
     aliases = reshape_aliases(graph)
     names = {t.onnx_name for t in graph.intermediate_tensors if t.onnx_name not in aliases}
+
+    def root(n: str) -> str:
+        seen = 0
+        while n in aliases and seen <= len(aliases):
+            n, seen = aliases[n], seen + 1
+        return n
+
     first: Dict[str, int] = {}
     last: Dict[str, int] = {}
     for i, sn in enumerate(graph.nodes):
         if sn.output.onnx_name in names:
             first[sn.output.onnx_name] = i
         for t in sn.inputs:
-            if t.onnx_name in names:
-                last[t.onnx_name] = i
+            r = root(t.onnx_name)
+            if r in names:
+                last[r] = i
     if live_from:
         for n, i in live_from.items():
             if n in first:

@@ -609,3 +609,24 @@ def test_fused_launches_mobilenet_small():
     oracle.set_threads(min(os.cpu_count() or 1, 8))
     got = gs.run_plan(plan, {"X": x}, launches=seq)["Y"]
     np.testing.assert_array_equal(got, gs.run_plan(BufferPlan(g), {"X": x})["Y"])
+
+
+def test_alias_reader_extends_source_lifetime():
+    """A tensor read through a reshape alias after the reshape node stays live
+    until that read: a tensor produced in between must not take its slot."""
+    N = ox.make_node
+    shp = ox.from_array(np.array([8], np.int64), "shp")
+    nodes = [N("Relu", ["X"], ["A"]),                 # 0
+             N("Reshape", ["A", "shp"], ["R"]),       # 1: R aliases A
+             N("Reshape", ["X", "shp"], ["XR"]),      # 2: alias of the graph input
+             N("Mul", ["XR", "XR"], ["B"]),           # 3: produced after A's last direct reader
+             N("Add", ["R", "B"], ["Y"])]             # 4: reads A through R
+    g = graph(ox.make_model(ox.make_graph(nodes, "alias_life", [ox.value_info("X", [2, 4])],
+                                          [ox.value_info("Y", [8])], [shp])))
+    iv = live_intervals(g)
+    assert iv["A"] == (0, 4) and iv["B"] == (3, 4)
+    plan = BufferPlan(g)
+    assert plan.storage["A"].offset != plan.storage["B"].offset
+    x = wl.uniform_q88(wl.rng(65), (2, 4), -4.0, 4.0)
+    np.testing.assert_array_equal(gs.run_plan(plan, {"X": x}, threads=False)["Y"],
+                                  gs.simulate_raw(g, {"X": x})["Y"])
