@@ -64,6 +64,164 @@ __global__ __launch_bounds__(kThreads) void conv_depthwise(const int16_t* __rest
     }
 }
 
+// ------------------------------------------------------------------ direct --
+// Standard convolution with few output channels on the vector ALUs.  The
+// int8-limb MFMA path works on 128 output channels x 128 pixels per block;
+// with 16-32 output channels most of that tile is empty, and each block's
+// fixed costs (operand staging, LDS round trips, the epilogue) dominate.  Here
+// a thread owns one output pixel (flattened over the images) and MT output
+// channels: it walks k = (c, kh, kw) two at a time, gathers the two input values
+// (one buffer load each, padding taps are sent out of the buffer range and read
+// 0), and accumulates w*x for all MT channels with v_dot2 (int16 x int16 pairs
+// into the int32 accumulator, wrapping mod 2^32 like the reference's).
+// Weights of the block's MT channels sit in LDS as [k pair][MT] words (read as
+// a broadcast), next to a per-k table of input byte offsets and tap numbers.
+constexpr int kDirThreads = 256;
+constexpr uint32_t kDirChunk = 8;   // k values gathered per load batch
+
+struct DirArgs {
+    const int16_t* x;
+    const int16_t* w;
+    const int16_t* bias;
+    int16_t* y;
+    uint32_t M, H, W, P, OW, kh, kw, sh, sw, dh, dw, pt, pl;
+    uint32_t K, Kc;          // C*kh*kw; K rounded up to 2*kDirChunk
+    uint32_t npix;           // batch * P
+    uint32_t x_bytes;        // whole input tensor, < 2^31
+    uint32_t x_img;          // C*H*W
+    uint64_t y_img;          // M*P
+    FastDiv div_p, div_ow, div_kk, div_kw;
+    EpiArgs epi;
+};
+
+typedef short v2s __attribute__((ext_vector_type(2)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t dot2(uint32_t x, uint32_t w, uint32_t acc) {
+    return (uint32_t)__builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, x), __builtin_bit_cast(v2s, w),
+                                            (int)acc, false);
+}
+
+template <int MT, bool HAS_BIAS>
+__global__ __launch_bounds__(kDirThreads) void conv_direct(DirArgs g) {
+    extern __shared__ __align__(16) uint32_t dsm[];
+    uint32_t* wt = dsm;                                          // [Kc / 2][MT]
+    int2* tab = reinterpret_cast<int2*>(dsm + (g.Kc / 2) * MT);   // [Kc + kDirChunk]
+    const uint32_t m0 = blockIdx.y * MT;
+    const uint32_t kk = g.kh * g.kw, hw = g.H * g.W;
+    // k >= K (padding up to Kc, and one chunk past it that the last prefetch
+    // reads) is tap 31, which every thread treats as outside the image
+    for (uint32_t k = threadIdx.x; k < g.Kc + kDirChunk; k += kDirThreads) {
+        const uint32_t c = fdiv(k, g.div_kk), r = k - c * kk;
+        const uint32_t khi = fdiv(r, g.div_kw), kwi = r - khi * g.kw;
+        tab[k] = k < g.K ? int2{(int)(2u * (c * hw + khi * g.dh * g.W + kwi * g.dw)), (int)r}
+                         : int2{0, 31};
+    }
+    for (uint32_t i = threadIdx.x; i < (g.Kc / 2) * MT; i += kDirThreads) {
+        const uint32_t kp = i / MT, mm = i - kp * MT;
+        const uint32_t m = m0 + mm, k = 2 * kp;
+        uint32_t lo = 0, hi = 0;
+        if (m < g.M) {
+            const int16_t* wm = g.w + (uint64_t)m * g.K;
+            if (k < g.K) lo = (uint16_t)wm[k];
+            if (k + 1 < g.K) hi = (uint16_t)wm[k + 1];
+        }
+        wt[i] = lo | hi << 16;
+    }
+
+    const uint32_t pix = blockIdx.x * kDirThreads + threadIdx.x;
+    const bool pok = pix < g.npix;
+    const uint32_t n = pok ? fdiv(pix, g.div_p) : 0u;
+    const uint32_t p = pok ? pix - n * g.P : 0u;
+    const uint32_t oh = fdiv(p, g.div_ow), ow = p - oh * g.OW;
+    const int32_t ih0 = (int32_t)(oh * g.sh) - (int32_t)g.pt;
+    const int32_t iw0 = (int32_t)(ow * g.sw) - (int32_t)g.pl;
+    uint32_t holes = 0x80000000u;   // bit r: tap r of this pixel's window is padding
+    for (uint32_t r = 0; r < kk; ++r) {
+        const uint32_t khi = fdiv(r, g.div_kw), kwi = r - khi * g.kw;
+        const int32_t ih = ih0 + (int32_t)(khi * g.dh), iw = iw0 + (int32_t)(kwi * g.dw);
+        const bool in = pok && ih >= 0 && ih < (int32_t)g.H && iw >= 0 && iw < (int32_t)g.W;
+        holes |= in ? 0u : 1u << r;
+    }
+    // byte offset of the window origin (negative when it starts in the padding;
+    // only taps inside the image are ever added to it unmasked)
+    const int32_t pbyte = 2 * ((int32_t)(n * g.x_img) + ih0 * (int32_t)g.W + iw0);
+    const __amdgpu_buffer_rsrc_t rsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<int16_t*>(g.x), (short)0, (int)g.x_bytes, 0x00020000);
+    __syncthreads();
+
+    uint32_t acc[MT];
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm) acc[mm] = 0u;
+    auto load_chunk = [&](uint32_t k0, uint32_t (&xv)[kDirChunk]) {
+#pragma unroll
+        for (uint32_t q = 0; q < kDirChunk; ++q) {
+            const int2 t = tab[k0 + q];
+            const uint32_t off = (((holes >> t.y) & 1u) << 31) | (uint32_t)(pbyte + t.x);
+            xv[q] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, 0);
+        }
+    };
+    auto compute_chunk = [&](uint32_t k0, const uint32_t (&xv)[kDirChunk]) {
+#pragma unroll
+        for (uint32_t q = 0; q < kDirChunk / 2; ++q) {
+            const uint32_t xp = xv[2 * q] | xv[2 * q + 1] << 16;
+            const uint32_t* wr = wt + (k0 / 2 + q) * MT;
+#pragma unroll
+            for (int mm = 0; mm < MT; mm += 4) {
+                const v4u wv = *reinterpret_cast<const v4u*>(wr + mm);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) acc[mm + e] = dot2(xp, wv[e], acc[mm + e]);
+            }
+        }
+    };
+    // two gather batches in flight: the next one loads while this one computes
+    // (loads are unconditional; the batch past the end reads only padding)
+    uint32_t xa[kDirChunk], xb[kDirChunk];
+    load_chunk(0, xa);
+    for (uint32_t k0 = 0; k0 < g.Kc; k0 += 2 * kDirChunk) {
+        load_chunk(k0 + kDirChunk, xb);
+        __builtin_amdgcn_sched_barrier(0);   // keep the loads ahead of the compute
+        compute_chunk(k0, xa);
+        load_chunk(k0 + 2 * kDirChunk, xa);
+        __builtin_amdgcn_sched_barrier(0);
+        compute_chunk(k0 + kDirChunk, xb);
+    }
+
+    if (!pok) return;
+    const int32_t lo = q88::act_lo(g.epi.act), hi = q88::act_hi(g.epi.act);
+    const uint64_t ybase = (uint64_t)n * g.y_img + p;
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm) {
+        const uint32_t m = m0 + mm;
+        if (m >= g.M) break;
+        uint32_t v = acc[mm];
+        if (HAS_BIAS) v += q88::data_to_acc(g.bias[m]);
+        int32_t yv = q88::acc_to_data(v);
+        const uint64_t o = ybase + (uint64_t)m * g.P;
+        if (g.epi.add_mode == 1u) yv = q88::add(yv, g.epi.add[o]);
+        g.y[o] = (int16_t)q88::clamp(yv, lo, hi);
+    }
+}
+
+// Output channels per thread for the direct path, or 0 when the MFMA path
+// suits the shape better.  The direct path pays per multiply-add (v_dot2 plus
+// a broadcast LDS read of the weights), the MFMA path per 128 x 128 tile; the
+// direct one wins for few output channels with a short k range (e.g. a 3-channel
+// stem, 1x1 convolutions of 16-32 channels) over enough pixels to fill the GPU.
+uint32_t direct_channels(uint64_t K, uint32_t out_ch, uint32_t kk, uint64_t npix, uint64_t x_bytes) {
+    if (out_ch > 32 || K > 32 || npix < 32768 || kk > 31 || x_bytes >= 0x80000000ull) return 0;
+    return out_ch <= 8 ? 8 : out_ch <= 16 ? 16 : out_ch <= 24 ? 24 : 32;
+}
+
+template <int MT>
+int launch_direct(const DirArgs& g, hipStream_t s) {
+    const dim3 grid((g.npix + kDirThreads - 1) / kDirThreads, (g.M + MT - 1) / MT);
+    const size_t lds = (size_t)(g.Kc / 2) * MT * 4u + (size_t)(g.Kc + kDirChunk) * 8u;
+    if (g.bias) hipLaunchKernelGGL((conv_direct<MT, true>), grid, dim3(kDirThreads), lds, s, g);
+    else hipLaunchKernelGGL((conv_direct<MT, false>), grid, dim3(kDirThreads), lds, s, g);
+    return cm_check_launch("conv_direct");
+}
+
 }  // namespace
 
 int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
@@ -82,6 +240,34 @@ int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int1
         if (b) hipLaunchKernelGGL(conv_depthwise<true>, grid, dim3(kThreads), 0, s, x, w, b, y, g, total, ea);
         else hipLaunchKernelGGL(conv_depthwise<false>, grid, dim3(kThreads), 0, s, x, w, b, y, g, total, ea);
         return cm_check_launch("conv_depthwise");
+    }
+    const uint64_t K = (uint64_t)in_ch * kh * kw;
+    const uint64_t x_bytes = 2ull * in_ch * in_h * in_w * batch;
+    const uint64_t npix = (uint64_t)batch * out_h * out_w;
+    if (const uint32_t mt = direct_channels(K, out_ch, kh * kw, npix, x_bytes)) {
+        if (npix == 0 || out_ch == 0) return CM_OK;
+        if (npix > 0x7FFFFFFFull) return cm_set_error(CM_ERR_RANGE, "conv: shape exceeds 32-bit indexing");
+        DirArgs g{};
+        g.x = x; g.w = w; g.bias = b; g.y = y;
+        g.M = out_ch; g.H = in_h; g.W = in_w; g.P = out_h * out_w; g.OW = out_w;
+        g.kh = kh; g.kw = kw; g.sh = sh; g.sw = sw; g.dh = dh; g.dw = dw; g.pt = pad_top; g.pl = pad_left;
+        g.K = (uint32_t)K;
+        g.Kc = (uint32_t)((K + 2 * kDirChunk - 1) / (2 * kDirChunk) * (2 * kDirChunk));
+        g.npix = (uint32_t)npix;
+        g.x_bytes = (uint32_t)x_bytes;
+        g.x_img = in_ch * in_h * in_w;
+        g.y_img = (uint64_t)out_ch * out_h * out_w;
+        g.div_p = make_fastdiv(g.P);
+        g.div_ow = make_fastdiv(out_w);
+        g.div_kk = make_fastdiv(kh * kw);
+        g.div_kw = make_fastdiv(kw);
+        g.epi = ea;
+        switch (mt) {
+            case 8: return launch_direct<8>(g, s);
+            case 16: return launch_direct<16>(g, s);
+            case 24: return launch_direct<24>(g, s);
+            default: return launch_direct<32>(g, s);
+        }
     }
     // 1x1 / stride 1 / no padding as one GEMM per image, when an image's
     // pixels fill its 128-column tiles to at least 80 %; small planes (e.g.

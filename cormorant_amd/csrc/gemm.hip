@@ -65,9 +65,14 @@ struct GemmArgs {
     FastDiv div_p, div_ow, div_kk, div_kw;   // divisions by P, OW, kh*kw, kw
     uint32_t x_bytes;            // table mode: size of the whole input tensor, < 2^31
     EpiArgs epi;                 // fused Add / Relu / Clip; add_mode 1 follows C's layout
+    // output (and add tensor) accesses of `out_w` elements at a time keep their
+    // alignment and stay inside one image: out_w divides ldc / c_bs (dense) or
+    // P (conv) and both base pointers are aligned to 2*out_w bytes
+    uint32_t out_w;
     // split-K: blockIdx.z selects k steps [z*split_steps, +split_steps) and the
-    // block stores its partial sums (no bias) to ws[z][row][col]; 0 = no split
-    uint32_t split_steps;
+    // block stores its partial sums (no bias) to ws[z][row][0..ws_ld); ws_ld is
+    // cols rounded up to 8; 0 = no split
+    uint32_t split_steps, ws_ld;
     uint32_t* ws;
 };
 
@@ -109,8 +114,15 @@ struct Planes {
     uint8_t b_lo[BN * kStride];
 };
 
+// Epilogue tile: the block's 128 x 128 raw sums, rows padded to 132 words so
+// the four row groups of an MFMA result write fall into different bank halves.
+constexpr int kTilePitch = 132;
+
 struct Smem {
-    Planes st[2];
+    union {
+        Planes st[2];                        // main loop
+        uint32_t tile[BM * kTilePitch];      // epilogue (after the last k step)
+    };
     uint32_t row_sum[BM];
     uint32_t col_sum[BN];
     int32_t bias[BM];      // bias << 8 of the block's rows (0 past the last row)
@@ -333,6 +345,63 @@ __device__ __forceinline__ void publish_dense(Smem& s, const int32_t (&hs)[4], c
 #pragma unroll
     for (int j = 0; j < 4; ++j)
         atomicAdd(&s.col_sum[cl + j], 256u * (uint32_t)hs[j] + (uint32_t)ls[j] + 128u * count);
+}
+
+// Eight int16 values of one output row at element offsets oc[0..7] from p:
+// w-wide accesses (w = 8, 4, 2; runs of w columns are contiguous and aligned)
+// when all eight columns exist, else one element per existing column (n < 8).
+__device__ __forceinline__ void store8(int16_t* p, const uint64_t (&oc)[8], uint32_t n, uint32_t w,
+                                       const int32_t (&y)[8]) {
+    if (n == 8u && w == 8u) {
+        *reinterpret_cast<v4u*>(p + oc[0]) = v4u{pack(y[0], y[1]), pack(y[2], y[3]),
+                                                 pack(y[4], y[5]), pack(y[6], y[7])};
+    } else if (n == 8u && w == 4u) {
+        *reinterpret_cast<v2u*>(p + oc[0]) = v2u{pack(y[0], y[1]), pack(y[2], y[3])};
+        *reinterpret_cast<v2u*>(p + oc[4]) = v2u{pack(y[4], y[5]), pack(y[6], y[7])};
+    } else if (n == 8u && w == 2u) {
+#pragma unroll
+        for (int q = 0; q < 8; q += 2) *reinterpret_cast<uint32_t*>(p + oc[q]) = pack(y[q], y[q + 1]);
+    } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            if ((uint32_t)q < n) p[oc[q]] = (int16_t)y[q];
+    }
+}
+
+// Adds the int16 values at the same offsets (the fused Add's tensor) to a[].
+__device__ __forceinline__ void load8(const int16_t* p, const uint64_t (&oc)[8], uint32_t n, uint32_t w,
+                                      int32_t (&a)[8]) {
+    int32_t x[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (n == 8u && w == 8u) {
+        const v4u v = *reinterpret_cast<const v4u*>(p + oc[0]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            x[2 * q] = (int32_t)(int16_t)(v[q] & 0xFFFFu);
+            x[2 * q + 1] = (int32_t)v[q] >> 16;
+        }
+    } else if (n == 8u && w == 4u) {
+        const v2u v0 = *reinterpret_cast<const v2u*>(p + oc[0]);
+        const v2u v1 = *reinterpret_cast<const v2u*>(p + oc[4]);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            x[2 * q] = (int32_t)(int16_t)(v0[q] & 0xFFFFu);
+            x[2 * q + 1] = (int32_t)v0[q] >> 16;
+            x[2 * q + 4] = (int32_t)(int16_t)(v1[q] & 0xFFFFu);
+            x[2 * q + 5] = (int32_t)v1[q] >> 16;
+        }
+    } else if (n == 8u && w == 2u) {
+#pragma unroll
+        for (int q = 0; q < 8; q += 2) {
+            const uint32_t v = *reinterpret_cast<const uint32_t*>(p + oc[q]);
+            x[q] = (int32_t)(int16_t)(v & 0xFFFFu);
+            x[q + 1] = (int32_t)v >> 16;
+        }
+    } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) x[q] = p[oc[(uint32_t)q < n ? q : 0]];
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) a[q] += x[q];
 }
 
 // ------------------------------------------------------- im2col B tile --
@@ -573,7 +642,14 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
             __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
         }
     };
+    // convolution: a wave whose 64 rows all lie past the last output channel
+    // (M <= 64) has no MFMA work and only helps stage the tiles (a uniform
+    // branch; the dense GEMM keeps the straight-line step, which schedules better)
+    const bool wave_rows = row0 + wrow < g.rows;
     auto mfma_step = [&](const Planes& p, uint32_t it) {
+        if constexpr (CONV) {
+            if (!wave_rows) return;
+        }
         const uint32_t koff = (lane >> 4) * 16;
         v4i ah[TI], al[TI];
 #pragma unroll
@@ -663,118 +739,162 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
         atomicAdd(&s.col_sum[threadIdx.x & 127], 256u * (uint32_t)chs + (uint32_t)cls + 128u * 16u * nk);
     else
         publish_dense(s, dhs, dls, 4u * nk);
-    __syncthreads();
+    __syncthreads();   // every wave is past its last plane read: the tile may overwrite them
 
-    // Epilogue: every value is computed, and every residual read issued, without
-    // a lane-dependent branch (out-of-range outputs read element 0 of the Add
-    // tensor and are not stored), so the reads are all in flight together.
-    const uint32_t kp_term = 16384u * (nk * (uint32_t)BK);
-    int16_t* cptr = g.c + (CONV ? 0 : (uint64_t)blockIdx.z * g.c_bs);
-    const int16_t* rptr = g.epi.add + (CONV ? 0 : (uint64_t)blockIdx.z * g.c_bs);
-    // MFMA tiles wholly past the last row or column are skipped (wave-uniform)
+    // Epilogue, phase 1: each wave's MFMA sums (limb terms combined mod 2^32)
+    // into the LDS tile, in the MFMA result layout (lane = column, 4 rows each).
 #pragma unroll
-    for (int j = 0; j < TJ; ++j) {
-        if (col0 + wcol + j * 16 >= g.cols) continue;
-        const uint32_t cl = wcol + j * 16 + (lane & 15);
-        const uint32_t col = col0 + cl;
-        const bool cok = col < g.cols;
-        const uint64_t coff = CONV ? s.coff[cl] : (uint64_t)col;
-        const uint64_t rstride = CONV ? (uint64_t)g.P : g.ldc;
-        const uint32_t csum = s.col_sum[cl];
-        if (g.ws) {   // split-K partial: raw sums, bias and epilogue in split_reduce
-            uint32_t* wp = g.ws + (uint64_t)blockIdx.z * g.rows * g.cols + col;
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-            for (int i = 0; i < TI; ++i) {
-                if (row0 + wrow + i * 16 >= g.rows) continue;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t rl = wrow + i * 16 + (lane >> 4) * 4 + e;
-                    uint32_t v = ((uint32_t)hh[i][j][e] << 16) + ((uint32_t)mid[i][j][e] << 8) +
-                                 (uint32_t)ll[i][j][e];
-                    v += 128u * (s.row_sum[rl] + csum) - kp_term;
-                    if (cok && row0 + rl < g.rows) wp[(uint64_t)(row0 + rl) * g.cols] = v;
-                }
-            }
-            continue;
-        }
-        const int32_t cadd = g.epi.add_mode == 2u ? (int32_t)g.epi.add[cok ? col : 0u] : 0;
-#pragma unroll
-        for (int i = 0; i < TI; ++i) {
-            if (row0 + wrow + i * 16 >= g.rows) continue;
-            int32_t yv[4];
-            uint64_t ov[4];
+        for (int j = 0; j < TJ; ++j)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const uint32_t rl = wrow + i * 16 + (lane >> 4) * 4 + e;
-                const bool ok = cok && row0 + rl < g.rows;
                 uint32_t v = ((uint32_t)hh[i][j][e] << 16) + ((uint32_t)mid[i][j][e] << 8) +
                              (uint32_t)ll[i][j][e];
                 if constexpr (FOLD) v += (uint32_t)tot[i][j][e];
-                v += 128u * (s.row_sum[rl] + csum) - kp_term;
-                if constexpr (HAS_BIAS) v += (uint32_t)s.bias[rl];
-                ov[e] = ok ? coff + (uint64_t)(row0 + rl) * rstride : ~0ull;
-                yv[e] = q88::acc_to_data(v);
+                s.tile[(wrow + i * 16 + (lane >> 4) * 4 + e) * kTilePitch + wcol + j * 16 + (lane & 15)] = v;
             }
-            if (g.epi.add_mode == 1u) {
+    __syncthreads();
+
+    // Phase 2, row-major: thread t finishes columns [c8, c8 + 8) of rows rb, rb + 32,
+    // rb + 64, rb + 96 (16 threads cover a row): sum corrections, bias, saturation,
+    // the fused Add and activation, then one store of the 8 values (or out_w-wide
+    // pieces).  Activation and Add mode are applied without a per-value branch.
+    const uint32_t c8 = (threadIdx.x & 15) * 8, rb = threadIdx.x >> 4;
+    const uint32_t cbase = col0 + c8;
+    if (cbase >= g.cols) return;
+    const uint32_t kp_term = 16384u * (nk * (uint32_t)BK);
+    uint32_t cterm[8];   // 128 * column sum - 16384 * Kp
+    {
+        const v4u c0 = *reinterpret_cast<const v4u*>(&s.col_sum[c8]);
+        const v4u c1 = *reinterpret_cast<const v4u*>(&s.col_sum[c8 + 4]);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) yv[e] = q88::add(yv[e], rptr[ov[e] == ~0ull ? 0 : ov[e]]);
-            } else if (g.epi.add_mode == 2u) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) yv[e] = q88::add(yv[e], cadd);
-            }
-#pragma unroll
-            for (int e = 0; e < 4; ++e)
-                if (ov[e] != ~0ull) cptr[ov[e]] = (int16_t)q88::epi_act(yv[e], g.epi.act);
+        for (int q = 0; q < 4; ++q) {
+            cterm[q] = 128u * c0[q] - kp_term;
+            cterm[q + 4] = 128u * c1[q] - kp_term;
         }
+    }
+    auto tile_row = [&](uint32_t r, uint32_t (&v)[8]) {
+        const v4u t0 = *reinterpret_cast<const v4u*>(&s.tile[r * kTilePitch + c8]);
+        const v4u t1 = *reinterpret_cast<const v4u*>(&s.tile[r * kTilePitch + c8 + 4]);
+        const uint32_t rs = 128u * s.row_sum[r] + (HAS_BIAS ? (uint32_t)s.bias[r] : 0u);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            v[q] = t0[q] + cterm[q] + rs;
+            v[q + 4] = t1[q] + cterm[q + 4] + rs;
+        }
+    };
+    if (g.ws) {   // split-K partial: raw sums; bias and epilogue in split_reduce
+        uint32_t* wp = g.ws + (uint64_t)blockIdx.z * g.rows * g.ws_ld + cbase;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const uint32_t r = rb + rr * 32;
+            if (row0 + r >= g.rows) break;
+            uint32_t v[8];
+            tile_row(r, v);
+            uint32_t* p = wp + (uint64_t)(row0 + r) * g.ws_ld;   // ws_ld >= cbase + 8
+            *reinterpret_cast<v4u*>(p) = v4u{v[0], v[1], v[2], v[3]};
+            *reinterpret_cast<v4u*>(p + 4) = v4u{v[4], v[5], v[6], v[7]};
+        }
+        return;
+    }
+    const uint32_t ncol = g.cols - cbase < 8u ? g.cols - cbase : 8u;
+    const int32_t lo = q88::act_lo(g.epi.act), hi = q88::act_hi(g.epi.act);
+    int32_t cadd[8] = {0, 0, 0, 0, 0, 0, 0, 0};   // Add of one value per column
+    if (g.epi.add_mode == 2u) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) cadd[q] = g.epi.add[cbase + ((uint32_t)q < ncol ? q : 0)];
+    }
+    uint64_t ocol[8];   // output offset of each column in row 0 of the output
+#pragma unroll
+    for (int q = 0; q < 8; ++q) ocol[q] = CONV ? s.coff[c8 + q] : (uint64_t)(cbase + q);
+    const uint64_t rstride = CONV ? (uint64_t)g.P : g.ldc;
+    int16_t* cptr = g.c + (CONV ? 0 : (uint64_t)blockIdx.z * g.c_bs);
+    const int16_t* rptr = g.epi.add + (CONV ? 0 : (uint64_t)blockIdx.z * g.c_bs);
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+        const uint32_t r = rb + rr * 32;
+        if (row0 + r >= g.rows) break;
+        const uint64_t ro = (uint64_t)(row0 + r) * rstride;
+        int32_t add[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) add[q] = cadd[q];
+        if (g.epi.add_mode == 1u) load8(rptr + ro, ocol, ncol, g.out_w, add);
+        uint32_t v[8];
+        tile_row(r, v);
+        int32_t y[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) y[q] = q88::clamp(q88::add(q88::acc_to_data(v[q]), add[q]), lo, hi);
+        store8(cptr + ro, ocol, ncol, g.out_w, y);
     }
 }
 
-// Split-K second pass: sums the partials of one output element over the
-// splits, adds the bias, saturates, applies the epilogue and stores the value
-// in the MatMul ([rows][ldc]) or convolution (NCHW) output layout.
+// Split-K second pass: sums the partials of four neighbouring elements of one
+// output row over the splits, adds the bias, saturates, applies the epilogue
+// and stores the values in the MatMul ([rows][ldc]) or convolution (NCHW)
+// output layout.
 constexpr int kReduceThreads = 256;
 constexpr uint32_t kMaxSplits = 16;
+
+struct ReduceArgs {
+    const uint32_t* ws;      // [splits][rows][ws_ld]
+    uint32_t rows, cols, ws_ld;
+    FastDiv div_q;           // division by ws_ld / 4 (chunks per row)
+    const int16_t* bias;
+    int16_t* y;
+    uint32_t conv, P;
+    FastDiv div_p;
+    uint64_t y_img, ldc;
+    EpiArgs epi;
+};
 
 // SPLITS is a template parameter so the partial loads are unrolled and all in
 // flight at once (a run-time trip count would wait for each in turn).
 template <uint32_t SPLITS>
-__global__ __launch_bounds__(kReduceThreads) void split_reduce(
-        const uint32_t* __restrict__ ws, uint32_t rows, uint32_t cols,
-        const int16_t* __restrict__ bias, int16_t* __restrict__ y, uint32_t conv, uint32_t P,
-        uint64_t y_img, uint64_t ldc, EpiArgs epi) {
-    const uint64_t n = (uint64_t)rows * cols;
-    for (uint64_t idx = (uint64_t)blockIdx.x * kReduceThreads + threadIdx.x; idx < n;
-         idx += (uint64_t)gridDim.x * kReduceThreads) {
-        const uint32_t row = (uint32_t)(idx / cols);
-        const uint32_t col = (uint32_t)(idx - (uint64_t)row * cols);
-        uint32_t part[SPLITS];
+__global__ __launch_bounds__(kReduceThreads) void split_reduce(ReduceArgs a) {
+    const uint32_t nq = a.ws_ld / 4u;
+    const uint32_t total = a.rows * nq;     // < 2^24: the workspace holds at most 64 MiB
+    const uint64_t zs = (uint64_t)a.rows * a.ws_ld;
+    const int32_t lo = q88::act_lo(a.epi.act), hi = q88::act_hi(a.epi.act);
+    for (uint32_t idx = blockIdx.x * kReduceThreads + threadIdx.x; idx < total;
+         idx += gridDim.x * kReduceThreads) {
+        const uint32_t row = fdiv(idx, a.div_q);
+        const uint32_t c4 = (idx - row * nq) * 4u;
+        if (c4 >= a.cols) continue;
+        const uint32_t* src = a.ws + (uint64_t)row * a.ws_ld + c4;
+        v4u part[SPLITS];
 #pragma unroll
-        for (uint32_t z = 0; z < SPLITS; ++z) part[z] = __builtin_nontemporal_load(ws + z * n + idx);
-        uint32_t v = bias ? (uint32_t)(int32_t)bias[row] << 8 : 0u;
+        for (uint32_t z = 0; z < SPLITS; ++z)
+            part[z] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(src + z * zs));
+        const uint32_t b = a.bias ? (uint32_t)(int32_t)a.bias[row] << 8 : 0u;
+        v4u v = v4u{b, b, b, b};
 #pragma unroll
         for (uint32_t z = 0; z < SPLITS; ++z) v += part[z];
-        uint64_t o;
-        if (conv) {
-            const uint32_t img = col / P;
-            o = (uint64_t)img * y_img + (uint64_t)row * P + (col - img * P);
-        } else {
-            o = (uint64_t)row * ldc + col;
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+            const uint32_t col = c4 + q;
+            if (col >= a.cols) break;
+            uint64_t o;
+            if (a.conv) {
+                const uint32_t img = fdiv(col, a.div_p);
+                o = (uint64_t)img * a.y_img + (uint64_t)row * a.P + (col - img * a.P);
+            } else {
+                o = (uint64_t)row * a.ldc + col;
+            }
+            int32_t yv = q88::acc_to_data(v[q]);
+            if (a.epi.add_mode) yv = q88::add(yv, a.epi.add[a.epi.add_mode == 1u ? o : (uint64_t)col]);
+            a.y[o] = (int16_t)q88::clamp(yv, lo, hi);
         }
-        int32_t yv = q88::acc_to_data(v);
-        if (epi.add_mode == 1u) yv = q88::add(yv, epi.add[o]);
-        else if (epi.add_mode == 2u) yv = q88::add(yv, epi.add[col]);
-        y[o] = (int16_t)q88::epi_act(yv, epi.act);
     }
 }
 
 template <uint32_t S>
-int launch_reduce(uint32_t splits, dim3 grid, hipStream_t s, const GemmArgs& g, uint32_t conv) {
+int launch_reduce(uint32_t splits, dim3 grid, hipStream_t s, const ReduceArgs& r) {
     if constexpr (S > kMaxSplits) {
         return cm_set_error(CM_ERR_INVALID, "split_reduce: %u splits", splits);
     } else {
-        if (splits != S) return launch_reduce<S + 1>(splits, grid, s, g, conv);
-        hipLaunchKernelGGL(split_reduce<S>, grid, dim3(kReduceThreads), 0, s, g.ws, g.rows, g.cols,
-                           g.bias, g.c, conv, g.P, g.y_img, g.ldc, g.epi);
+        if (splits != S) return launch_reduce<S + 1>(splits, grid, s, r);
+        hipLaunchKernelGGL(split_reduce<S>, grid, dim3(kReduceThreads), 0, s, r);
         return cm_check_launch("split_reduce");
     }
 }
@@ -843,10 +963,12 @@ int launch_gemm(GemmArgs& g0, uint32_t zdim, hipStream_t s, const char* name) {
         if (splits > 1) {
             const uint32_t sps = (nk_all + splits - 1) / splits;
             splits = (nk_all + sps - 1) / sps;
-            const size_t bytes = (size_t)splits * g.rows * g.cols * 4u;
+            const uint32_t ws_ld = (g.cols + 7u) & ~7u;
+            const size_t bytes = (size_t)splits * g.rows * ws_ld * 4u;
             uint32_t* ws = bytes <= kWsMax ? split_workspace(s, bytes) : nullptr;
             if (ws) {
                 g.split_steps = sps;
+                g.ws_ld = ws_ld;
                 g.ws = ws;
                 g.a_bs = g.b_bs = g.c_bs = 0;
                 grid.z = splits;
@@ -856,6 +978,17 @@ int launch_gemm(GemmArgs& g0, uint32_t zdim, hipStream_t s, const char* name) {
         }
     }
     const bool bias = g.bias != nullptr && splits == 1;
+    // widest output / Add access that keeps alignment and stays in one image row run
+    g.out_w = 8;
+    const bool add_same = g.epi.add_mode == 1u;
+    while (g.out_w > 1u) {
+        const uint32_t w = g.out_w;
+        const bool ok = (MODE == B_DENSE ? g.ldc % w == 0 && (grid.z == 1 || g.c_bs % w == 0)
+                                         : g.P % w == 0) &&
+                        aligned(g.c, 2u * w) && (!add_same || aligned(g.epi.add, 2u * w));
+        if (ok) break;
+        g.out_w = w / 2u;
+    }
     // Buffer loads need each per-block resource below 2^31 bytes: 128 rows of A
     // and 64 k rows of dense B.  The table-gather conv always satisfies it.
     const bool buf = MODE == B_CONV_TAB ||
@@ -886,9 +1019,15 @@ int launch_gemm(GemmArgs& g0, uint32_t zdim, hipStream_t s, const char* name) {
     if (splits == 1) return cm_check_launch(name);
     const int rc = cm_check_launch(name);
     if (rc) return rc;
-    const uint64_t n = (uint64_t)g.rows * g.cols;
-    const dim3 rgrid((uint32_t)cm_grid_blocks(n, kReduceThreads, 4096));
-    return launch_reduce<2>(splits, rgrid, s, g, (uint32_t)(MODE != B_DENSE));
+    ReduceArgs r{};
+    r.ws = g.ws; r.rows = g.rows; r.cols = g.cols; r.ws_ld = g.ws_ld;
+    r.div_q = make_fastdiv(g.ws_ld / 4u);
+    r.bias = g.bias; r.y = g.c;
+    r.conv = MODE != B_DENSE; r.P = g.P; r.div_p = g.div_p;
+    r.y_img = g.y_img; r.ldc = g.ldc; r.epi = g.epi;
+    const uint64_t chunks = (uint64_t)g.rows * (g.ws_ld / 4u);
+    const dim3 rgrid((uint32_t)cm_grid_blocks(chunks, kReduceThreads, 4096));
+    return launch_reduce<2>(splits, rgrid, s, r);
 }
 
 }  // namespace

@@ -75,6 +75,15 @@ __device__ __forceinline__ int32_t epi_act(int32_t y, uint32_t act) {
     return act == 1u ? relu(y) : (act == 2u ? relu6(y) : y);
 }
 
+// The same activation as clamp bounds for a saturated value y: RELU = [0, 32767],
+// RELU6 = [0, 1536], none = the full int16 range.  Computed once, it turns the
+// per-value choice into one min / max pair with no branch.
+__device__ __forceinline__ int32_t act_lo(uint32_t act) { return act == 1u || act == 2u ? 0 : -32768; }
+__device__ __forceinline__ int32_t act_hi(uint32_t act) { return act == 2u ? 1536 : 32767; }
+__device__ __forceinline__ int32_t clamp(int32_t y, int32_t lo, int32_t hi) {
+    return __builtin_elementwise_min(__builtin_elementwise_max(y, lo), hi);
+}
+
 // (float)AccData_t: nearest-even rounding of raw, then exact scale by 2^-16.
 __device__ __forceinline__ float acc_to_float(uint32_t acc) {
     return mul_rn((float)(int32_t)acc, 1.0f / 65536.0f);   // v_cvt_f32_i32 rounds to nearest even

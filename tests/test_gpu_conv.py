@@ -65,6 +65,11 @@ GEOMS = [
     (1, 6, 9, 9, 4, 5, 5, 2, 2, 1, 1, 2, 2, 0, 1),        # depthwise, out_ch < in_ch
     (1, 256, 6, 6, 20, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0),     # K = 2304: gather without the k table
     (1, 40, 11, 11, 9, 7, 7, 1, 1, 3, 2, 9, 6, 1, 0),     # large dilation, pad beyond the window
+    # direct (vector ALU) path: <= 32 output channels, K <= 32, >= 32768 output pixels
+    (4, 3, 256, 130, 32, 3, 3, 2, 2, 1, 1, 1, 1, 1, 0),   # stem, K = 27, 8 k of padding
+    (3, 32, 112, 100, 16, 1, 1, 1, 1, 1, 1, 0, 0, 1, 0),  # 1x1, K = 32, 16 channels
+    (3, 16, 110, 110, 20, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0),  # 20 channels in a group of 24
+    (1, 7, 200, 190, 5, 2, 2, 1, 1, 2, 3, 3, 1, 1, 0),    # 2x2 dilated, padding, 5 channels
 ]
 
 

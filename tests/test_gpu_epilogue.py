@@ -94,6 +94,7 @@ CONV_CASES = [
     ("1x1_pointwise", 2, 24, 14, 14, 32, 1, 1, 1, 0, 0),
     ("3x3_inc_k2304", 1, 256, 9, 9, 20, 3, 1, 1, 1, 0),
     ("depthwise_3x3", 2, 12, 11, 13, 12, 3, 1, 1, 1, 1),
+    ("direct_1x1", 2, 24, 130, 130, 24, 1, 1, 1, 0, 0),
 ]
 
 
