@@ -11,7 +11,9 @@ ports = 3 for binary and 2 for unary ops (bench_src/bench_vectorop.c:93-95).
 The same run also reports (under "results") the GEMM, convolution and pooling
 configurations: Q8.8 GOP/s = 2*MAC / t (bench_matmul.c:95, bench_conv.c:129-132)
 with the int8-MFMA utilisation of the four limb products, and pool GB/s =
-(x + y) * 2 B / t (bench_pool.c:116-117) with rotating input buffers; and the
+(x + y) * 2 B / t (bench_pool.c:116-117) with rotating input buffers, next to a
+VectorOP copy of the same byte count timed the same way (the streaming ceiling
+at that size, `frac_of_copy_ceiling`); and the
 two ONNX graphs run by the scheduler's HIP backend: the MLP's batch-64 latency
 and the MobileNetV2-like graph's images/s at batch 16, each with its roofline
 fraction (sum of per-kernel lower bounds / measured time).
@@ -202,6 +204,18 @@ def bench_pool(steps: int, warmup: int):
                               hbm_frac=round(gbs / HBM_PEAK_GBS, 4), bytes=nbytes,
                               rotating_inputs=POOL_ROTATE, timing="HIP graph of back-to-back launches")
         out[case.name]["_dev"] = (xs[0], ys[0], a)
+    # Streaming ceiling at this size: VectorOP copy moving the largest pool's byte
+    # count (half read, half written), same rotation and graph timing.  At ~32 MB
+    # a launch's ramp and tail are a visible share of its time.
+    ncopy = max(e["bytes"] for e in out.values()) // 4
+    dst = [torch.empty(ncopy, dtype=torch.int16, device="cuda") for _ in range(POOL_ROTATE)]
+    calls = [lambda i=i: K.VectorOPKernel(xs[i], None, dst[i], ncopy, 6) for i in range(POOL_ROTATE)]
+    ms = time_graph(calls, max(steps, 4 * POOL_ROTATE))
+    gbs = 4 * ncopy / (ms * 1e-3) / 1e9
+    for e in out.values():
+        e["frac_of_copy_ceiling"] = round(e["gbs"] / gbs, 4)
+    out["pool_copy_ceiling"] = dict(ms=round(ms, 5), gbs=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4),
+                                    bytes=4 * ncopy, kernel="vecop_flat<6>", rotating_inputs=POOL_ROTATE)
     return out
 
 
