@@ -937,11 +937,13 @@ uint32_t* split_workspace(hipStream_t s, size_t bytes) {
 
 // Number of k splits for a launch of `tiles` blocks over nk_all k steps: enough
 // blocks for every CU when the tile grid alone leaves most of the chip idle,
-// at least two k steps per split, at most 16 splits.
+// at least two k steps per split (one when there are fewer than 64 tiles: a
+// handful of blocks each walking all of K is the slowest case), at most 16.
 uint32_t choose_splits(uint32_t tiles, uint32_t nk_all) {
-    if (tiles >= 160 || nk_all < 4) return 1;
-    uint32_t want = (256 + tiles - 1) / tiles;
-    uint32_t sp = want < nk_all / 2 ? want : nk_all / 2;
+    if (tiles >= 160 || nk_all < 2) return 1;
+    const uint32_t want = (256 + tiles - 1) / tiles;
+    const uint32_t cap = tiles < 64 ? nk_all : nk_all / 2;
+    uint32_t sp = want < cap ? want : cap;
     if (sp > kMaxSplits) sp = kMaxSplits;
     return sp < 2 ? 1 : sp;
 }
