@@ -169,13 +169,50 @@ __device__ __forceinline__ BandItem band_item(const PoolGeom& g, const BandGeom&
 // Output rows per thread on the strip path (fixed window, row stride SH).
 constexpr int kStrip = 4;
 
+// Row partial of a KW-wide window (KW = 2 or 3) starting at LDS element p, in
+// the accumulator form of Acc<KIND> (MAX: max << 8; sums wrap mod 2^32).  The
+// taps are read as one aligned 4-byte pair plus at most one single value:
+// `odd` says p itself is not 4-byte aligned.  Sums go through v_dot2 on the
+// packed pair (x0*1 + x1*1, or x0*x0 + x1*x1 for p = 2), wrapping like the
+// reference's accumulator; shifting a sum by 8 afterwards equals summing the
+// shifted taps modulo 2^32.
+template <int KIND, int KW>
+__device__ __forceinline__ uint32_t row_window(const int16_t* p, bool odd) {
+    typedef short v2s __attribute__((ext_vector_type(2)));
+    uint32_t pair, single = 0;
+    bool has_single = KW == 3;
+    if (odd) {
+        pair = *reinterpret_cast<const uint32_t*>(p + 1);
+        single = (uint32_t)(int32_t)p[0];
+        if (KW == 2) { pair = (pair << 16) | (single & 0xFFFFu); has_single = false; }
+    } else {
+        pair = *reinterpret_cast<const uint32_t*>(p);
+        if (KW == 3) single = (uint32_t)(int32_t)p[2];
+    }
+    const int32_t s1 = has_single ? (int32_t)single : 0;
+    const v2s pv = __builtin_bit_cast(v2s, pair);
+    if constexpr (KIND == K_MAX) {
+        const int32_t lo = (int32_t)(int16_t)(pair & 0xFFFFu), hi = (int32_t)pair >> 16;
+        const int32_t m = has_single ? __builtin_elementwise_max(__builtin_elementwise_max(lo, hi), s1)
+                                     : __builtin_elementwise_max(lo, hi);
+        return (uint32_t)m << 8;
+    } else if constexpr (KIND == K_AVG) {
+        return (uint32_t)__builtin_amdgcn_sdot2(pv, __builtin_bit_cast(v2s, 0x00010001u), s1, false) << 8;
+    } else if constexpr (KIND == K_LP1) {
+        const int32_t lo = (int32_t)(int16_t)(pair & 0xFFFFu), hi = (int32_t)pair >> 16;
+        return ((uint32_t)__builtin_abs(lo) + (uint32_t)__builtin_abs(hi) + (uint32_t)__builtin_abs(s1)) << 8;
+    } else {
+        return (uint32_t)__builtin_amdgcn_sdot2(pv, pv, s1 * s1, false);
+    }
+}
+
 // KH/KW > 0: window fixed at compile time (dilation 1).  SH > 0 (with KH > 0):
 // row stride fixed too, and each thread reduces a vertical strip of kStrip
 // outputs of one column: every input row of the strip is reduced across the
 // window's columns once, and each output merges KH of those row partials
 // (max and the wrapping sums are associative, so the result is the same as
 // tap-by-tap accumulation).  Otherwise one output per thread and pass.
-template <int KIND, int KH, int KW, int SH>
+template <int KIND, int KH, int KW, int SH, int PAIR>
 __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict__ x,
                                                       int16_t* __restrict__ y, PoolGeom g,
                                                       BandGeom b, float inv_full) {
@@ -273,6 +310,7 @@ __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict_
         if constexpr (STRIP) {
             constexpr int NR = (kStrip - 1) * SH + KH;     // input rows of one strip
             const uint32_t nrows = cur.oh1 - cur.oh0;
+
             for (uint32_t st = my_r; my_r < rows_pp && st * kStrip < nrows; st += rows_pp) {
                 const uint32_t oh_b = cur.oh0 + st * kStrip;
                 // strip rows run past the tile only for outputs that are not stored;
@@ -281,12 +319,18 @@ __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict_
                 for (uint32_t ow = my_c; ow < g.out_w; ow += cstep) {
                     const int16_t* w0 = wrow + ow * g.sw;
                     uint32_t part[NR];
+                    if constexpr (PAIR > 0) {
 #pragma unroll
-                    for (int rr = 0; rr < NR; ++rr) {
-                        Acc<KIND> a;
+                        for (int rr = 0; rr < NR; ++rr)
+                            part[rr] = row_window<KIND, KW>(w0 + rr * b.pitch, PAIR == 2);
+                    } else {
 #pragma unroll
-                        for (int kwi = 0; kwi < KW; ++kwi) a.add(w0[rr * b.pitch + kwi]);
-                        part[rr] = a.v;
+                        for (int rr = 0; rr < NR; ++rr) {
+                            Acc<KIND> a;
+#pragma unroll
+                            for (int kwi = 0; kwi < KW; ++kwi) a.add(w0[rr * b.pitch + kwi]);
+                            part[rr] = a.v;
+                        }
                     }
 #pragma unroll
                     for (int o = 0; o < kStrip; ++o) {
@@ -469,23 +513,32 @@ int pool_launch(const int16_t* x, int16_t* y, uint64_t planes, const PoolGeom& g
             const uint32_t kwin = unit_dil && g.ph == g.pw && (g.ph == 2 || g.ph == 3) ? g.ph : 0;
             const uint32_t sh = kwin && (g.sh == 1 || g.sh == 2) ? g.sh : 0;
             b.alloc_rows = b.lds_rows + (sh ? (kStrip - 1) * sh : 0);
-            const uint32_t lds = b.alloc_rows * b.pitch * 2;
+            // + 16 B: a 2-wide window at an odd column reads its taps as the
+            // aligned pair that starts one element later
+            const uint32_t lds = b.alloc_rows * b.pitch * 2 + 16;
             // persistent blocks: exactly as many as are resident at once (a block
             // beyond that would start a second round and double the tail)
-#define CM_BAND(KW_, SH_)                                                                        \
-    do {                                                                                         \
-        const uint64_t cap = resident_blocks((const void*)pool_band<KIND, KW_, KW_, SH_>, lds);  \
-        const dim3 grid((uint32_t)(items < cap ? items : cap)), block(kThreads);                 \
-        hipLaunchKernelGGL((pool_band<KIND, KW_, KW_, SH_>), grid, block, lds, s, x, y, g, b,    \
-                           inv_full);                                                            \
+            // strip path with an even column stride: every window starts at the
+            // same parity, so its taps are read as aligned pairs (PAIR 1: the
+            // window starts 4-byte aligned, 2: one element past that)
+            const int pair = sh && g.sw % 2 == 0 ? ((b.cofs - g.pl) % 2 == 0 ? 1 : 2) : 0;
+#define CM_BAND(KW_, SH_, P_)                                                                        \
+    do {                                                                                             \
+        const uint64_t cap = resident_blocks((const void*)pool_band<KIND, KW_, KW_, SH_, P_>, lds);  \
+        const dim3 grid((uint32_t)(items < cap ? items : cap)), block(kThreads);                     \
+        hipLaunchKernelGGL((pool_band<KIND, KW_, KW_, SH_, P_>), grid, block, lds, s, x, y, g, b,    \
+                           inv_full);                                                                \
     } while (0)
+#define CM_BAND_P(KW_, SH_) \
+    do { if (pair == 1) CM_BAND(KW_, SH_, 1); else if (pair == 2) CM_BAND(KW_, SH_, 2); else CM_BAND(KW_, SH_, 0); } while (0)
             if (kwin == 3) {
-                if (sh == 2) CM_BAND(3, 2); else if (sh == 1) CM_BAND(3, 1); else CM_BAND(3, 0);
+                if (sh == 2) CM_BAND_P(3, 2); else if (sh == 1) CM_BAND_P(3, 1); else CM_BAND(3, 0, 0);
             } else if (kwin == 2) {
-                if (sh == 2) CM_BAND(2, 2); else if (sh == 1) CM_BAND(2, 1); else CM_BAND(2, 0);
+                if (sh == 2) CM_BAND_P(2, 2); else if (sh == 1) CM_BAND_P(2, 1); else CM_BAND(2, 0, 0);
             } else {
-                CM_BAND(0, 0);
+                CM_BAND(0, 0, 0);
             }
+#undef CM_BAND_P
 #undef CM_BAND
             return cm_check_launch("pool_band");
         }

@@ -111,15 +111,24 @@ __device__ __forceinline__ int16_t float_to_data(float f) {
     return r;
 }
 
-// PoolingKernel.cpp:137, 259, 265: AccData_t((float)acc * (1.0f / denom)).
-__device__ __forceinline__ int16_t avg_finalize(uint32_t acc, float inv_denom) {
-    return float_to_data(mul_rn(acc_to_float(acc), inv_denom));
+// float_to_data for |f| < 32768: sat16(floor(f * 256)) with no wide path.
+__device__ __forceinline__ int16_t float_to_data_bounded(float f) {
+    const float s = __builtin_amdgcn_fmed3f(__builtin_floorf(mul_rn(f, 256.0f)), -8388608.0f, 8388607.0f);
+    return (int16_t)sat16((int32_t)s);
 }
 
-// PoolingKernel.cpp:263, 265: AccData_t(sqrtf((float)acc)).
+// PoolingKernel.cpp:137, 259, 265: AccData_t((float)acc * (1.0f / denom)).
+// |acc * 2^-16| <= 32768, times 1/d <= 1/2 for d >= 2; for d = 1 the sum is one
+// value << 8, so |f| <= 128; d = 0 gives 0: the result is always in range.
+__device__ __forceinline__ int16_t avg_finalize(uint32_t acc, float inv_denom) {
+    return float_to_data_bounded(mul_rn(acc_to_float(acc), inv_denom));
+}
+
+// PoolingKernel.cpp:263, 265: AccData_t(sqrtf((float)acc)).  A non-negative
+// acc is below 2^31, so the root is at most 2^7.5.
 __device__ __forceinline__ int16_t lp2_finalize(uint32_t acc) {
     if ((int32_t)acc < 0) return 0;   // sqrt of a negative (wrapped) sum: NaN -> 0
-    return float_to_data(sqrt_rn(acc_to_float(acc)));
+    return float_to_data_bounded(sqrt_rn(acc_to_float(acc)));
 }
 
 }  // namespace q88
