@@ -89,30 +89,10 @@ __device__ __forceinline__ float acc_to_float(uint32_t acc) {
     return mul_rn((float)(int32_t)acc, 1.0f / 65536.0f);   // v_cvt_f32_i32 rounds to nearest even
 }
 
-// saturate_cast<Data_t>(AccData_t(f)) for NaN / Inf / |f| >= 32768:
-// AccData_t(f) floors f to 2^-16 and wraps (keep the low 32 bits of the exact
-// value), then >> 8 and saturate.  NaN / Inf (only reachable from a wrapped
-// LP p=2 accumulator) give 0.
-__device__ __forceinline__ int16_t float_to_data_wide(float f) {
-    if (!__builtin_isfinite(f)) return 0;
-    const double s = __builtin_floor((double)f * 65536.0);
-    if (!(__builtin_fabs(s) < 9.2e18)) return 0;
-    return acc_to_data((uint32_t)(uint64_t)(int64_t)s);
-}
-
-// saturate_cast<Data_t>(AccData_t(f)): for |f| < 32768 this is
-// sat16(floor(f * 256)) (the scale is exact); other values take the rare
-// path behind one branch, so the common case is straight-line code.
+// saturate_cast<Data_t>(AccData_t(f)) for |f| < 32768: AccData_t floors f to a
+// multiple of 2^-16 and the output keeps floor(f * 256), saturated (the scale is
+// exact).  Both pool finalisers stay in that range (see below).
 __device__ __forceinline__ int16_t float_to_data(float f) {
-    // clamped into int32 range before the conversion (only matters off the fast path)
-    const float s = __builtin_amdgcn_fmed3f(__builtin_floorf(mul_rn(f, 256.0f)), -8388608.0f, 8388607.0f);
-    int16_t r = (int16_t)sat16((int32_t)s);
-    if (!(__builtin_fabsf(f) < 32768.0f)) r = float_to_data_wide(f);
-    return r;
-}
-
-// float_to_data for |f| < 32768: sat16(floor(f * 256)) with no wide path.
-__device__ __forceinline__ int16_t float_to_data_bounded(float f) {
     const float s = __builtin_amdgcn_fmed3f(__builtin_floorf(mul_rn(f, 256.0f)), -8388608.0f, 8388607.0f);
     return (int16_t)sat16((int32_t)s);
 }
@@ -121,14 +101,14 @@ __device__ __forceinline__ int16_t float_to_data_bounded(float f) {
 // |acc * 2^-16| <= 32768, times 1/d <= 1/2 for d >= 2; for d = 1 the sum is one
 // value << 8, so |f| <= 128; d = 0 gives 0: the result is always in range.
 __device__ __forceinline__ int16_t avg_finalize(uint32_t acc, float inv_denom) {
-    return float_to_data_bounded(mul_rn(acc_to_float(acc), inv_denom));
+    return float_to_data(mul_rn(acc_to_float(acc), inv_denom));
 }
 
 // PoolingKernel.cpp:263, 265: AccData_t(sqrtf((float)acc)).  A non-negative
 // acc is below 2^31, so the root is at most 2^7.5.
 __device__ __forceinline__ int16_t lp2_finalize(uint32_t acc) {
     if ((int32_t)acc < 0) return 0;   // sqrt of a negative (wrapped) sum: NaN -> 0
-    return float_to_data_bounded(sqrt_rn(acc_to_float(acc)));
+    return float_to_data(sqrt_rn(acc_to_float(acc)));
 }
 
 }  // namespace q88
