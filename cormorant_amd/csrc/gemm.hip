@@ -939,8 +939,12 @@ uint32_t* split_workspace(hipStream_t s, size_t bytes) {
 // blocks for every CU when the tile grid alone leaves most of the chip idle,
 // at least two k steps per split (one when there are fewer than 64 tiles: a
 // handful of blocks each walking all of K is the slowest case), at most 16.
+// A split saves k steps per block but adds the reduce launch (~4-5 us); measured
+// on MobileNetV2-like layers it pays from 8 k steps at 64-159 tiles, and below
+// 64 tiles from 3 steps (2 when there are fewer than 20 tiles).
 uint32_t choose_splits(uint32_t tiles, uint32_t nk_all) {
-    if (tiles >= 160 || nk_all < 2) return 1;
+    if (tiles >= 160) return 1;
+    if (tiles >= 64 ? nk_all < 8 : (nk_all < 2 || (nk_all == 2 && tiles >= 20))) return 1;
     const uint32_t want = (256 + tiles - 1) / tiles;
     const uint32_t cap = tiles < 64 ? nk_all : nk_all / 2;
     uint32_t sp = want < cap ? want : cap;

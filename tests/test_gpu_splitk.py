@@ -23,6 +23,7 @@ MM = [
     ("odd_steps_k449", 130, 449, 70, 4.0),
     ("wrap_full_range", 64, 4096, 96, None),
     ("k256_two_tiles", 200, 256, 100, 8.0),
+    ("tiles64_k640", 1024, 640, 1024, 1.0),    # 64 tiles: split with two k steps per split
 ]
 
 
