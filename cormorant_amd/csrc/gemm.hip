@@ -865,7 +865,7 @@ __global__ __launch_bounds__(kReduceThreads) void split_reduce(ReduceArgs a) {
         v4u part[SPLITS];
 #pragma unroll
         for (uint32_t z = 0; z < SPLITS; ++z)
-            part[z] = __builtin_nontemporal_load(reinterpret_cast<const v4u*>(src + z * zs));
+            part[z] = *reinterpret_cast<const v4u*>(src + z * zs);
         const uint32_t b = a.bias ? (uint32_t)(int32_t)a.bias[row] << 8 : 0u;
         v4u v = v4u{b, b, b, b};
 #pragma unroll
