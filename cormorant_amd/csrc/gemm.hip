@@ -611,9 +611,12 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     // is a real k step (`real`); the last step of the unrolled loop stages a
     // stale register set into planes nobody reads, without a branch, so the
     // split can interleave with the MFMA phase.
+    // convolution: weight rows past the last output channel are never stored,
+    // so their limbs need not be staged (uniform per wave when M % 16 == 0)
+    const bool a_row_live = !CONV || row0 + (threadIdx.x >> 2) < g.rows;
     auto stage_tile = [&](ATile& a, BTile& b, Planes& p, bool real) {
         int32_t h = 0, l = 0;
-        a.store(AV == 0 ? g.a_vec != 0 : AV == 1, p, h, l);
+        if (a_row_live) a.store(AV == 0 ? g.a_vec != 0 : AV == 1, p, h, l);
         row_hs += real ? h : 0;
         row_ls += real ? l : 0;
         if constexpr (CONV) {
@@ -642,18 +645,15 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
             __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
         }
     };
-    // convolution: a wave whose 64 rows all lie past the last output channel
-    // (M <= 64) has no MFMA work and only helps stage the tiles (a uniform
-    // branch; the dense GEMM keeps the straight-line step, which schedules better)
     const bool wave_rows = row0 + wrow < g.rows;
-    auto mfma_step = [&](const Planes& p, uint32_t it) {
-        if constexpr (CONV) {
-            if (!wave_rows) return;
-        }
+    const bool wave_half = row0 + wrow + 32 >= g.rows;   // row tiles 2, 3 of the wave empty
+    // the MFMAs of the wave's first NI row tiles (the others are left untouched)
+    auto mfma_rows = [&](auto ni, const Planes& p, uint32_t it) {
+        constexpr int NI = decltype(ni)::value;
         const uint32_t koff = (lane >> 4) * 16;
         v4i ah[TI], al[TI];
 #pragma unroll
-        for (int i = 0; i < TI; ++i) {
+        for (int i = 0; i < NI; ++i) {
             const uint32_t r = (wrow + i * 16 + (lane & 15)) * kStride + koff;
             ah[i] = *reinterpret_cast<const v4i*>(p.a_hi + r);
             al[i] = *reinterpret_cast<const v4i*>(p.a_lo + r);
@@ -664,16 +664,16 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
             const v4i bh = *reinterpret_cast<const v4i*>(p.b_hi + cidx);
             const v4i bl = *reinterpret_cast<const v4i*>(p.b_lo + cidx);
 #pragma unroll
-            for (int i = 0; i < TI; ++i)
+            for (int i = 0; i < NI; ++i)
                 hh[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bh, hh[i][j], 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < TI; ++i)
+            for (int i = 0; i < NI; ++i)
                 mid[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bl, mid[i][j], 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < TI; ++i)
+            for (int i = 0; i < NI; ++i)
                 ll[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], bl, ll[i][j], 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < TI; ++i)
+            for (int i = 0; i < NI; ++i)
                 mid[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], bh, mid[i][j], 0, 0, 0);
         }
 
@@ -691,6 +691,20 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
                     }
             }
         }
+    };
+    // convolution with few output channels: waves past the last channel skip
+    // the step, waves with at most 32 live rows run half of it (uniform
+    // branches; the dense GEMM keeps the single straight-line step, which
+    // schedules better)
+    auto mfma_step = [&](const Planes& p, uint32_t it) {
+        if constexpr (CONV) {
+            if (!wave_rows) return;
+            if (wave_half) {
+                mfma_rows(std::integral_constant<int, 2>{}, p, it);
+                return;
+            }
+        }
+        mfma_rows(std::integral_constant<int, TI>{}, p, it);
     };
 
     // this block's k steps: all of them, or its split's share (sums over any
