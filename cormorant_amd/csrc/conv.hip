@@ -190,16 +190,25 @@ __global__ __launch_bounds__(kDirThreads) void conv_direct(DirArgs g) {
     if (!pok) return;
     const int32_t lo = q88::act_lo(g.epi.act), hi = q88::act_hi(g.epi.act);
     const uint64_t ybase = (uint64_t)n * g.y_img + p;
+    // the fused Add's values for all MT channels first (channels past M read the
+    // last one), so the loads are in flight together rather than one per store
+    int32_t res[MT];
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm) res[mm] = 0;
+    if (g.epi.add_mode == 1u) {
+#pragma unroll
+        for (int mm = 0; mm < MT; ++mm) {
+            const uint32_t m = min(m0 + mm, g.M - 1u);
+            res[mm] = g.epi.add[ybase + (uint64_t)m * g.P];
+        }
+    }
 #pragma unroll
     for (int mm = 0; mm < MT; ++mm) {
         const uint32_t m = m0 + mm;
-        if (m >= g.M) break;
         uint32_t v = acc[mm];
-        if (HAS_BIAS) v += q88::data_to_acc(g.bias[m]);
-        int32_t yv = q88::acc_to_data(v);
-        const uint64_t o = ybase + (uint64_t)m * g.P;
-        if (g.epi.add_mode == 1u) yv = q88::add(yv, g.epi.add[o]);
-        g.y[o] = (int16_t)q88::clamp(yv, lo, hi);
+        if (HAS_BIAS) v += q88::data_to_acc(g.bias[min(m, g.M - 1u)]);
+        const int32_t yv = q88::clamp(q88::add(q88::acc_to_data(v), res[mm]), lo, hi);
+        if (m < g.M) g.y[ybase + (uint64_t)m * g.P] = (int16_t)yv;
     }
 }
 

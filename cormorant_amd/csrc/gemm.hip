@@ -825,20 +825,30 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     const uint64_t rstride = CONV ? (uint64_t)g.P : g.ldc;
     int16_t* cptr = g.c + (CONV ? 0 : (uint64_t)blockIdx.z * g.c_bs);
     const int16_t* rptr = g.epi.add + (CONV ? 0 : (uint64_t)blockIdx.z * g.c_bs);
+    // the fused Add's values of all four rows first (rows past the end read the
+    // last row), so their loads are in flight together
+    int32_t add[4][8];
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) add[rr][q] = cadd[q];
+    if (g.epi.add_mode == 1u) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+            const uint32_t row = min(row0 + rb + rr * 32, g.rows - 1u);
+            load8(rptr + (uint64_t)row * rstride, ocol, ncol, g.out_w, add[rr]);
+        }
+    }
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
         const uint32_t r = rb + rr * 32;
         if (row0 + r >= g.rows) break;
         const uint64_t ro = (uint64_t)(row0 + r) * rstride;
-        int32_t add[8];
-#pragma unroll
-        for (int q = 0; q < 8; ++q) add[q] = cadd[q];
-        if (g.epi.add_mode == 1u) load8(rptr + ro, ocol, ncol, g.out_w, add);
         uint32_t v[8];
         tile_row(r, v);
         int32_t y[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) y[q] = q88::clamp(q88::add(q88::acc_to_data(v[q]), add[q]), lo, hi);
+        for (int q = 0; q < 8; ++q) y[q] = q88::clamp(q88::add(q88::acc_to_data(v[q]), add[rr][q]), lo, hi);
         store8(cptr + ro, ocol, ncol, g.out_w, y);
     }
 }
