@@ -16,7 +16,11 @@ VectorOP copy of the same byte count timed the same way (the streaming ceiling
 at that size, `frac_of_copy_ceiling`); and the
 two ONNX graphs run by the scheduler's HIP backend: the MLP's batch-64 latency
 and the MobileNetV2-like graph's images/s at batch 16, each with its roofline
-fraction (sum of per-kernel lower bounds / measured time).
+fraction (sum of per-kernel lower bounds / measured time).  CPU figures (the oracle,
+a C restatement of the reference C-simulation loops, on this host): one thread
+(the faithful C-simulation path, `cpu_baseline.value` and each result's
+`cpu.gops` / `cpu.gbs`) and OpenMP over the independent outer loop (`*_mt`);
+`host` records the CPU model and the thread count.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
                        [--workloads vecop,gemm,conv,pool,graphs] [--no-cpu]
@@ -278,7 +282,7 @@ def bench_graphs(steps: int, warmup: int, check: bool):
         if check:
             import oracle
             from oracle import graph_sim as gs
-            threads = min(os.cpu_count() or 1, 16)
+            threads = host_threads()
             oracle.set_threads(threads)
             t0 = time.perf_counter()
             want = gs.run_plan(sess.plan, {"X": x}, threads=True)["Y"]
@@ -294,11 +298,36 @@ def bench_graphs(steps: int, warmup: int, check: bool):
 
 
 # ------------------------------------------------------------ cpu baseline --
+def host_threads() -> int:
+    """OpenMP threads for the multi-thread CPU figures: the CPUs this process may
+    run on, at most 16."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def host_info() -> dict:
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return dict(cpu_model=model, logical_cpus=os.cpu_count(), omp_threads=host_threads())
+
+
 def cpu_baseline(vec_bufs, extras: dict):
     """The oracle (C restatement of the reference C-simulation loops, -O2) timed
-    on this host: single thread, on a bounded sample.  The same run checks the
-    GPU outputs of that sample bit-for-bit."""
+    on this host on a bounded sample: single thread (the faithful C-simulation
+    path; this run also checks the GPU outputs of that sample bit-for-bit), and
+    with OpenMP over the independent outer loop (`*_mt`, host_threads() threads)."""
     import oracle
+    mt = host_threads()
     oracle.set_threads(1)
     res = {}
     # VectorOP: the whole 64Mi sweep, one thread
@@ -314,6 +343,16 @@ def cpu_baseline(vec_bufs, extras: dict):
         if not np.array_equal(got, want):
             raise SystemExit(f"bench: GPU {bf['name']} output differs from the oracle")
     res["vecop"] = dict(gbs=bytes_total / t_total / 1e9, seconds=t_total)
+    oracle.set_threads(mt)
+    t_mt = 0.0
+    for bf in vec_bufs:
+        want = np.empty(bf["a_host"].size, np.int16)
+        b = bf["b_host"] if bf["b_host"] is not None else np.zeros(1, np.int16)
+        t0 = time.perf_counter()
+        oracle.vectorop(bf["a_host"], b, want, want.size, bf["op"], threads=True)
+        t_mt += time.perf_counter() - t0
+    res["vecop"].update(gbs_mt=bytes_total / t_mt / 1e9, seconds_mt=t_mt, threads_mt=mt)
+    oracle.set_threads(1)
     # GEMM 3a: one of the 32 batches (1024^3); GEMM 3b: 16 rows
     if "gemm_b32_1024" in extras:
         da, db, dc, a, b = extras["gemm_b32_1024"].pop("_dev")
@@ -327,6 +366,13 @@ def cpu_baseline(vec_bufs, extras: dict):
             raise SystemExit("bench: GPU gemm batch 0 differs from the oracle")
         res["gemm_b32_1024"] = dict(gops=2.0 * n * k * m / dt / 1e9, seconds=dt,
                                     sample="batch 0 of 32 (1024^3)")
+        oracle.set_threads(mt)
+        t0 = time.perf_counter()
+        oracle.matmul(np.ascontiguousarray(a[0]).reshape(-1), np.ascontiguousarray(b[0]).reshape(-1),
+                      want, n, k, m, threads=True)
+        dt = time.perf_counter() - t0
+        oracle.set_threads(1)
+        res["gemm_b32_1024"].update(gops_mt=2.0 * n * k * m / dt / 1e9, seconds_mt=dt, threads_mt=mt)
     if "gemm_b1_4096" in extras:
         da, db, dc, a, b = extras["gemm_b1_4096"].pop("_dev")
         n = k = m = 4096
@@ -340,6 +386,18 @@ def cpu_baseline(vec_bufs, extras: dict):
         dt = time.perf_counter() - t0
         res["gemm_b1_4096"] = dict(gops=2.0 * len(rows) * k * m / dt / 1e9, seconds=dt,
                                    sample=f"{len(rows)} of 4096 rows")
+        nr = 128
+        part = np.empty(nr * m, np.int16)
+        oracle.set_threads(mt)
+        t0 = time.perf_counter()
+        oracle.matmul(np.ascontiguousarray(a2[:nr]).reshape(-1), np.ascontiguousarray(b2).reshape(-1),
+                      part, nr, k, m, threads=True)
+        dt = time.perf_counter() - t0
+        oracle.set_threads(1)
+        if not np.array_equal(got[:nr].reshape(-1), part):
+            raise SystemExit("bench: GPU gemm 4096 rows 0-127 differ from the oracle")
+        res["gemm_b1_4096"].update(gops_mt=2.0 * nr * k * m / dt / 1e9, seconds_mt=dt, threads_mt=mt,
+                                   sample_mt=f"rows 0-{nr - 1}")
     for name in ("conv_a_3x3_s1_p1", "conv_b_3x3_s2_d2_p2"):
         if name not in extras:
             continue
@@ -357,6 +415,14 @@ def cpu_baseline(vec_bufs, extras: dict):
             raise SystemExit(f"bench: GPU {name} image 0 differs from the oracle")
         res[name] = dict(gops=2.0 * case.macs / case.batch / dt / 1e9, seconds=dt,
                          sample="image 0 of 32")
+        oracle.set_threads(mt)
+        t0 = time.perf_counter()
+        oracle.conv(np.ascontiguousarray(x[0]).reshape(-1), w.reshape(-1), b, want, 1, case.in_ch,
+                    case.hw, case.hw, case.out_ch, o, o, case.k, case.k, case.stride, case.stride,
+                    case.dil, case.dil, case.pad, case.pad, 1, 0, threads=True)
+        dt = time.perf_counter() - t0
+        oracle.set_threads(1)
+        res[name].update(gops_mt=2.0 * case.macs / case.batch / dt / 1e9, seconds_mt=dt, threads_mt=mt)
     for name, e in list(extras.items()):
         if not name.startswith(("maxpool", "avgpool", "lppool", "globalavgpool")):
             continue
@@ -372,6 +438,15 @@ def cpu_baseline(vec_bufs, extras: dict):
         if not np.array_equal(y.cpu().numpy(), want):
             raise SystemExit(f"bench: GPU {name} differs from the oracle")
         res[name] = dict(gbs=(xh.size + want.size) * 2 / dt / 1e9, seconds=dt, sample="full tensor")
+        oracle.set_threads(mt)
+        t0 = time.perf_counter()
+        oracle.pool(xh, want, a["batch"], a["channels"], a["in_h"], a["in_w"], a["out_h"],
+                    a["out_w"], a["pool_h"], a["pool_w"], a["stride_h"], a["stride_w"],
+                    a["pad_top"], a["pad_left"], a["dil_h"], a["dil_w"], a["pool_type"],
+                    a["lp_order"], a["count_include_pad"], threads=True)
+        dt = time.perf_counter() - t0
+        oracle.set_threads(1)
+        res[name].update(gbs_mt=(xh.size + want.size) * 2 / dt / 1e9, seconds_mt=dt, threads_mt=mt)
     return res
 
 
@@ -468,16 +543,19 @@ def main() -> int:
         graphs = bench_graphs(max(5, args.steps // 2), 2, check=not args.no_cpu)
     cpu_res = {}
     if not args.no_cpu:
-        log("CPU baseline (oracle, 1 thread) and sample check")
+        log("CPU baseline (oracle, 1 thread and OpenMP) and sample check")
         cpu_res = cpu_baseline(bufs, extras)
-        cpu = dict(value=round(cpu_res["vecop"]["gbs"], 3), unit="GB/s", cores=1, kind="port",
+        v = cpu_res["vecop"]
+        cpu = dict(value=round(v["gbs"], 3), unit="GB/s", cores=1, kind="port",
                    sample="the full six-op 64Mi-element sweep, oracle C restatement -O2, one thread",
-                   seconds=round(cpu_res["vecop"]["seconds"], 3))
+                   seconds=round(v["seconds"], 3),
+                   value_mt=round(v["gbs_mt"], 3), cores_mt=v["threads_mt"],
+                   seconds_mt=round(v["seconds_mt"], 3))
     for name, e in extras.items():
         e.pop("_dev", None)
         if name in cpu_res:
-            e["cpu_1t"] = {k: (round(v, 4) if isinstance(v, float) else v)
-                           for k, v in cpu_res[name].items()}
+            e["cpu"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                        for k, v in cpu_res[name].items()}
         results[name] = e
     results.update(graphs)
 
@@ -503,6 +581,7 @@ def main() -> int:
         },
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "host": host_info(),
         "results": results,
     }
     print(json.dumps(line))
