@@ -52,6 +52,17 @@ __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
     return (uint32_t)(t >> f.p);
 }
 
+// Raw buffer resource word 3 for gfx950 (32-bit data, no swizzle): loads past
+// num_records return 0 and stores past it are dropped.  kOob is an offset past
+// every resource used here (all are smaller than 2^31 bytes).
+constexpr int kBufferWord3 = 0x00020000;
+constexpr uint32_t kOob = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const int16_t* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<int16_t*>(base), (short)0, (int)bytes,
+                                             kBufferWord3);
+}
+
 inline uint64_t cm_grid_blocks(uint64_t work, uint32_t threads, uint64_t cap = 1u << 20) {
     uint64_t b = (work + threads - 1) / threads;
     if (b == 0) b = 1;

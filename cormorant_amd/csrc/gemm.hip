@@ -76,16 +76,6 @@ struct GemmArgs {
     uint32_t* ws;
 };
 
-// Raw buffer resource word 3 for gfx950 (32-bit data, no swizzle): loads past
-// num_records return 0.  kOob is an offset past every resource used here.
-constexpr int kBufferWord3 = 0x00020000;
-constexpr uint32_t kOob = 0x80000000u;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const int16_t* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<int16_t*>(base), (short)0, (int)bytes,
-                                             kBufferWord3);
-}
-
 // Limb bytes of four int16 values held in two words w0 = (v0 | v1 << 16),
 // w1 = (v2 | v3 << 16): one v_perm_b32 gathers the high bytes (v >> 8) and one
 // more the low bytes, which the xor offsets by -128.  Byte i of the result is

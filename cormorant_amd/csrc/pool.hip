@@ -20,6 +20,8 @@
 #include "cm_internal.h"
 #include "q88.h"
 
+#include <algorithm>
+
 namespace {
 
 typedef short v8s __attribute__((ext_vector_type(8)));
@@ -126,14 +128,22 @@ __global__ __launch_bounds__(kThreads) void pool_global(const int16_t* __restric
 // `vec` (in_w % 8 == 0, 16-byte aligned planes) selects 16-byte row copies;
 // otherwise rows are copied element by element.  KH/KW > 0 fix the window at
 // compile time (dilation 1) so the taps unroll with immediate LDS offsets.
-constexpr int kPre = 2;
-constexpr uint32_t kBandBytes = kPre * kThreads * 16;
+constexpr uint32_t kBandBytes = 8192;   // input bytes one item fetches at most (16 B per load)
 #ifndef CM_POOL_BAND_TARGET
 #define CM_POOL_BAND_TARGET (16u << 10)
 #endif
 // LDS bytes of input a band aims for: smaller bands give each persistent block
 // more items to pipeline and a shorter last item
 constexpr uint32_t kBandTarget = CM_POOL_BAND_TARGET < kBandBytes ? CM_POOL_BAND_TARGET : kBandBytes;
+// Persistent band / strip blocks per CU, at most.  The occupancy query allows
+// 8 blocks of these kernels per CU; 6 measured ~12 % faster on 32 MB tensors
+// (5 and 8 slower): blocks then hold more items, so more of each item's load
+// latency hides behind the previous item's reduction.
+#ifndef CM_POOL_PERSIST_PER_CU
+#define CM_POOL_PERSIST_PER_CU 6
+#endif
+constexpr int kPersistPerCu = CM_POOL_PERSIST_PER_CU;
+constexpr int kNonTemporal = 2;   // buffer access cache policy: nt
 constexpr uint32_t kInvTab = 64;   // AVG: 1/d for every denominator d <= 63, per block
 
 struct BandGeom {
@@ -141,6 +151,7 @@ struct BandGeom {
     uint32_t pitch, cofs, lds_rows;    // LDS tile: lds_rows x pitch elements (+ slack rows)
     uint32_t alloc_rows;               // rows allocated (slack for the last strip's reads)
     uint32_t vec;                      // 16-byte row copies
+    uint32_t n_strips;                 // pool_strip: strips of kStrip output rows per band
     FastDiv div_w;                     // division by in_w (element copies)
 };
 
@@ -220,6 +231,7 @@ __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict_
     __shared__ float inv_tab[kInvTab];
     constexpr int16_t kPadV = KIND == K_MAX ? (int16_t)-32768 : (int16_t)0;
     constexpr bool STRIP = KH > 0 && SH > 0;
+    constexpr int PRE = kBandBytes / (kThreads * 16);   // 16-byte loads per thread and item
     const int32_t ph = KH > 0 ? KH : (int32_t)g.ph, pw = KW > 0 ? KW : (int32_t)g.pw;
     const int32_t dh = KH > 0 ? 1 : (int32_t)g.dh, dw = KW > 0 ? 1 : (int32_t)g.dw;
     const bool avg_tab = KIND == K_AVG && !g.cip && (uint32_t)(ph * pw) < kInvTab;
@@ -242,9 +254,9 @@ __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict_
     // this thread's 16-byte vectors u: row (relative to the item's first real
     // row) and vector column, the same for every item
     const uint32_t vpr = g.in_w / 8;                 // 16-byte vectors per input row (vec path)
-    uint32_t vslot[kPre];   // LDS element offset of vector u, relative to the item's row r0
+    uint32_t vslot[PRE];   // LDS element offset of vector u, relative to the item's row r0
 #pragma unroll
-    for (int u = 0; u < kPre; ++u) {
+    for (int u = 0; u < PRE; ++u) {
         const uint32_t v = u * kThreads + threadIdx.x;
         const uint32_t r = b.vec ? v / vpr : 0u;
         vslot[u] = r * b.pitch + b.cofs + (v - r * vpr) * 8;
@@ -255,14 +267,14 @@ __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict_
     const uint32_t cstep = g.out_w > kThreads ? kThreads : g.out_w;
 
     // fetch: the real input rows of an item into registers
-    v8s pre[kPre];
+    v8s pre[PRE];
     auto fetch = [&](const BandItem& it) {
         if (!b.vec) return;
         const int16_t* xp = x + it.plane * (uint64_t)g.in_h * g.in_w;
         const uint32_t nv = (it.r1 - it.r0) * vpr;
         const v8s* sv = reinterpret_cast<const v8s*>(xp + (int64_t)(it.ih_lo + (int32_t)it.r0) * g.in_w);
 #pragma unroll
-        for (int u = 0; u < kPre; ++u) {
+        for (int u = 0; u < PRE; ++u) {
             const uint32_t v = u * kThreads + threadIdx.x;
             if (v < nv) pre[u] = __builtin_nontemporal_load(sv + v);
         }
@@ -284,7 +296,7 @@ __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict_
             if (b.vec) {
                 const uint32_t nv = (cur.r1 - cur.r0) * vpr;
 #pragma unroll
-                for (int u = 0; u < kPre; ++u) {
+                for (int u = 0; u < PRE; ++u) {
                     const uint32_t v = u * kThreads + threadIdx.x;
                     if (v < nv) *reinterpret_cast<v8s*>(lds + cur.r0 * b.pitch + vslot[u]) = pre[u];
                 }
@@ -332,10 +344,16 @@ __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict_
                             part[rr] = a.v;
                         }
                     }
+                    // Every row partial is read before any output is formed: the
+                    // empty asm takes the values as operands, so the compiler
+                    // cannot sink a read behind an output's store condition and
+                    // the strip's LDS reads are all in flight together.
+#pragma unroll
+                    for (int rr = 0; rr < NR; ++rr) asm volatile("" : "+v"(part[rr]));
+                    int16_t res[kStrip];
 #pragma unroll
                     for (int o = 0; o < kStrip; ++o) {
                         const uint32_t oh = oh_b + o;
-                        if (oh >= cur.oh1) break;
                         Acc<KIND> a;
                         a.v = part[o * SH];
 #pragma unroll
@@ -350,8 +368,12 @@ __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict_
                                 inv = avg_tab ? inv_tab[d] : q88::inv_denom(d);
                             }
                         }
-                        yp[(uint64_t)oh * g.out_w + ow] = a.finish(inv);
+                        res[o] = a.finish(inv);
                     }
+                    const uint32_t n_out = cur.oh1 - oh_b;   // >= 1: the strip starts inside the band
+#pragma unroll
+                    for (int o = 0; o < kStrip; ++o)
+                        if ((uint32_t)o < n_out) yp[(uint64_t)(oh_b + o) * g.out_w + ow] = res[o];
                 }
             }
         } else {
@@ -384,6 +406,148 @@ __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict_
         if (!more) break;
         item = next;
         cur = nb;
+    }
+}
+
+// ----------------------------------------------------------------- strip --
+// The band layout with one strip per thread: fixed KW x KW window, row stride
+// SH, 16-byte row copies, and every strip of a band (n_strips x out_w) within
+// one block, so a thread owns strip threadIdx.x / out_w, column
+// threadIdx.x % out_w of every item.  The next item's loads are issued into
+// the registers that the current item's rows have just left, as non-temporal
+// loads (each input byte is read once).  Every global access is a buffer
+// access whose range is the item's own rows (input) or output band (stores),
+// so loads past the item read 0 and stores past the band -- a strip's rows
+// beyond the band, or a thread with no strip -- are dropped by the hardware:
+// no access needs a condition, and each item issues a fixed number of loads
+// and stores.  (A second item in flight per block measured slower: with the
+// first items' loads competing with the second ones', the first stagings
+// arrived later than the second items saved.)
+template <int KIND, int KW, int SH, int PAIR>
+__global__ __launch_bounds__(kThreads) void pool_strip(const int16_t* __restrict__ x,
+                                                       int16_t* __restrict__ y, PoolGeom g,
+                                                       BandGeom b, float inv_full) {
+    extern __shared__ __align__(16) int16_t lds[];
+    __shared__ float inv_tab[kInvTab];
+    constexpr int KH = KW;
+    constexpr int NR = (kStrip - 1) * SH + KH;   // input rows of one strip
+    constexpr int PRE = kBandBytes / (kThreads * 16);
+    constexpr int16_t kPadV = KIND == K_MAX ? (int16_t)-32768 : (int16_t)0;
+    const bool avg_tab = KIND == K_AVG && !g.cip && (uint32_t)(KH * KW) < kInvTab;
+    if (KIND == K_AVG && threadIdx.x < kInvTab) inv_tab[threadIdx.x] = q88::inv_denom(threadIdx.x);
+    {
+        // left / right padding columns of every row, the same for every item
+        const uint32_t rcols = b.pitch - b.cofs - g.in_w;
+        const uint32_t strip = b.cofs + rcols;
+        if (strip) {
+            const uint32_t n = b.alloc_rows * strip;
+            for (uint32_t i = threadIdx.x; i < n; i += kThreads) {
+                const uint32_t r = i / strip, c = i - r * strip;
+                lds[r * b.pitch + (c < b.cofs ? c : c + g.in_w)] = kPadV;
+            }
+        }
+    }
+    const uint32_t vpr = g.in_w / 8;
+    uint32_t vslot[PRE];
+#pragma unroll
+    for (int u = 0; u < PRE; ++u) {
+        const uint32_t v = u * kThreads + threadIdx.x;
+        const uint32_t r = v / vpr;
+        vslot[u] = r * b.pitch + b.cofs + (v - r * vpr) * 8;
+    }
+    const uint32_t st = threadIdx.x / g.out_w;
+    const uint32_t ow = threadIdx.x - st * g.out_w;
+    // LDS element of this strip's first tap, relative to the tile.  Threads with
+    // no strip read the first window of row 0 (in bounds, and at the same
+    // parity as every window, so the pair reads stay 4-byte aligned); their
+    // stores are dropped.
+    const uint32_t wofs = (st < b.n_strips ? st * kStrip * SH * b.pitch + ow * g.sw : 0u) + b.cofs - g.pl;
+
+    // loads of an item's real input rows; an item past the end reads nothing
+    auto issue = [&](uint32_t item, v8s (&pre)[PRE]) {
+        const int16_t* base = x;
+        uint32_t bytes = 0;
+        if (item < b.n_items) {
+            const BandItem it = band_item(g, b, item);
+            base = x + it.plane * (uint64_t)g.in_h * g.in_w + (int64_t)(it.ih_lo + (int32_t)it.r0) * g.in_w;
+            bytes = (it.r1 - it.r0) * g.in_w * 2u;
+        }
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, bytes);
+#pragma unroll
+        for (int u = 0; u < PRE; ++u) {
+            typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+            const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rs, (u * kThreads + threadIdx.x) * 16u, 0, kNonTemporal);
+            pre[u] = __builtin_bit_cast(v8s, v);
+        }
+    };
+
+    auto step = [&](uint32_t item, v8s (&pre)[PRE]) {
+        const BandItem cur = band_item(g, b, item);
+        __syncthreads();                       // the previous item's LDS reads are done
+        {
+            const uint32_t top = cur.r0 * b.pitch;
+            const uint32_t bottom = (b.lds_rows - cur.r1) * b.pitch;
+            for (uint32_t i = threadIdx.x; i < top; i += kThreads) lds[i] = kPadV;
+            for (uint32_t i = threadIdx.x; i < bottom; i += kThreads) lds[cur.r1 * b.pitch + i] = kPadV;
+            const uint32_t nv = (cur.r1 - cur.r0) * vpr;
+#pragma unroll
+            for (int u = 0; u < PRE; ++u) {
+                const uint32_t v = u * kThreads + threadIdx.x;
+                if (v < nv) *reinterpret_cast<v8s*>(lds + cur.r0 * b.pitch + vslot[u]) = pre[u];
+            }
+        }
+        __syncthreads();
+        issue(item + gridDim.x, pre);         // the next item, into the registers just staged
+
+        const int16_t* w0 = lds + wofs;
+        uint32_t part[NR];
+        if constexpr (PAIR > 0) {
+#pragma unroll
+            for (int rr = 0; rr < NR; ++rr) part[rr] = row_window<KIND, KW>(w0 + rr * b.pitch, PAIR == 2);
+        } else {
+#pragma unroll
+            for (int rr = 0; rr < NR; ++rr) {
+                Acc<KIND> a;
+#pragma unroll
+                for (int kwi = 0; kwi < KW; ++kwi) a.add(w0[rr * b.pitch + kwi]);
+                part[rr] = a.v;
+            }
+        }
+        const __amdgpu_buffer_rsrc_t ry =
+            make_rsrc(y + cur.plane * (uint64_t)g.out_h * g.out_w + (uint64_t)cur.oh0 * g.out_w,
+                      (cur.oh1 - cur.oh0) * g.out_w * 2u);
+#pragma unroll
+        for (int o = 0; o < kStrip; ++o) {
+            const uint32_t oh = cur.oh0 + st * kStrip + o;
+            Acc<KIND> a;
+            a.v = part[o * SH];
+#pragma unroll
+            for (int khi = 1; khi < KH; ++khi) a.merge(part[o * SH + khi]);
+            float inv = inv_full;
+            if constexpr (KIND == K_AVG) {
+                if (!g.cip) {
+                    const int32_t ih0 = (int32_t)(oh * SH) - (int32_t)g.pt;
+                    const int32_t iw0 = (int32_t)(ow * g.sw) - (int32_t)g.pl;
+                    const uint32_t d = (uint32_t)(valid_taps(ih0, KH, 1, (int32_t)g.in_h) *
+                                                  valid_taps(iw0, KW, 1, (int32_t)g.in_w));
+                    inv = avg_tab ? inv_tab[d] : q88::inv_denom(d);
+                }
+            }
+            // rows past the band (and threads with no strip, st >= n_strips)
+            // fall past the resource: the store is dropped
+            const uint32_t off = ((st * kStrip + o) * g.out_w + ow) * 2u;
+            __builtin_amdgcn_raw_buffer_store_b16(a.finish(inv), ry, off, 0, 0);
+        }
+    };
+
+    uint32_t item = blockIdx.x;
+    if (item >= b.n_items) return;
+    v8s pre[PRE];
+    issue(item, pre);
+    for (;;) {
+        step(item, pre);
+        item += gridDim.x;
+        if (item >= b.n_items) break;
     }
 }
 
@@ -432,8 +596,9 @@ uint64_t rows_needed(const PoolGeom& g, uint32_t bh) {
 }
 
 // Blocks of kThreads threads with `lds` dynamic LDS bytes resident on the whole
-// device at once (occupancy x CU count), kPoolBlocks if the runtime cannot say.
-uint64_t resident_blocks(const void* kernel, uint32_t lds) {
+// device at once (occupancy, at most max_per_cu, x CU count), kPoolBlocks if
+// the runtime cannot say.
+uint64_t resident_blocks(const void* kernel, uint32_t lds, int max_per_cu) {
     int per_cu = 0, dev = 0, cus = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess ||
         hipGetDevice(&dev) != hipSuccess ||
@@ -442,7 +607,7 @@ uint64_t resident_blocks(const void* kernel, uint32_t lds) {
         (void)hipGetLastError();
         return kPoolBlocks;
     }
-    return (uint64_t)per_cu * (uint64_t)cus;
+    return (uint64_t)(per_cu < max_per_cu ? per_cu : max_per_cu) * (uint64_t)cus;
 }
 
 // 1.0f / (float)d on the host: IEEE round-to-nearest-even, like the device path.
@@ -496,6 +661,14 @@ int pool_launch(const int16_t* x, int16_t* y, uint64_t planes, const PoolGeom& g
         }
         band_h = lo;
     }
+    const bool unit_dil = g.dh == 1 && g.dw == 1;
+    const uint32_t kwin = unit_dil && g.ph == g.pw && (g.ph == 2 || g.ph == 3) ? g.ph : 0;
+    const uint32_t sh = kwin && (g.sh == 1 || g.sh == 2) ? g.sh : 0;
+    const uint32_t vec = (g.in_w % 8 == 0) && (((uintptr_t)x & 15u) == 0);
+    // pool_strip: fixed window and row stride, 16-byte rows, and every strip of
+    // a band in one block (bands of at most kThreads / out_w strips)
+    const bool one_pass = band_h > 0 && sh && vec && g.out_w <= (uint32_t)kThreads;
+    if (one_pass) band_h = std::min<uint32_t>(band_h, (kThreads / g.out_w) * kStrip);
     if (band_h > 0) {
         const uint32_t n_bands = (g.out_h + band_h - 1) / band_h;
         const uint64_t items = planes * n_bands;
@@ -507,30 +680,39 @@ int pool_launch(const int16_t* x, int16_t* y, uint64_t planes, const PoolGeom& g
             b.pitch = (uint32_t)pitch;
             b.cofs = (uint32_t)cofs;
             b.lds_rows = (uint32_t)rows_needed(g, band_h);
-            b.vec = (g.in_w % 8 == 0) && (((uintptr_t)x & 15u) == 0);
+            b.vec = vec;
+            b.n_strips = (band_h + kStrip - 1) / kStrip;
             b.div_w = make_fastdiv(g.in_w);
-            const bool unit_dil = g.dh == 1 && g.dw == 1;
-            const uint32_t kwin = unit_dil && g.ph == g.pw && (g.ph == 2 || g.ph == 3) ? g.ph : 0;
-            const uint32_t sh = kwin && (g.sh == 1 || g.sh == 2) ? g.sh : 0;
             b.alloc_rows = b.lds_rows + (sh ? (kStrip - 1) * sh : 0);
             // + 16 B: a 2-wide window at an odd column reads its taps as the
             // aligned pair that starts one element later
             const uint32_t lds = b.alloc_rows * b.pitch * 2 + 16;
-            // persistent blocks: exactly as many as are resident at once (a block
-            // beyond that would start a second round and double the tail)
             // strip path with an even column stride: every window starts at the
             // same parity, so its taps are read as aligned pairs (PAIR 1: the
             // window starts 4-byte aligned, 2: one element past that)
             const int pair = sh && g.sw % 2 == 0 ? ((b.cofs - g.pl) % 2 == 0 ? 1 : 2) : 0;
-#define CM_BAND(KW_, SH_, P_)                                                                        \
-    do {                                                                                             \
-        const uint64_t cap = resident_blocks((const void*)pool_band<KIND, KW_, KW_, SH_, P_>, lds);  \
-        const dim3 grid((uint32_t)(items < cap ? items : cap)), block(kThreads);                     \
-        hipLaunchKernelGGL((pool_band<KIND, KW_, KW_, SH_, P_>), grid, block, lds, s, x, y, g, b,    \
-                           inv_full);                                                                \
+            // persistent blocks: at most as many as are resident at once (a block
+            // beyond that would start a second round and double the tail)
+#define CM_LAUNCH(KERNEL)                                                                      \
+    do {                                                                                       \
+        const uint64_t cap = resident_blocks((const void*)KERNEL, lds, kPersistPerCu);          \
+        const dim3 grid((uint32_t)(items < cap ? items : cap)), block(kThreads);               \
+        hipLaunchKernelGGL(KERNEL, grid, block, lds, s, x, y, g, b, inv_full);                 \
     } while (0)
+#define CM_BAND(KW_, SH_, P_) CM_LAUNCH((pool_band<KIND, KW_, KW_, SH_, P_>))
 #define CM_BAND_P(KW_, SH_) \
     do { if (pair == 1) CM_BAND(KW_, SH_, 1); else if (pair == 2) CM_BAND(KW_, SH_, 2); else CM_BAND(KW_, SH_, 0); } while (0)
+#define CM_STRIP(KW_, SH_, P_) CM_LAUNCH((pool_strip<KIND, KW_, SH_, P_>))
+#define CM_STRIP_P(KW_, SH_) \
+    do { if (pair == 1) CM_STRIP(KW_, SH_, 1); else if (pair == 2) CM_STRIP(KW_, SH_, 2); else CM_STRIP(KW_, SH_, 0); } while (0)
+            if (one_pass) {
+                if (kwin == 3) {
+                    if (sh == 2) CM_STRIP_P(3, 2); else CM_STRIP_P(3, 1);
+                } else {
+                    if (sh == 2) CM_STRIP_P(2, 2); else CM_STRIP_P(2, 1);
+                }
+                return cm_check_launch("pool_strip");
+            }
             if (kwin == 3) {
                 if (sh == 2) CM_BAND_P(3, 2); else if (sh == 1) CM_BAND_P(3, 1); else CM_BAND(3, 0, 0);
             } else if (kwin == 2) {
@@ -538,8 +720,11 @@ int pool_launch(const int16_t* x, int16_t* y, uint64_t planes, const PoolGeom& g
             } else {
                 CM_BAND(0, 0, 0);
             }
+#undef CM_STRIP_P
+#undef CM_STRIP
 #undef CM_BAND_P
 #undef CM_BAND
+#undef CM_LAUNCH
             return cm_check_launch("pool_band");
         }
     }

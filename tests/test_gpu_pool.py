@@ -42,6 +42,18 @@ EDGE_CASES = [
     (2, 4, 56, 56, 56, 56, 1, 1, 0, 0, 1, 1),   # global (wave reduction path)
     (1, 3, 7, 9, 7, 9, 1, 1, 0, 0, 1, 1),       # global, plane not a multiple of 8
     (3, 2, 33, 31, 4, 4, 4, 4, 0, 0, 1, 1),
+    # widths a multiple of 8 with 2x2 / 3x3 windows and row stride 1 or 2: the
+    # one-strip-per-thread path (pair reads at even / odd offsets, several bands
+    # per plane, a 255-wide output, and more items than twice the grid)
+    (2, 3, 16, 16, 3, 3, 2, 2, 1, 1, 1, 1),
+    (1, 4, 24, 32, 2, 2, 2, 2, 0, 0, 1, 1),
+    (1, 3, 40, 128, 3, 3, 1, 1, 1, 1, 1, 1),
+    (2, 2, 21, 64, 2, 2, 1, 2, 0, 1, 1, 1),
+    (1, 2, 9, 512, 3, 3, 2, 2, 0, 0, 1, 1),
+    (1, 1, 8, 8, 3, 3, 1, 1, 1, 1, 1, 1),
+    (1, 2, 12, 16, 3, 3, 2, 3, 1, 1, 1, 1),
+    (32, 128, 8, 16, 2, 2, 2, 2, 0, 0, 1, 1),
+    (16, 512, 8, 8, 3, 3, 1, 1, 1, 1, 1, 1),
 ]
 
 
