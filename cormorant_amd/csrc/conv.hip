@@ -278,6 +278,11 @@ int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int1
             default: return launch_direct<32>(g, s);
         }
     }
+    {
+        const int rc = cm_conv_patch_launch(x, w, b, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w,
+                                            kh, kw, sh, sw, dh, dw, pad_top, pad_left, epi, s);
+        if (rc != 1) return rc;
+    }
     // 1x1 / stride 1 / no padding as one GEMM per image, when an image's
     // pixels fill its 128-column tiles to at least 80 %; small planes (e.g.
     // 7x7, 14x14) go through the gather path, whose columns run across images
