@@ -38,7 +38,6 @@ typedef short v2s __attribute__((ext_vector_type(2)));
 constexpr int kThreads = 256;
 constexpr int TH = 8, TW = 16, TP = TH * TW;   // output tile: 8 rows x 16 columns
 constexpr int kTilePitch = TP + 4;             // epilogue tile: uint32 per row
-constexpr uint32_t kMaxChunks = 36;            // 16-wide k chunks: 9 taps x 64 channels / 16
 constexpr int kAB = 6;                         // weight vectors in flight per thread
 constexpr int kPB = 6;                         // patch tasks (4 loads each) in flight per thread
 
@@ -81,7 +80,6 @@ __global__ __launch_bounds__(kThreads, MT <= 32 ? 4 : 2) void conv_patch(PatchAr
     constexpr int PW = PG::PW, NPOS = PG::NPOS;
     constexpr int MI = MT / 16;   // MFMA row tiles
     extern __shared__ __align__(16) uint8_t lds[];
-    __shared__ int32_t chunk_off[kMaxChunks];
     __shared__ uint32_t colsum[TP], rowsum[MT], biasv[MT];
     uint8_t* a_hi = lds;
     uint8_t* a_lo = lds + MT * g.apitch;
@@ -99,15 +97,6 @@ __global__ __launch_bounds__(kThreads, MT <= 32 ? 4 : 2) void conv_patch(PatchAr
     const uint32_t Q = 9 * g.C16 / 16;   // chunks holding real taps
     const uint32_t cpt = g.C16 / 16;     // chunks per tap
 
-    if (tid < g.nk * 4) {
-        int32_t off = 0;   // chunks past the last tap read position 0 and are zeroed
-        if (tid < Q) {
-            const uint32_t tap = tid / cpt, c0 = (tid - tap * cpt) * 16;
-            const uint32_t khi = tap / 3, kwi = tap - khi * 3;
-            off = (int32_t)((khi * PW + kwi) * g.ppitch + c0);
-        }
-        chunk_off[tid] = off;
-    }
 
     // Weight limb planes: row m, byte (tap * C16 + c).  They start as the
     // encoding of 0 (high 0, low 0x80), which padding channels, k past 9*C16
@@ -242,10 +231,14 @@ __global__ __launch_bounds__(kThreads, MT <= 32 ? 4 : 2) void conv_patch(PatchAr
     int32_t rh[MI], rl[MI], ch[2] = {0, 0}, cl[2] = {0, 0};
 #pragma unroll
     for (int i = 0; i < MI; ++i) { rh[i] = 0; rl[i] = 0; }
+    // chunk q = tap * cpt + c0 / 16: its offset from the column's window origin,
+    // in registers (tap = q / cpt by a multiply: exact for q < 36, cpt <= 4)
+    const uint32_t m_cpt = (256u + cpt - 1u) / cpt;
     for (uint32_t it = 0; it < g.nk; ++it) {
         const uint32_t q = it * 4 + qin;
         const bool real = q < Q;
-        const uint32_t off = (uint32_t)chunk_off[q];
+        const uint32_t tap = (q * m_cpt) >> 8, khi = tap / 3, kwi = tap - khi * 3;
+        const uint32_t off = real ? (khi * PW + kwi) * g.ppitch + (q - tap * cpt) * 16 : 0u;
         v4i ah[MI], al[MI];
 #pragma unroll
         for (int i = 0; i < MI; ++i) {

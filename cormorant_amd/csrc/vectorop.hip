@@ -42,7 +42,10 @@ __device__ __forceinline__ v8s apply8(v8s a, v8s b) {
 constexpr bool is_binary(int op) { return op < CM_OP_RELU; }
 
 constexpr int kThreads = 256;
-constexpr int kUnroll = 4;
+// 16-byte vectors per thread (all loads issued before any op): 2 measured best
+// on the 64 Mi sweep -- DIV, whose per-element work keeps a wave longer between
+// its loads and its stores, 69 us against 73-75 us at 4; the other ops equal
+constexpr int kUnroll = 2;
 
 // Flat stream over nvec 16-byte vectors + a scalar tail of `tail` elements.
 template <int OP>
