@@ -70,15 +70,17 @@ GEOMS = [
     (3, 32, 112, 100, 16, 1, 1, 1, 1, 1, 1, 0, 0, 1, 0),  # 1x1, K = 32, 16 channels
     (3, 16, 110, 110, 20, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0),  # 20 channels in a group of 24
     (1, 7, 200, 190, 5, 2, 2, 1, 1, 2, 3, 3, 1, 1, 0),    # 2x2 dilated, padding, 5 channels
-    # 3x3 patch path (channels a multiple of 8, <= 64 of them in and out): partial
-    # 8x16 tiles, padding channels, dead weight rows, every output access width
-    (2, 32, 37, 45, 32, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0),    # odd output width (1-wide stores)
-    (1, 16, 30, 60, 16, 3, 3, 2, 2, 1, 1, 1, 1, 0, 0),    # stride 2, no bias, width 30
-    (2, 24, 28, 28, 24, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0),    # 24 of 32 channels, 24 of 32 rows
-    (1, 64, 20, 24, 64, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0),    # 64 x 64, nine k steps
-    (1, 8, 18, 34, 5, 3, 3, 2, 2, 1, 1, 0, 0, 1, 0),      # 8 channels, 5 outputs, no padding
-    (1, 40, 16, 16, 48, 3, 3, 1, 1, 1, 1, 2, 2, 1, 0),    # 48-byte positions, padding 2
-    (1, 56, 9, 12, 33, 3, 3, 2, 2, 1, 1, 2, 1, 1, 0),     # 80-byte positions, pads 2 / 1
+    # 3x3 patch path (channels a multiple of 8, <= 64 of them in and out, at least
+    # 64 output tiles of 8 x 16): partial tiles, padding channels, dead weight
+    # rows, every output access width
+    (32, 32, 9, 17, 32, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0),    # odd output width (1-wide stores)
+    (16, 16, 30, 60, 16, 3, 3, 2, 2, 1, 1, 1, 1, 0, 0),   # stride 2, no bias, width 30
+    (8, 24, 28, 28, 24, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0),    # 24 of 32 channels, 24 of 32 rows
+    (12, 64, 20, 24, 64, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0),   # 64 x 64, nine k steps
+    (64, 8, 18, 34, 5, 3, 3, 2, 2, 1, 1, 0, 0, 1, 0),     # 8 channels, 5 outputs, no padding
+    (16, 40, 16, 16, 48, 3, 3, 1, 1, 1, 1, 2, 2, 1, 0),   # 48-byte positions, padding 2
+    (64, 56, 9, 12, 33, 3, 3, 2, 2, 1, 1, 2, 1, 1, 0),    # 80-byte positions, pads 2 / 1
+    (2, 32, 37, 45, 32, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0),    # the same layer under 64 tiles: gather
 ]
 
 

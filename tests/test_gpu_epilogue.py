@@ -89,8 +89,9 @@ def test_matmul_column_add_strided_rows():
 
 CONV_CASES = [
     # name, N, C, H, W, M, k, s, d, p, depthwise
-    ("3x3_s1_patch", 2, 16, 20, 20, 24, 3, 1, 1, 1, 0),
-    ("3x3_s2_patch", 3, 8, 17, 15, 40, 3, 2, 1, 1, 0),
+    ("3x3_s1_patch", 16, 16, 20, 20, 24, 3, 1, 1, 1, 0),
+    ("3x3_s2_patch", 64, 8, 17, 15, 40, 3, 2, 1, 1, 0),
+    ("3x3_s2_small", 3, 8, 17, 15, 40, 3, 2, 1, 1, 0),
     ("3x3_s1_tab", 2, 20, 20, 20, 24, 3, 1, 1, 1, 0),
     ("1x1_pointwise", 2, 24, 14, 14, 32, 1, 1, 1, 0, 0),
     ("3x3_inc_k2304", 1, 256, 9, 9, 20, 3, 1, 1, 1, 0),
