@@ -1,6 +1,6 @@
 """Benchmark of the MI355X Q8.8 kernels (one JSON line on stdout).
 
-Headline workload (the BASELINE metric's vector-op configuration): one step is
+Headline workload (the headline metric's vector-op configuration): one step is
 the six-op VectorOP sweep -- Add, Sub, Mul, Div, Relu, Clip(0,6) -- over
 67,108,864-element int16 Q8.8 tensors (70% uniform over [-8, 8), 30% pinned at
 the saturation edges), every op with its own operand buffers (2.3 GB touched
@@ -476,7 +476,7 @@ def main() -> int:
     if args.quick:
         work, args.no_cpu = {"vecop"}, True
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py: this build measures one MI355X; multi-GPU runs are not part of it "
+        print("bench.py measures one MI355X; multi-GPU runs are not part of it "
               "(--gpus must be 1).", file=sys.stderr)
         return 2
 

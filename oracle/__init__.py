@@ -10,7 +10,7 @@ Two independent restatements of the reference arithmetic live here:
   (inference-scheduler/src/codegen/_simulate.py:49-383).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline leg
-may import this package, and only as the checker.  The product package
+may import this package, and only to check results.  The product package
 ``cormorant_amd`` never imports it.
 """
 from __future__ import annotations

@@ -2,7 +2,7 @@
 
 Markers:
   gpu -- needs an MI355X (gfx950) and the built libcormorant_amd.so.  GPU tests
-         are skipped only when no GPU device exists at all; on a GPU box a
+         are skipped only when no GPU device exists at all; on a GPU host a
          missing or unloadable library is a hard failure, never a fallback.
 """
 import os

@@ -27,7 +27,7 @@ def empty_dev(shape, fill: int = 0x5A5A):
 
 
 def oracle_threads() -> int:
-    """CPU threads for the oracle on this host (the GPU box share is 16)."""
+    """CPU threads for the oracle on this host (at most 16, one GPU host's CPU share)."""
     n = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
     return n if n > 0 else min(os.cpu_count() or 1, 16)
 

@@ -306,7 +306,7 @@ def test_lp2_finalizer_float32_path_above_2_24():
     f_lp2 = oracle.lib().ora_lp2_finalize
     got = np.fromiter((f_lp2(int(x)) for x in a), dtype=np.int64, count=a.size)
     np.testing.assert_array_equal(got, want)
-    # the survey's first float32-vs-float64 divergence: A = 16785407 -> 16.0039 (not 16.0)
+    # the first float32-vs-float64 divergence above 2^24: A = 16785407 -> 16.0039 (not 16.0)
     assert oracle.lp2_finalize(16785407) == 4097 and math.isqrt(16785407) == 4096
     assert oracle.lp2_finalize(-5) == 0         # wrapped accumulator: NaN -> 0 (unpinned)
 
