@@ -107,7 +107,12 @@ __global__ __launch_bounds__(kDirThreads) void conv_direct(DirArgs g) {
     extern __shared__ __align__(16) uint32_t dsm[];
     uint32_t* wt = dsm;                                          // [Kc / 2][MT]
     int2* tab = reinterpret_cast<int2*>(dsm + (g.Kc / 2) * MT);   // [Kc + kDirChunk]
+    // bias << 8 of the block's channels, staged with the weights so that the
+    // epilogue does not start with a memory round trip
+    uint32_t* bsm = reinterpret_cast<uint32_t*>(tab + g.Kc + kDirChunk);   // [MT]
     const uint32_t m0 = blockIdx.y * MT;
+    if (threadIdx.x < (uint32_t)MT)
+        bsm[threadIdx.x] = HAS_BIAS ? q88::data_to_acc(g.bias[min(m0 + threadIdx.x, g.M - 1u)]) : 0u;
     const uint32_t kk = g.kh * g.kw, hw = g.H * g.W;
     // k >= K (padding up to Kc, and one chunk past it that the last prefetch
     // reads) is tap 31, which every thread treats as outside the image
@@ -206,7 +211,7 @@ __global__ __launch_bounds__(kDirThreads) void conv_direct(DirArgs g) {
     for (int mm = 0; mm < MT; ++mm) {
         const uint32_t m = m0 + mm;
         uint32_t v = acc[mm];
-        if (HAS_BIAS) v += q88::data_to_acc(g.bias[min(m, g.M - 1u)]);
+        if (HAS_BIAS) v += bsm[mm];
         const int32_t yv = q88::clamp(q88::add(q88::acc_to_data(v), res[mm]), lo, hi);
         if (m < g.M) g.y[ybase + (uint64_t)m * g.P] = (int16_t)yv;
     }
@@ -225,7 +230,7 @@ uint32_t direct_channels(uint64_t K, uint32_t out_ch, uint32_t kk, uint64_t npix
 template <int MT>
 int launch_direct(const DirArgs& g, hipStream_t s) {
     const dim3 grid((g.npix + kDirThreads - 1) / kDirThreads, (g.M + MT - 1) / MT);
-    const size_t lds = (size_t)(g.Kc / 2) * MT * 4u + (size_t)(g.Kc + kDirChunk) * 8u;
+    const size_t lds = (size_t)(g.Kc / 2) * MT * 4u + (size_t)(g.Kc + kDirChunk) * 8u + MT * 4u;
     if (g.bias) hipLaunchKernelGGL((conv_direct<MT, true>), grid, dim3(kDirThreads), lds, s, g);
     else hipLaunchKernelGGL((conv_direct<MT, false>), grid, dim3(kDirThreads), lds, s, g);
     return cm_check_launch("conv_direct");
