@@ -111,8 +111,33 @@ __global__ __launch_bounds__(kDirThreads) void conv_direct(DirArgs g) {
     // epilogue does not start with a memory round trip
     uint32_t* bsm = reinterpret_cast<uint32_t*>(tab + g.Kc + kDirChunk);   // [MT]
     const uint32_t m0 = blockIdx.y * MT;
-    if (threadIdx.x < (uint32_t)MT)
-        bsm[threadIdx.x] = HAS_BIAS ? q88::data_to_acc(g.bias[min(m0 + threadIdx.x, g.M - 1u)]) : 0u;
+    // Weight words (k pair, channel): at most 16 x MT (K <= 32), two per thread.
+    // Their loads and the bias load are buffer loads issued before anything is
+    // stored, so one memory round trip covers them and overlaps the k table
+    // below; taps past K and channels past M read 0 (offsets with bit 31 set).
+    constexpr int WPT = (16 * MT + kDirThreads - 1) / kDirThreads;
+    const uint32_t nwords = (g.Kc / 2) * MT;
+    uint32_t wlo[WPT], whi[WPT];
+    {
+        const __amdgpu_buffer_rsrc_t wr = make_rsrc(g.w, g.M * g.K * 2u);
+#pragma unroll
+        for (int u = 0; u < WPT; ++u) {
+            const uint32_t i = u * kDirThreads + threadIdx.x;
+            const uint32_t kp = i / MT, mm = i - kp * MT;
+            const uint32_t m = m0 + mm, k = 2 * kp;
+            const uint32_t ok = (uint32_t)(i < nwords) & (uint32_t)(m < g.M);
+            const uint32_t base = ((m * g.K + k) * 2u) & 0x7FFFFFFFu;
+            const uint32_t ok_lo = ok & (uint32_t)(k < g.K), ok_hi = ok & (uint32_t)(k + 1 < g.K);
+            wlo[u] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(wr, base | ((ok_lo ^ 1u) << 31), 0, 0);
+            whi[u] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(wr, (base + 2u) | ((ok_hi ^ 1u) << 31), 0, 0);
+        }
+    }
+    uint32_t bias_v = 0;
+    if constexpr (HAS_BIAS) {
+        const __amdgpu_buffer_rsrc_t br = make_rsrc(g.bias, g.M * 2u);
+        const uint32_t m = min(m0 + threadIdx.x, g.M - 1u);
+        bias_v = q88::data_to_acc((int32_t)(int16_t)__builtin_amdgcn_raw_buffer_load_b16(br, m * 2u, 0, 0));
+    }
     const uint32_t kk = g.kh * g.kw, hw = g.H * g.W;
     // k >= K (padding up to Kc, and one chunk past it that the last prefetch
     // reads) is tap 31, which every thread treats as outside the image
@@ -122,17 +147,12 @@ __global__ __launch_bounds__(kDirThreads) void conv_direct(DirArgs g) {
         tab[k] = k < g.K ? int2{(int)(2u * (c * hw + khi * g.dh * g.W + kwi * g.dw)), (int)r}
                          : int2{0, 31};
     }
-    for (uint32_t i = threadIdx.x; i < (g.Kc / 2) * MT; i += kDirThreads) {
-        const uint32_t kp = i / MT, mm = i - kp * MT;
-        const uint32_t m = m0 + mm, k = 2 * kp;
-        uint32_t lo = 0, hi = 0;
-        if (m < g.M) {
-            const int16_t* wm = g.w + (uint64_t)m * g.K;
-            if (k < g.K) lo = (uint16_t)wm[k];
-            if (k + 1 < g.K) hi = (uint16_t)wm[k + 1];
-        }
-        wt[i] = lo | hi << 16;
+#pragma unroll
+    for (int u = 0; u < WPT; ++u) {
+        const uint32_t i = u * kDirThreads + threadIdx.x;
+        if (i < nwords) wt[i] = wlo[u] | whi[u] << 16;
     }
+    if (threadIdx.x < (uint32_t)MT) bsm[threadIdx.x] = bias_v;
 
     const uint32_t pix = blockIdx.x * kDirThreads + threadIdx.x;
     const bool pok = pix < g.npix;
