@@ -107,3 +107,34 @@ def test_config4_full_size(case):
                           case.k, case.k, case.stride, case.stride, case.dil, case.dil, case.pad,
                           case.pad, 1, 0)
     np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_patch_path_random(seed):
+    """Random 3x3 shapes that take the patch path (channels a multiple of 8, <= 64
+    in and out, >= 64 output tiles): full-range operands, random padding, stride,
+    bias, fused Add and activation."""
+    g = wl.rng(977, seed)
+    C = int(g.choice([8, 16, 24, 32, 40, 48, 56, 64]))
+    M = int(g.integers(1, 65))
+    S = int(g.choice([1, 2]))
+    pt, pl = int(g.integers(0, 3)), int(g.integers(0, 3))
+    H, W = int(g.integers(5, 40)), int(g.integers(5, 70))
+    OH, OW = (H + 2 * pt - 3) // S + 1, (W + 2 * pl - 3) // S + 1
+    tiles_img = ((OH + 7) // 8) * ((OW + 15) // 16)
+    N = -(-64 // tiles_img)
+    bias, act = int(g.integers(0, 2)), int(g.integers(0, 3))
+    say(f"conv patch random seed {seed}: {(N, C, H, W, M, S, pt, pl, bias, act)}")
+    x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
+    w = g.integers(-32768, 32768, M * C * 9, dtype=np.int16)
+    b = g.integers(-32768, 32768, M, dtype=np.int16)
+    add = g.integers(-32768, 32768, N * M * OH * OW, dtype=np.int16)
+    want = np.zeros(N * M * OH * OW, np.int16)
+    oracle.set_threads(oracle_threads())
+    oracle.conv(x, w, b, want, N, C, H, W, M, OH, OW, 3, 3, S, S, 1, 1, pt, pl, bias, 0, threads=True)
+    want = np.clip(want.astype(np.int32) + add, -32768, 32767)   # fused Add: saturating
+    want = np.clip(want, 0, 32767 if act == K.ACT_RELU else 1536) if act else want
+    y = empty_dev(N * M * OH * OW)
+    K.ConvKernel(dev(x), dev(w), dev(b), y, N, C, H, W, M, OH, OW, 3, 3, S, S, 1, 1, pt, pl, bias, 0,
+                 add=dev(add), act=act)
+    np.testing.assert_array_equal(host(y).astype(np.int32), want)
