@@ -101,3 +101,24 @@ def test_avg_finalizer_all_accumulators(d):
     say(f"avg sweep d={d}")
     oracle.set_threads(oracle_threads())
     assert K.selftest_finalize(1, 0, 1 << 24, d) == oracle.avg_checksum(0, 1 << 24, d)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_strip_path_random(seed):
+    """Random shapes on the one-strip-per-thread path (2x2 / 3x3 window, row
+    stride 1 or 2, rows a multiple of 8 elements, output width <= 256): every
+    pool type, padding, column stride and count_include_pad, full-range values."""
+    g = wl.rng(811, seed)
+    k = int(g.choice([2, 3]))
+    sh, sw = int(g.choice([1, 2])), int(g.choice([1, 2, 3]))
+    pt, pl = int(g.integers(0, k)), int(g.integers(0, k))
+    H, W = int(g.integers(k, 40)), 8 * int(g.integers(1, 24))
+    N, C = int(g.integers(1, 4)), int(g.integers(1, 40))
+    ptype, lp = [(0, 0), (1, 0), (2, 1), (2, 2)][int(g.integers(0, 4))]
+    cip = int(g.integers(0, 2)) if ptype == 1 else 0
+    OH = (H + 2 * pt - k) // sh + 1
+    OW = (W + 2 * pl - k) // sw + 1
+    say(f"pool strip random seed {seed}: {(N, C, H, W, k, sh, sw, pt, pl, ptype, lp, cip)}")
+    x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
+    got, want = pool_both(x, N, C, H, W, OH, OW, k, k, sh, sw, pt, pl, 1, 1, ptype, lp, cip)
+    np.testing.assert_array_equal(got, want)
