@@ -8,22 +8,30 @@ per step, far beyond the 256 MB Infinity Cache).  `value` is the aggregate
 GB/s of the step with the reference formula ports * elements * 2 B / time,
 ports = 3 for binary and 2 for unary ops (bench_src/bench_vectorop.c:93-95).
 
-The same run also reports (under "results") the GEMM, convolution and pooling
-configurations: Q8.8 GOP/s = 2*MAC / t (bench_matmul.c:95, bench_conv.c:129-132)
-with the int8-MFMA utilisation of the four limb products, and pool GB/s =
-(x + y) * 2 B / t (bench_pool.c:116-117) with rotating input buffers, next to a
-VectorOP copy of the same byte count timed the same way (the streaming ceiling
-at that size, `frac_of_copy_ceiling`); and the
-two ONNX graphs run by the scheduler's HIP backend: the MLP's batch-64 latency
-and the MobileNetV2-like graph's images/s at batch 16, each with its roofline
-fraction (sum of per-kernel lower bounds / measured time).  CPU figures (the oracle,
-a C restatement of the reference C-simulation loops, on this host): one thread
-(the faithful C-simulation path, `cpu_baseline.value` and each result's
-`cpu.gops` / `cpu.gbs`) and OpenMP over the independent outer loop (`*_mt`);
-`host` records the CPU model and the thread count.
+The same run also reports, under "results":
+* the GEMM configurations and the conv + pool block: Q8.8 GOP/s = 2*MAC / t
+  (bench_matmul.c:95, bench_conv.c:129-132) with the int8-MFMA utilisation of
+  the four limb products; conv A and conv B, then MaxPool / AvgPool / LpPool /
+  GlobalAveragePool on each convolution's own output, pool GB/s = (x + y) * 2 B
+  / t (bench_pool.c:116-117) with rotating inputs larger than the Infinity
+  Cache, next to a VectorOP copy of the same byte count timed the same way
+  (`frac_of_copy_ceiling`);
+* the two ONNX graphs run by the scheduler's HIP backend: the MLP's batch-64
+  latency and the MobileNetV2-like graph's images/s at batch 16, each with its
+  roofline fraction (sum of per-kernel lower bounds / measured time);
+* `perf_cases`: the reference's per-kernel case list (perf_config.json.example
+  and the published KV260 report's rows) through cm_bench, the C counterpart
+  of bench_src/bench_*.c, one record per case with the reference's fields and
+  the published KV260 figures beside it, every output checked against the
+  oracle.
+CPU figures (the oracle, a C restatement of the reference C-simulation loops, on
+this host): one thread (the faithful C-simulation path, `cpu_baseline.value` and
+each result's `cpu.gops` / `cpu.gbs`; GEMM / conv on a stated slice) and OpenMP
+over the independent outer loop (`*_mt`, the whole product, which also checks
+the GPU output bit for bit); `host` records the CPU model and the thread count.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
-                       [--workloads vecop,gemm,conv,pool,graphs] [--no-cpu]
+                       [--workloads vecop,gemm,conv,pool,graphs,cases] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -70,8 +78,7 @@ def time_graph(calls, steps: int) -> float:
     """Mean duration (ms) of one launch with host overhead removed: `steps`
     launches (cycling through `calls`) are captured into one HIP graph, which is
     replayed once untimed and then once between HIP events.  The calls run once
-    eagerly on the capture stream first (per-stream split-K workspaces are
-    allocated there; nothing is allocated during capture)."""
+    eagerly on the capture stream first."""
     import torch
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -154,14 +161,24 @@ def bench_gemm(steps: int, warmup: int):
     return out
 
 
-# ------------------------------------------------------------------- conv --
-def bench_conv(steps: int, warmup: int):
+# ------------------------------------------------------- conv + pool block --
+MALL_BYTES = 256 << 20      # MI355X Infinity Cache: rotating inputs must exceed it
+POOL_ROTATE_MIN = 12
+
+
+def bench_block(steps: int, warmup: int):
+    """Conv A and conv B (timed back to back on one input), then the four pools on
+    each convolution's own device output.  Pool inputs rotate over copies of that
+    output totalling more than the Infinity Cache, timed as a HIP graph of
+    back-to-back launches, next to a VectorOP copy of the same byte count timed
+    the same way (the streaming ceiling at that size)."""
     import torch
     from cormorant_amd import kernels as K
     from cormorant_amd import workloads as wl
     out = {}
     x, w, b = wl.conv_operands(wl.CONV_CASES[0])
     dx, dw_, db = dev(x), dev(w), dev(b)
+    conv_out = {}
     for case in wl.CONV_CASES:
         o = case.out_hw
         dy = torch.empty(case.batch * case.out_ch * o * o, dtype=torch.int16, device="cuda")
@@ -177,49 +194,42 @@ def bench_conv(steps: int, warmup: int):
                   f"s{case.stride} d{case.dil} p{case.pad} bias -> {o}x{o}",
             ms=round(ms, 5), gops=round(gops, 1),
             mfma_int8_tops=round(LIMB_PRODUCTS * gops / 1e3, 2),
-            mfma_frac=round(LIMB_PRODUCTS * gops / 1e3 / INT8_PEAK_TOPS, 4),
-            kernel="q88_gemm (implicit GEMM)")
+            mfma_frac=round(LIMB_PRODUCTS * gops / 1e3 / INT8_PEAK_TOPS, 4))
         out[case.name]["_dev"] = (dx, dw_, db, dy, x, w, b)
-    return out
-
-
-# ------------------------------------------------------------------- pool --
-POOL_ROTATE = 12     # 12 x 25.7 MB inputs > 256 MB Infinity Cache
-
-
-def bench_pool(steps: int, warmup: int):
-    import torch
-    from cormorant_amd import kernels as K
-    from cormorant_amd import workloads as wl
-    n, c, hw = 32, 128, 56
-    xs = [dev(wl.uniform_q88(wl.rng(5, i), (n, c, hw, hw), -4.0, 4.0)) for i in range(POOL_ROTATE)]
-    out = {}
-    for case in wl.POOL_CASES:
-        a = wl.pool_args(case, n, c, hw)
+        conv_out[case.name] = (dy, o)
+    ceilings = {}
+    for cv, pc, name in wl.block_pools():
+        dy, o = conv_out[cv.name]
+        n, c = cv.batch, cv.out_ch
+        rot = max(POOL_ROTATE_MIN, -(-MALL_BYTES // (dy.numel() * 2)) + 1)
+        xs = [dy] + [dy.clone() for _ in range(rot - 1)]
+        a = wl.pool_args(pc, n, c, o)
         ny = n * c * a["out_h"] * a["out_w"]
-        ys = [torch.empty(ny, dtype=torch.int16, device="cuda") for _ in range(POOL_ROTATE)]
-        calls = [lambda i=i: K.PoolingKernel(xs[i], ys[i], **a) for i in range(POOL_ROTATE)]
+        ys = [torch.empty(ny, dtype=torch.int16, device="cuda") for _ in range(rot)]
+        calls = [lambda i=i: K.PoolingKernel(xs[i], ys[i], **a) for i in range(rot)]
         for i in range(warmup):
-            calls[i % POOL_ROTATE]()
-        ms = time_graph(calls, max(steps, 4 * POOL_ROTATE))
-        nbytes = (n * c * hw * hw + ny) * 2
+            calls[i % rot]()
+        ms = time_graph(calls, max(steps, 4 * rot))
+        nbytes = (dy.numel() + ny) * 2
         gbs = nbytes / (ms * 1e-3) / 1e9
-        out[case.name] = dict(ms=round(ms, 5), gbs=round(gbs, 1),
-                              hbm_frac=round(gbs / HBM_PEAK_GBS, 4), bytes=nbytes,
-                              rotating_inputs=POOL_ROTATE, timing="HIP graph of back-to-back launches")
-        out[case.name]["_dev"] = (xs[0], ys[0], a)
-    # Streaming ceiling at this size: VectorOP copy moving the largest pool's byte
-    # count (half read, half written), same rotation and graph timing.  At ~32 MB
-    # a launch's ramp and tail are a visible share of its time.
-    ncopy = max(e["bytes"] for e in out.values()) // 4
-    dst = [torch.empty(ncopy, dtype=torch.int16, device="cuda") for _ in range(POOL_ROTATE)]
-    calls = [lambda i=i: K.VectorOPKernel(xs[i], None, dst[i], ncopy, 6) for i in range(POOL_ROTATE)]
-    ms = time_graph(calls, max(steps, 4 * POOL_ROTATE))
-    gbs = 4 * ncopy / (ms * 1e-3) / 1e9
-    for e in out.values():
-        e["frac_of_copy_ceiling"] = round(e["gbs"] / gbs, 4)
-    out["pool_copy_ceiling"] = dict(ms=round(ms, 5), gbs=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4),
-                                    bytes=4 * ncopy, kernel="vecop_flat<6>", rotating_inputs=POOL_ROTATE)
+        if o not in ceilings:   # VectorOP copy of the largest pool's byte count, same timing
+            ncopy = (dy.numel() + n * c * (o // 2) ** 2) // 2
+            src = [t[:ncopy] for t in xs]
+            dst = [torch.empty(ncopy, dtype=torch.int16, device="cuda") for _ in range(rot)]
+            ccalls = [lambda i=i: K.VectorOPKernel(src[i], None, dst[i], ncopy, 6) for i in range(rot)]
+            cms = time_graph(ccalls, max(steps, 4 * rot))
+            ceilings[o] = dict(ms=round(cms, 5), gbs=round(4 * ncopy / (cms * 1e-3) / 1e9, 1),
+                               bytes=4 * ncopy, kernel="vecop_flat<6>", rotating_inputs=rot)
+            ceilings[o]["hbm_frac"] = round(ceilings[o]["gbs"] / HBM_PEAK_GBS, 4)
+            del dst
+        out[name] = dict(input=f"{cv.name} output [{n},{c},{o},{o}]", ms=round(ms, 5),
+                         gbs=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4), bytes=nbytes,
+                         frac_of_copy_ceiling=round(gbs / ceilings[o]["gbs"], 4),
+                         rotating_inputs=rot, timing="HIP graph of back-to-back launches")
+        out[name]["_dev"] = (dy, ys[0], a)
+        del xs
+    for o, cl in ceilings.items():
+        out[f"pool_copy_ceiling_{o}x{o}"] = cl
     return out
 
 
@@ -353,101 +363,103 @@ def cpu_baseline(vec_bufs, extras: dict):
         t_mt += time.perf_counter() - t0
     res["vecop"].update(gbs_mt=bytes_total / t_mt / 1e9, seconds_mt=t_mt, threads_mt=mt)
     oracle.set_threads(1)
-    # GEMM 3a: one of the 32 batches (1024^3); GEMM 3b: 16 rows
-    if "gemm_b32_1024" in extras:
-        da, db, dc, a, b = extras["gemm_b32_1024"].pop("_dev")
-        n = k = m = 1024
-        want = np.empty(n * m, np.int16)
+    # GEMM / conv: the whole product with OpenMP (it also checks the GPU output
+    # bit for bit), and a slice on one thread (the faithful C-simulation path;
+    # the whole product would take minutes), scaled by its share of the MACs
+    from cormorant_amd import workloads as wl
+
+    def timed(fn, threads):
+        oracle.set_threads(threads)
         t0 = time.perf_counter()
-        oracle.matmul(np.ascontiguousarray(a[0]).reshape(-1), np.ascontiguousarray(b[0]).reshape(-1),
-                      want, n, k, m)
-        dt = time.perf_counter() - t0
-        if not np.array_equal(dc[: n * m].cpu().numpy(), want):
-            raise SystemExit("bench: GPU gemm batch 0 differs from the oracle")
-        res["gemm_b32_1024"] = dict(gops=2.0 * n * k * m / dt / 1e9, seconds=dt,
-                                    sample="batch 0 of 32 (1024^3)")
-        oracle.set_threads(mt)
-        t0 = time.perf_counter()
-        oracle.matmul(np.ascontiguousarray(a[0]).reshape(-1), np.ascontiguousarray(b[0]).reshape(-1),
-                      want, n, k, m, threads=True)
+        fn()
         dt = time.perf_counter() - t0
         oracle.set_threads(1)
-        res["gemm_b32_1024"].update(gops_mt=2.0 * n * k * m / dt / 1e9, seconds_mt=dt, threads_mt=mt)
-    if "gemm_b1_4096" in extras:
-        da, db, dc, a, b = extras["gemm_b1_4096"].pop("_dev")
-        n = k = m = 4096
-        a2, b2 = a.reshape(n, k), b.reshape(k, m)
-        got = dc.cpu().numpy().reshape(n, m)
-        rows = list(range(0, n, n // 16))
-        t0 = time.perf_counter()
-        for r in rows:
-            if not np.array_equal(got[r], oracle.matmul_row(a2[r], b2, k, m)):
-                raise SystemExit(f"bench: GPU gemm 4096 row {r} differs from the oracle")
-        dt = time.perf_counter() - t0
-        res["gemm_b1_4096"] = dict(gops=2.0 * len(rows) * k * m / dt / 1e9, seconds=dt,
-                                   sample=f"{len(rows)} of 4096 rows")
-        nr = 128
-        part = np.empty(nr * m, np.int16)
-        oracle.set_threads(mt)
-        t0 = time.perf_counter()
-        oracle.matmul(np.ascontiguousarray(a2[:nr]).reshape(-1), np.ascontiguousarray(b2).reshape(-1),
-                      part, nr, k, m, threads=True)
-        dt = time.perf_counter() - t0
-        oracle.set_threads(1)
-        if not np.array_equal(got[:nr].reshape(-1), part):
-            raise SystemExit("bench: GPU gemm 4096 rows 0-127 differ from the oracle")
-        res["gemm_b1_4096"].update(gops_mt=2.0 * nr * k * m / dt / 1e9, seconds_mt=dt, threads_mt=mt,
-                                   sample_mt=f"rows 0-{nr - 1}")
-    for name in ("conv_a_3x3_s1_p1", "conv_b_3x3_s2_d2_p2"):
-        if name not in extras:
+        return dt
+
+    for cid, case in enumerate(wl.GEMM_CASES):
+        if case.name not in extras:
             continue
-        from cormorant_amd import workloads as wl
-        case = [c for c in wl.CONV_CASES if c.name == name][0]
-        dx, dw_, db_, dy, x, w, b = extras[name].pop("_dev")
+        da, db, dc, a, b = extras[case.name].pop("_dev")
+        n, k, m, bt = case.n, case.k, case.m, case.batch
+        a1, b1 = np.ascontiguousarray(a).reshape(-1), np.ascontiguousarray(b).reshape(-1)
+        want = np.empty(bt * n * m, np.int16)
+        dt_mt = timed(lambda: oracle.matmul(a1, b1, want, n, k, m, bt, n * k, k * m, n * m,
+                                            threads=True), mt)
+        if not np.array_equal(dc.cpu().numpy(), want):
+            raise SystemExit(f"bench: GPU {case.name} differs from the oracle")
+        rows = n if bt > 1 else 64          # batch 0 of 32, or 64 rows of 4096
+        part = np.empty(rows * m, np.int16)
+        dt_1 = timed(lambda: oracle.matmul(a1, b1, part, rows, k, m), 1)
+        if not np.array_equal(part, want[: rows * m]):
+            raise SystemExit(f"bench: {case.name} one-thread slice differs")
+        res[case.name] = dict(gops=2.0 * rows * k * m / dt_1 / 1e9, seconds=dt_1,
+                              sample=f"{'batch 0 of 32' if bt > 1 else '64 of 4096 rows'}, one thread",
+                              gops_mt=2.0 * case.macs / dt_mt / 1e9, seconds_mt=dt_mt,
+                              threads_mt=mt, sample_mt="the whole product, checked bit for bit")
+    for case in wl.CONV_CASES:
+        if case.name not in extras:
+            continue
+        dx, dw_, db_, dy, x, w, b = extras[case.name].pop("_dev")
         o = case.out_hw
-        want = np.empty(case.out_ch * o * o, np.int16)
-        t0 = time.perf_counter()
-        oracle.conv(np.ascontiguousarray(x[0]).reshape(-1), w.reshape(-1), b, want, 1, case.in_ch,
-                    case.hw, case.hw, case.out_ch, o, o, case.k, case.k, case.stride, case.stride,
-                    case.dil, case.dil, case.pad, case.pad, 1, 0)
-        dt = time.perf_counter() - t0
-        if not np.array_equal(dy[: want.size].cpu().numpy(), want):
-            raise SystemExit(f"bench: GPU {name} image 0 differs from the oracle")
-        res[name] = dict(gops=2.0 * case.macs / case.batch / dt / 1e9, seconds=dt,
-                         sample="image 0 of 32")
-        oracle.set_threads(mt)
-        t0 = time.perf_counter()
-        oracle.conv(np.ascontiguousarray(x[0]).reshape(-1), w.reshape(-1), b, want, 1, case.in_ch,
-                    case.hw, case.hw, case.out_ch, o, o, case.k, case.k, case.stride, case.stride,
-                    case.dil, case.dil, case.pad, case.pad, 1, 0, threads=True)
-        dt = time.perf_counter() - t0
-        oracle.set_threads(1)
-        res[name].update(gops_mt=2.0 * case.macs / case.batch / dt / 1e9, seconds_mt=dt, threads_mt=mt)
+        args = (case.in_ch, case.hw, case.hw, case.out_ch, o, o, case.k, case.k, case.stride,
+                case.stride, case.dil, case.dil, case.pad, case.pad, 1, 0)
+        x1, w1 = np.ascontiguousarray(x).reshape(-1), w.reshape(-1)
+        want = np.empty(case.batch * case.out_ch * o * o, np.int16)
+        dt_mt = timed(lambda: oracle.conv(x1, w1, b, want, case.batch, *args, threads=True), mt)
+        if not np.array_equal(dy.cpu().numpy(), want):
+            raise SystemExit(f"bench: GPU {case.name} differs from the oracle")
+        part = np.empty(case.out_ch * o * o, np.int16)
+        dt_1 = timed(lambda: oracle.conv(x1, w1, b, part, 1, *args), 1)
+        if not np.array_equal(part, want[: part.size]):
+            raise SystemExit(f"bench: {case.name} one-thread slice differs")
+        res[case.name] = dict(gops=2.0 * case.macs / case.batch / dt_1 / 1e9, seconds=dt_1,
+                              sample="image 0 of 32, one thread",
+                              gops_mt=2.0 * case.macs / dt_mt / 1e9, seconds_mt=dt_mt,
+                              threads_mt=mt, sample_mt="all 32 images, checked bit for bit")
     for name, e in list(extras.items()):
-        if not name.startswith(("maxpool", "avgpool", "lppool", "globalavgpool")):
+        if "_on_conv" not in name:
             continue
         x, y, a = e.pop("_dev")
         xh = x.cpu().numpy()
         want = np.empty(y.numel(), np.int16)
-        t0 = time.perf_counter()
-        oracle.pool(xh, want, a["batch"], a["channels"], a["in_h"], a["in_w"], a["out_h"],
-                    a["out_w"], a["pool_h"], a["pool_w"], a["stride_h"], a["stride_w"],
-                    a["pad_top"], a["pad_left"], a["dil_h"], a["dil_w"], a["pool_type"],
-                    a["lp_order"], a["count_include_pad"])
-        dt = time.perf_counter() - t0
+        pargs = tuple(a.values())
+        dt_1 = timed(lambda: oracle.pool(xh, want, *pargs), 1)
         if not np.array_equal(y.cpu().numpy(), want):
             raise SystemExit(f"bench: GPU {name} differs from the oracle")
-        res[name] = dict(gbs=(xh.size + want.size) * 2 / dt / 1e9, seconds=dt, sample="full tensor")
-        oracle.set_threads(mt)
-        t0 = time.perf_counter()
-        oracle.pool(xh, want, a["batch"], a["channels"], a["in_h"], a["in_w"], a["out_h"],
-                    a["out_w"], a["pool_h"], a["pool_w"], a["stride_h"], a["stride_w"],
-                    a["pad_top"], a["pad_left"], a["dil_h"], a["dil_w"], a["pool_type"],
-                    a["lp_order"], a["count_include_pad"], threads=True)
-        dt = time.perf_counter() - t0
-        oracle.set_threads(1)
-        res[name].update(gbs_mt=(xh.size + want.size) * 2 / dt / 1e9, seconds_mt=dt, threads_mt=mt)
+        dt_mt = timed(lambda: oracle.pool(xh, want, *pargs, threads=True), mt)
+        res[name] = dict(gbs=(xh.size + want.size) * 2 / dt_1 / 1e9, seconds=dt_1,
+                         sample="full tensor, one thread",
+                         gbs_mt=(xh.size + want.size) * 2 / dt_mt / 1e9, seconds_mt=dt_mt,
+                         threads_mt=mt)
     return res
+
+
+# ------------------------------------------------------ per-case harness --
+def bench_cases(dump_dir: str | None):
+    """The reference's per-kernel case list (perf_config.json.example plus the published
+    report's rows) through cm_bench, the C counterpart of bench_src/bench_*.c: one JSON
+    line per case with the reference's fields, the published KV260 figures beside it."""
+    import subprocess
+    from cormorant_amd import build as hipbuild
+    from cormorant_amd.bench_src import perf_cases as pc
+    if not os.path.exists(hipbuild.BENCH_BIN):
+        raise SystemExit(f"bench: {hipbuild.BENCH_BIN} is missing (run the build)")
+    lines = "\n".join(pc.case_line(c) for c in pc.CASES) + "\n"
+    env = dict(os.environ)
+    if dump_dir:
+        env["CM_BENCH_DUMP"] = dump_dir
+    r = subprocess.run([hipbuild.BENCH_BIN, "-"], input=lines, capture_output=True, text=True,
+                       timeout=600, env=env)
+    if r.returncode != 0:
+        raise SystemExit(f"bench: cm_bench failed ({r.returncode}): {r.stderr[-2000:]}")
+    rows = [json.loads(l) for l in r.stdout.splitlines() if l.startswith("{")]
+    for case, row in zip(pc.CASES, rows):
+        kv = case[5]
+        if kv is not None:
+            metric = "gbs" if case[0] in ("vectorop", "pool") else "gops"
+            row["kv260"] = {"lat_ms": kv[0], metric: kv[1]}
+            row["speedup_vs_kv260"] = round(kv[0] / row["lat_ms"], 1)
+    return rows
 
 
 def load_traffic(kernel: str):
@@ -468,8 +480,10 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--quick", action="store_true", help="headline workload only, no CPU baseline")
-    ap.add_argument("--workloads", default="vecop,gemm,conv,pool,graphs",
-                    help="comma list of vecop (always run: the headline), gemm, conv, pool, graphs")
+    ap.add_argument("--workloads", default="vecop,gemm,conv,pool,graphs,cases",
+                    help="comma list of vecop (always run: the headline), gemm, conv, pool "
+                         "(conv and pool: the conv + pool block), graphs, cases (the "
+                         "reference's per-kernel case list through cm_bench)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     args = ap.parse_args()
     work = set(args.workloads.split(","))
@@ -532,12 +546,16 @@ def main() -> int:
     if "gemm" in work:
         log("GEMM configurations")
         extras.update(bench_gemm(max(5, args.steps // 2), 2))
-    if "conv" in work:
-        log("convolution configurations")
-        extras.update(bench_conv(max(5, args.steps // 2), 2))
-    if "pool" in work:
-        log("pool configurations")
-        extras.update(bench_pool(max(args.steps, POOL_ROTATE), 2))
+    if "conv" in work or "pool" in work:
+        log("conv + pool block: conv A, conv B, four pools on each output")
+        extras.update(bench_block(max(5, args.steps // 2), 2))
+    cases = []
+    dump_dir = None
+    if "cases" in work:
+        import tempfile
+        log("reference per-case list through cm_bench")
+        dump_dir = None if args.no_cpu else tempfile.mkdtemp(prefix="cm_bench_")
+        cases = bench_cases(dump_dir)
     if "graphs" in work:
         log("scheduler graphs: MLP b64, MobileNetV2-like b16")
         graphs = bench_graphs(max(5, args.steps // 2), 2, check=not args.no_cpu)
@@ -551,6 +569,22 @@ def main() -> int:
                    seconds=round(v["seconds"], 3),
                    value_mt=round(v["gbs_mt"], 3), cores_mt=v["threads_mt"],
                    seconds_mt=round(v["seconds_mt"], 3))
+    if cases and dump_dir:
+        from cormorant_amd.bench_src import perf_cases as pc
+        from oracle import bench_cases as bc
+        oracle_threads = host_threads()
+        import oracle
+        oracle.set_threads(oracle_threads)
+        for case, row in zip(pc.CASES, cases):
+            n_bad = bc.check_dump(case, dump_dir, seed=row["seed"])
+            if n_bad:
+                raise SystemExit(f"bench: cm_bench case {case[1]} differs from the oracle "
+                                 f"in {n_bad} elements")
+            row["checked_vs_oracle"] = True
+        import shutil
+        shutil.rmtree(dump_dir, ignore_errors=True)
+    if cases:
+        results["perf_cases"] = cases
     for name, e in extras.items():
         e.pop("_dev", None)
         if name in cpu_res:

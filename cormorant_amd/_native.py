@@ -20,6 +20,7 @@ EXPORTS = (
     "cm_buf_sync_from_device", "cm_run_op", "cm_run_matmul", "cm_run_matmul_at", "cm_run_conv",
     "cm_run_pool", "cm_set_stream", "cm_get_stream", "cm_sync", "cm_last_error", "cm_version",
     "cm_selftest_div", "cm_selftest_finalize", "cm_matmul_ex", "cm_conv_ex",
+    "cm_matmul_workspace_size", "cm_conv_workspace_size", "cm_set_workspace",
 )
 
 CM_OK = 0
@@ -99,8 +100,13 @@ _SIGS = {
     "cm_selftest_div": (_i, [_u32, _u32, ctypes.POINTER(ctypes.c_uint64),
                                 ctypes.POINTER(ctypes.c_uint64), _vp]),
     "cm_selftest_finalize": (_i, [_u32, _u32, _u32, _u32, ctypes.POINTER(ctypes.c_uint64), _vp]),
-    "cm_matmul_ex": (_i, [_vp, _vp, _vp] + [_u32] * 7 + [ctypes.POINTER(CmEpilogue), _vp]),
-    "cm_conv_ex": (_i, [_vp, _vp, _vp, _vp] + [_u32] * 17 + [ctypes.POINTER(CmEpilogue), _vp]),
+    "cm_matmul_ex": (_i, [_vp, _vp, _vp] + [_u32] * 7 +
+                     [ctypes.POINTER(CmEpilogue), _vp, ctypes.c_size_t, _vp]),
+    "cm_conv_ex": (_i, [_vp, _vp, _vp, _vp] + [_u32] * 17 +
+                   [ctypes.POINTER(CmEpilogue), _vp, ctypes.c_size_t, _vp]),
+    "cm_matmul_workspace_size": (ctypes.c_size_t, [_u32] * 7),
+    "cm_conv_workspace_size": (ctypes.c_size_t, [_u32] * 17),
+    "cm_set_workspace": (_i, [_vp, ctypes.c_size_t]),
 }
 
 _lib = None

@@ -1,11 +1,13 @@
-"""Build libcormorant_amd.so (gfx950) in-tree with hipcc.
+"""Build libcormorant_amd.so (gfx950) in-tree with hipcc, and the cm_bench tool.
 
 Usage: python -m cormorant_amd.build [--jobs N]
 
 Every .hip file under csrc/ is compiled for gfx950 only and linked into one
 shared library next to this file.  FP contraction is off (the pool
 finalisers round exactly as written) and packed-FP32 instruction selection is
-disabled.
+disabled.  bench_src/cm_bench.c (the per-case benchmark, a C program against
+include/cormorant_amd.h) is compiled with the host C compiler and linked
+against that library.
 """
 from __future__ import annotations
 
@@ -70,11 +72,30 @@ def build(jobs: int | None = None) -> str:
     return LIB
 
 
+BENCH_SRC = os.path.join(HERE, "bench_src", "cm_bench.c")
+BENCH_BIN = os.path.join(HERE, "bench_src", "cm_bench")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
+
+
+def build_bench() -> str:
+    """Compile bench_src/cm_bench with gcc against the in-tree library."""
+    cmd = [os.environ.get("CC", "gcc"), "-O2", "-std=c11", "-Wall", "-Wextra",
+           "-D__HIP_PLATFORM_AMD__", "-I", os.path.join(ROCM, "include"),
+           "-I", os.path.join(HERE, "..", "include"), BENCH_SRC,
+           "-L", HERE, "-lcormorant_amd", "-L", os.path.join(ROCM, "lib"), "-lamdhip64",
+           "-Wl,-rpath,$ORIGIN/..", f"-Wl,-rpath,{os.path.join(ROCM, 'lib')}", "-o", BENCH_BIN]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"cm_bench build failed:\n{r.stdout}\n{r.stderr}")
+    return BENCH_BIN
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     args = ap.parse_args()
     print(build(args.jobs))
+    print(build_bench())
 
 
 if __name__ == "__main__":

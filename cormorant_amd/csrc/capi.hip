@@ -11,6 +11,8 @@ namespace {
 
 thread_local char g_err[512] = "";
 hipStream_t g_stream = nullptr;
+void* g_ws = nullptr;      // default split-K workspace (cm_set_workspace), caller-owned
+size_t g_ws_bytes = 0;
 int g_sync_check = -1;   // CM_SYNC_CHECK=1: wait after every launch (fault localisation)
 
 hipStream_t pick(hipStream_t s) { return s ? s : g_stream; }
@@ -94,21 +96,42 @@ int cm_vectorop(const int16_t* a, const int16_t* b, int16_t* c, uint32_t size, u
     return cm_vectorop_launch(a, b, c, size, op, outer, a_inc, b_inc, pick(stream));
 }
 
+int cm_set_workspace(void* workspace, size_t bytes) {
+    g_ws = bytes ? workspace : nullptr;
+    g_ws_bytes = workspace ? bytes : 0u;
+    return CM_OK;
+}
+
 int cm_matmul_ex(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
                  uint32_t m, uint32_t batch, uint32_t a_stride, uint32_t b_stride,
-                 uint32_t c_stride, const cm_epilogue_t* epi, hipStream_t stream) {
+                 uint32_t c_stride, const cm_epilogue_t* epi, void* workspace,
+                 size_t workspace_bytes, hipStream_t stream) {
     if (batch == 0 || n == 0 || m == 0) return CM_OK;
     if (!c || (k > 0 && (!a || !b))) return cm_set_error(CM_ERR_INVALID, "matmul: null pointer");
     const int rc = check_epilogue(epi, true, "matmul");
     if (rc) return rc;
-    return cm_matmul_launch(a, b, c, n, k, m, batch, a_stride, b_stride, c_stride, epi,
-                            pick(stream));
+    const LaunchCtx lc{pick(stream), workspace_bytes ? workspace : nullptr,
+                       workspace ? workspace_bytes : 0u, nullptr};
+    return cm_matmul_launch(a, b, c, n, k, m, batch, a_stride, b_stride, c_stride, epi, lc);
 }
 
 int cm_matmul(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
               uint32_t m, uint32_t batch, uint32_t a_stride, uint32_t b_stride,
               uint32_t c_stride, hipStream_t stream) {
-    return cm_matmul_ex(a, b, c, n, k, m, batch, a_stride, b_stride, c_stride, nullptr, stream);
+    return cm_matmul_ex(a, b, c, n, k, m, batch, a_stride, b_stride, c_stride, nullptr, g_ws,
+                        g_ws_bytes, stream);
+}
+
+size_t cm_matmul_workspace_size(uint32_t n, uint32_t k, uint32_t m, uint32_t batch,
+                                uint32_t a_stride, uint32_t b_stride, uint32_t c_stride) {
+    if (batch == 0 || n == 0 || m == 0) return 0;
+    size_t need = 0;
+    static int16_t probe[8] __attribute__((aligned(16)));   // never dereferenced in a dry run
+    const LaunchCtx lc{nullptr, nullptr, 0u, &need};
+    if (cm_matmul_launch(probe, probe, probe, n, k, m, batch, a_stride, b_stride, c_stride,
+                         nullptr, lc) != CM_OK)
+        return 0;
+    return need;
 }
 
 int cm_matmul_at(const int16_t* a, uint32_t a_off, const int16_t* b, uint32_t b_off,
@@ -125,7 +148,8 @@ int cm_conv_ex(const int16_t* x, const int16_t* weight, const int16_t* bias, int
                uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
                uint32_t stride_w, uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
                uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise,
-               const cm_epilogue_t* epi, hipStream_t stream) {
+               const cm_epilogue_t* epi, void* workspace, size_t workspace_bytes,
+               hipStream_t stream) {
     if ((uint64_t)batch * out_ch * out_h * out_w == 0) return CM_OK;
     if (!x || !weight || !y) return cm_set_error(CM_ERR_INVALID, "conv: null x, weight or y");
     if (has_bias && !bias) return cm_set_error(CM_ERR_INVALID, "conv: has_bias with null bias");
@@ -133,9 +157,11 @@ int cm_conv_ex(const int16_t* x, const int16_t* weight, const int16_t* bias, int
         return cm_set_error(CM_ERR_INVALID, "conv: depthwise needs out_ch (%u) <= in_ch (%u)", out_ch, in_ch);
     const int rc = check_epilogue(epi, false, "conv");
     if (rc) return rc;
+    const LaunchCtx lc{pick(stream), workspace_bytes ? workspace : nullptr,
+                       workspace ? workspace_bytes : 0u, nullptr};
     return cm_conv_launch(x, weight, bias, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh,
                           kw, stride_h, stride_w, dilation_h, dilation_w, pad_top, pad_left,
-                          has_bias, is_depthwise, epi, pick(stream));
+                          has_bias, is_depthwise, epi, lc);
 }
 
 int cm_conv(const int16_t* x, const int16_t* weight, const int16_t* bias, int16_t* y,
@@ -145,7 +171,23 @@ int cm_conv(const int16_t* x, const int16_t* weight, const int16_t* bias, int16_
             uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise, hipStream_t stream) {
     return cm_conv_ex(x, weight, bias, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw,
                       stride_h, stride_w, dilation_h, dilation_w, pad_top, pad_left, has_bias,
-                      is_depthwise, nullptr, stream);
+                      is_depthwise, nullptr, g_ws, g_ws_bytes, stream);
+}
+
+size_t cm_conv_workspace_size(uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                              uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh,
+                              uint32_t kw, uint32_t stride_h, uint32_t stride_w,
+                              uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
+                              uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise) {
+    if ((uint64_t)batch * out_ch * out_h * out_w == 0) return 0;
+    size_t need = 0;
+    static int16_t probe[8] __attribute__((aligned(16)));   // never dereferenced in a dry run
+    const LaunchCtx lc{nullptr, nullptr, 0u, &need};
+    if (cm_conv_launch(probe, probe, has_bias ? probe : nullptr, probe, batch, in_ch, in_h, in_w,
+                       out_ch, out_h, out_w, kh, kw, stride_h, stride_w, dilation_h, dilation_w,
+                       pad_top, pad_left, has_bias, is_depthwise, nullptr, lc) != CM_OK)
+        return 0;
+    return need;
 }
 
 int cm_pool(const int16_t* x, int16_t* y, uint32_t batch, uint32_t channels, uint32_t in_h,

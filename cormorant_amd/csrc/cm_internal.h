@@ -19,6 +19,18 @@ enum {
 
 int cm_set_error(int code, const char* fmt, ...);
 
+// Where a MatMul / Conv launch runs and what scratch memory it may use.
+//   ws / ws_bytes: the caller's workspace for split-K partial sums (null / 0 =
+//     none: the call runs unsplit).  The library never allocates one.
+//   need: dry run -- nothing is launched; *need is raised to the workspace
+//     bytes the call would use with an unlimited workspace.
+struct LaunchCtx {
+    hipStream_t s;
+    void* ws;
+    size_t ws_bytes;
+    size_t* need;
+};
+
 // Epilogue of a MatMul / Conv launch, flattened for kernel arguments:
 // add_mode / act as in cm_epilogue_t (0 = none).
 struct EpiArgs {
@@ -83,17 +95,17 @@ int cm_finalize_sweep_launch(uint32_t mode, uint32_t lo, uint32_t count, uint32_
                              unsigned long long* checksum, hipStream_t s);
 int cm_matmul_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
                      uint32_t m, uint32_t batch, uint32_t a_bs, uint32_t b_bs, uint32_t c_bs,
-                     const cm_epilogue_t* epi, hipStream_t s);
+                     const cm_epilogue_t* epi, const LaunchCtx& lc);
 // 3x3 convolution through an LDS-staged input patch (conv_patch.hip); returns
 // 1, launching nothing, for shapes it does not take.
 int cm_conv_patch_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
                          uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
                          uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
                          uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
-                         uint32_t pad_left, const cm_epilogue_t* epi, hipStream_t s);
+                         uint32_t pad_left, const cm_epilogue_t* epi, const LaunchCtx& lc);
 int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
                    uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
                    uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
                    uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
                    uint32_t pad_left, uint32_t has_bias, uint32_t is_dw, const cm_epilogue_t* epi,
-                   hipStream_t s);
+                   const LaunchCtx& lc);

@@ -17,10 +17,10 @@ int cm_conv_gemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias,
                         uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
                         uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
                         uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
-                        uint32_t pad_left, const cm_epilogue_t* epi, hipStream_t s);
+                        uint32_t pad_left, const cm_epilogue_t* epi, const LaunchCtx& lc);
 int cm_conv_pointwise_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
                              uint32_t batch, uint32_t in_ch, uint32_t out_ch, uint32_t hw,
-                             const cm_epilogue_t* epi, hipStream_t s);
+                             const cm_epilogue_t* epi, const LaunchCtx& lc);
 
 namespace {
 
@@ -263,12 +263,13 @@ int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int1
                    uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
                    uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
                    uint32_t pad_left, uint32_t has_bias, uint32_t is_dw, const cm_epilogue_t* epi,
-                   hipStream_t s) {
+                   const LaunchCtx& lc) {
+    const hipStream_t s = lc.s;
     const int16_t* b = has_bias ? bias : nullptr;
     const EpiArgs ea = cm_epi_args(epi);
     if (is_dw) {
         const uint64_t total = (uint64_t)batch * out_ch * out_h * out_w;
-        if (total == 0) return CM_OK;
+        if (total == 0 || lc.need) return CM_OK;
         DwGeom g{in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, sh, sw, dh, dw, pad_top, pad_left};
         const dim3 grid((uint32_t)cm_grid_blocks(total, kThreads));
         if (b) hipLaunchKernelGGL(conv_depthwise<true>, grid, dim3(kThreads), 0, s, x, w, b, y, g, total, ea);
@@ -279,7 +280,7 @@ int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int1
     const uint64_t x_bytes = 2ull * in_ch * in_h * in_w * batch;
     const uint64_t npix = (uint64_t)batch * out_h * out_w;
     if (const uint32_t mt = direct_channels(K, out_ch, kh * kw, npix, x_bytes)) {
-        if (npix == 0 || out_ch == 0) return CM_OK;
+        if (npix == 0 || out_ch == 0 || lc.need) return CM_OK;
         if (npix > 0x7FFFFFFFull) return cm_set_error(CM_ERR_RANGE, "conv: shape exceeds 32-bit indexing");
         DirArgs g{};
         g.x = x; g.w = w; g.bias = b; g.y = y;
@@ -305,7 +306,7 @@ int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int1
     }
     {
         const int rc = cm_conv_patch_launch(x, w, b, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w,
-                                            kh, kw, sh, sw, dh, dw, pad_top, pad_left, epi, s);
+                                            kh, kw, sh, sw, dh, dw, pad_top, pad_left, epi, lc);
         if (rc != 1) return rc;
     }
     // 1x1 / stride 1 / no padding as one GEMM per image, when an image's
@@ -315,7 +316,7 @@ int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int1
     const uint64_t tiles = (hw + 127) / 128;
     if (kh == 1 && kw == 1 && sh == 1 && sw == 1 && pad_top == 0 && pad_left == 0 &&
         out_h == in_h && out_w == in_w && hw <= 0x7FFFFFFFull && (tiles * 128 - hw) * 5 <= tiles * 128)
-        return cm_conv_pointwise_launch(x, w, b, y, batch, in_ch, out_ch, (uint32_t)hw, epi, s);
+        return cm_conv_pointwise_launch(x, w, b, y, batch, in_ch, out_ch, (uint32_t)hw, epi, lc);
     return cm_conv_gemm_launch(x, w, b, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw,
-                               sh, sw, dh, dw, pad_top, pad_left, epi, s);
+                               sh, sw, dh, dw, pad_top, pad_left, epi, lc);
 }

@@ -388,7 +388,8 @@ int cm_conv_patch_launch(const int16_t* x, const int16_t* w, const int16_t* bias
                          uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
                          uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
                          uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
-                         uint32_t pad_left, const cm_epilogue_t* epi, hipStream_t s) {
+                         uint32_t pad_left, const cm_epilogue_t* epi, const LaunchCtx& lc) {
+    const hipStream_t s = lc.s;
     const EpiArgs ea = cm_epi_args(epi);
     if (kh != 3 || kw != 3 || dh != 1 || dw != 1 || sh != sw || (sh != 1 && sh != 2)) return 1;
     if (in_ch == 0 || in_ch > 64 || out_ch == 0 || out_ch > 64 || (in_ch * 9) % 8 != 0) return 1;
@@ -417,6 +418,7 @@ int cm_conv_patch_launch(const int16_t* x, const int16_t* w, const int16_t* bias
     const uint32_t tile_bytes = mt * kTilePitch * 4;
     if (lds < tile_bytes) lds = tile_bytes;
     if (lds > 160u * 1024u - 2048u) return 1;
+    if (lc.need) return CM_OK;   // dry run: this path uses no workspace
     g.tiles_w = tiles_w; g.tiles_h = tiles_h;
     g.div_tw = make_fastdiv(tiles_w);
     g.div_th = make_fastdiv(tiles_h);

@@ -27,11 +27,7 @@
 // banks).  The next tile's loads are issued before the MFMA phase; loads are
 // unconditional (out-of-range elements are zeroed by the buffer range check
 // or by a select), so all of a tile's loads are in flight at once.
-#include <map>
-#include <mutex>
 #include <type_traits>
-#include <utility>
-#include <vector>
 
 #include "cm_internal.h"
 #include "q88.h"
@@ -705,7 +701,9 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     const uint32_t kbase = s0 * BK;
     load_tile(at[0], bt[0], kbase);
     load_tile(at[1], bt[1], kbase + BK);
-    stage_tile(at[0], bt[0], s.st[0], true);
+    // with K = 0 there is no step: the staged (all-zero) tile must not count,
+    // its limb sums are not those of zeros (low limbs are offset by -128)
+    stage_tile(at[0], bt[0], s.st[0], nk > 0);
     __syncthreads();
     // Steps go in pairs (it, it + 1).  Step it computes on planes 0 while the
     // loads of step it+2 fly into register set 0 (free: its tile was staged one
@@ -867,7 +865,7 @@ struct ReduceArgs {
 template <uint32_t SPLITS>
 __global__ __launch_bounds__(kReduceThreads) void split_reduce(ReduceArgs a) {
     const uint32_t nq = a.ws_ld / 4u;
-    const uint32_t total = a.rows * nq;     // < 2^24: the workspace holds at most 64 MiB
+    const uint32_t total = a.rows * nq;     // < 2^20: splits need fewer than 160 output tiles
     const uint64_t zs = (uint64_t)a.rows * a.ws_ld;
     const int32_t lo = q88::act_lo(a.epi.act), hi = q88::act_hi(a.epi.act);
     for (uint32_t idx = blockIdx.x * kReduceThreads + threadIdx.x; idx < total;
@@ -913,42 +911,6 @@ int launch_reduce(uint32_t splits, dim3 grid, hipStream_t s, const ReduceArgs& r
     }
 }
 
-// Per-(device, stream) split-K workspace.  It only grows, and a replaced
-// buffer is kept until the process ends, since a captured HIP graph may still
-// hold its address; calls on one stream are ordered, so they share it safely.
-// Inside a stream capture nothing is allocated: the call then runs unsplit.
-struct SplitWorkspace {
-    uint32_t* ptr = nullptr;
-    size_t bytes = 0;
-};
-std::mutex g_ws_mutex;
-std::map<std::pair<int, hipStream_t>, SplitWorkspace> g_ws;
-std::vector<uint32_t*> g_ws_retired;
-constexpr size_t kWsMin = 8u << 20, kWsMax = 64u << 20;
-
-uint32_t* split_workspace(hipStream_t s, size_t bytes) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return nullptr;
-    std::lock_guard<std::mutex> lock(g_ws_mutex);
-    SplitWorkspace& w = g_ws[{dev, s}];
-    if (w.bytes >= bytes) return w.ptr;
-    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) {
-        (void)hipGetLastError();
-        return nullptr;
-    }
-    const size_t nb = bytes > kWsMin ? bytes : kWsMin;
-    uint32_t* p = nullptr;
-    if (hipMalloc((void**)&p, nb) != hipSuccess) {
-        (void)hipGetLastError();
-        return nullptr;
-    }
-    if (w.ptr) g_ws_retired.push_back(w.ptr);
-    w.ptr = p;
-    w.bytes = nb;
-    return p;
-}
-
 // Number of k splits for a launch of `tiles` blocks over nk_all k steps: enough
 // blocks for every CU when the tile grid alone leaves most of the chip idle,
 // at least two k steps per split (one when there are fewer than 64 tiles: a
@@ -969,33 +931,45 @@ uint32_t choose_splits(uint32_t tiles, uint32_t nk_all) {
 inline bool aligned(const void* p, uintptr_t n) { return ((uintptr_t)p & (n - 1)) == 0; }
 
 template <int MODE>
-int launch_gemm(GemmArgs& g0, uint32_t zdim, hipStream_t s, const char* name) {
+int launch_gemm(GemmArgs& g0, uint32_t zdim, const LaunchCtx& lc, const char* name) {
     GemmArgs g = g0;
+    const hipStream_t s = lc.s;
     dim3 grid((g.cols + BN - 1) / BN, (g.rows + BM - 1) / BM, zdim);
     if (grid.y > 65535u || grid.z > 65535u || grid.x > 0x7FFFFFFFu)
         return cm_set_error(CM_ERR_RANGE, "%s: grid too large", name);
     const bool fold = g.k > (uint32_t)(kFoldIters * BK);
-    // split-K when the output tiles cannot fill the chip (single launch, no fold)
+    // split-K when the output tiles cannot fill the chip (single launch, no
+    // fold), through the caller's workspace: the preferred split if it fits,
+    // else as many splits as fit (at least two), else none
     uint32_t splits = 1;
     if (zdim == 1 && !fold) {
         const uint32_t nk_all = (g.k + BK - 1) / BK;
         splits = choose_splits(grid.x * grid.y, nk_all);
-        if (splits > 1) {
-            const uint32_t sps = (nk_all + splits - 1) / splits;
-            splits = (nk_all + sps - 1) / sps;
-            const uint32_t ws_ld = (g.cols + 7u) & ~7u;
-            const size_t bytes = (size_t)splits * g.rows * ws_ld * 4u;
-            uint32_t* ws = bytes <= kWsMax ? split_workspace(s, bytes) : nullptr;
-            if (ws) {
-                g.split_steps = sps;
-                g.ws_ld = ws_ld;
-                g.ws = ws;
-                g.a_bs = g.b_bs = g.c_bs = 0;
-                grid.z = splits;
-            } else {
-                splits = 1;
-            }
+        const uint32_t ws_ld = (g.cols + 7u) & ~7u;
+        const size_t per_split = (size_t)g.rows * ws_ld * 4u;
+        auto even = [nk_all](uint32_t sp) {   // equal step counts: no empty split
+            const uint32_t sps = (nk_all + sp - 1) / sp;
+            return (nk_all + sps - 1) / sps;
+        };
+        if (splits > 1) splits = even(splits);
+        if (lc.need) {
+            const size_t want = splits > 1 ? (size_t)splits * per_split : 0u;
+            if (want > *lc.need) *lc.need = want;
+            return CM_OK;
         }
+        if (splits > 1) {
+            const size_t fit = lc.ws ? lc.ws_bytes / per_split : 0u;
+            if (fit < splits) splits = fit >= 2 ? even((uint32_t)fit) : 1u;
+        }
+        if (splits > 1) {
+            g.split_steps = (nk_all + splits - 1) / splits;
+            g.ws_ld = ws_ld;
+            g.ws = static_cast<uint32_t*>(lc.ws);
+            g.a_bs = g.b_bs = g.c_bs = 0;
+            grid.z = splits;
+        }
+    } else if (lc.need) {
+        return CM_OK;
     }
     const bool bias = g.bias != nullptr && splits == 1;
     // widest output / Add access that keeps alignment and stays in one image row run
@@ -1054,7 +1028,7 @@ int launch_gemm(GemmArgs& g0, uint32_t zdim, hipStream_t s, const char* name) {
 
 int cm_matmul_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
                      uint32_t m, uint32_t batch, uint32_t a_bs, uint32_t b_bs, uint32_t c_bs,
-                     const cm_epilogue_t* epi, hipStream_t s) {
+                     const cm_epilogue_t* epi, const LaunchCtx& lc) {
     if (batch == 0 || n == 0 || m == 0) return CM_OK;
     GemmArgs g{};
     g.a = a; g.b = b; g.c = c; g.bias = nullptr;
@@ -1072,15 +1046,20 @@ int cm_matmul_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n,
         g.b_vec = aligned(g.b, 8) && m % 4 == 0;
         batch = 1;
     }
+    // Batches whose outputs overlap (0 < c_stride < n*m) run one launch each, in
+    // batch order: the reference's sequential batch loop (MatmulKernel.cpp:108-111)
+    // leaves each shared element with the last batch's value.
+    const bool overlap = c_bs != 0 && (uint64_t)c_bs < (uint64_t)n * m;
+    const uint32_t zmax = overlap ? 1u : 65535u;   // grid.z holds at most 65535 batches
     uint32_t done = 0;
-    while (done < batch) {   // grid.z is limited to 65535 batches per launch
-        const uint32_t z = (batch - done) > 65535u ? 65535u : (batch - done);
+    while (done < batch) {
+        const uint32_t z = (batch - done) > zmax ? zmax : (batch - done);
         GemmArgs gz = g;
         gz.a = g.a + (uint64_t)done * a_bs;
         gz.b = g.b + (uint64_t)done * b_bs;
         gz.c = g.c + (uint64_t)done * c_bs;
         if (g.epi.add_mode == 1u) gz.epi.add = g.epi.add + (uint64_t)done * c_bs;
-        const int rc = launch_gemm<B_DENSE>(gz, z, s, "matmul");
+        const int rc = launch_gemm<B_DENSE>(gz, z, lc, "matmul");
         if (rc) return rc;
         done += z;
     }
@@ -1091,7 +1070,7 @@ int cm_conv_gemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias,
                         uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
                         uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
                         uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
-                        uint32_t pad_left, const cm_epilogue_t* epi, hipStream_t s) {
+                        uint32_t pad_left, const cm_epilogue_t* epi, const LaunchCtx& lc) {
     const uint64_t P = (uint64_t)out_h * out_w;
     const uint64_t K = (uint64_t)in_ch * kh * kw;
     const uint64_t cols = P * batch;
@@ -1121,13 +1100,13 @@ int cm_conv_gemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias,
     const bool table = ((K + BK - 1) / BK + 2) * BK <= kTabMax && (uint64_t)kh * kw <= 31u &&
                        x_bytes < 0x80000000ull &&
                        ((uint64_t)(kh - 1) * dh * in_w + (uint64_t)(kw - 1) * dw) < (1ull << 29);
-    if (table) return launch_gemm<B_CONV_TAB>(g, 1, s, "conv_gemm");
-    return launch_gemm<B_CONV_INC>(g, 1, s, "conv_gemm");
+    if (table) return launch_gemm<B_CONV_TAB>(g, 1, lc, "conv_gemm");
+    return launch_gemm<B_CONV_INC>(g, 1, lc, "conv_gemm");
 }
 
 int cm_conv_pointwise_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
                              uint32_t batch, uint32_t in_ch, uint32_t out_ch, uint32_t hw,
-                             const cm_epilogue_t* epi, hipStream_t s) {
+                             const cm_epilogue_t* epi, const LaunchCtx& lc) {
     // 1x1, stride 1, no padding: y[n] = W[out_ch][in_ch] x X[n][in_ch][hw] (+ bias)
     if (batch == 0 || out_ch == 0 || hw == 0) return CM_OK;
     GemmArgs g{};
@@ -1145,7 +1124,7 @@ int cm_conv_pointwise_launch(const int16_t* x, const int16_t* w, const int16_t* 
         gz.b = x + (uint64_t)done * g.b_bs;
         gz.c = y + (uint64_t)done * g.c_bs;
         if (g.epi.add_mode == 1u) gz.epi.add = g.epi.add + (uint64_t)done * g.c_bs;
-        const int rc = launch_gemm<B_DENSE>(gz, z, s, "conv_pointwise");
+        const int rc = launch_gemm<B_DENSE>(gz, z, lc, "conv_pointwise");
         if (rc) return rc;
         done += z;
     }

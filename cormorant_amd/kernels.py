@@ -82,35 +82,65 @@ def _epilogue(add, column: bool, act: int, need: int):
     return e
 
 
+def _workspace(ws):
+    """(device address, bytes) of a split-K workspace tensor (any dtype), or (None, 0)."""
+    if ws is None:
+        return None, 0
+    if not ws.is_cuda or not ws.is_contiguous():
+        raise ValueError("workspace must be a contiguous device tensor")
+    return int(ws.data_ptr()), int(ws.numel() * ws.element_size())
+
+
+def matmul_workspace_size(n, k, m, batch=1, a_batch_stride=0, b_batch_stride=0,
+                          c_batch_stride=0) -> int:
+    """Bytes of split-K workspace MatmulKernel(..., workspace=) uses for this shape."""
+    return int(_native.load().cm_matmul_workspace_size(
+        *(_u32("matmul arg", v) for v in (n, k, m, batch, a_batch_stride, b_batch_stride,
+                                           c_batch_stride))))
+
+
+def conv_workspace_size(batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h=1,
+                        stride_w=1, dilation_h=1, dilation_w=1, pad_top=0, pad_left=0,
+                        has_bias=0, is_depthwise=0) -> int:
+    """Bytes of split-K workspace ConvKernel(..., workspace=) uses for this shape."""
+    args = [batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w,
+            dilation_h, dilation_w, pad_top, pad_left, int(bool(has_bias)), int(bool(is_depthwise))]
+    return int(_native.load().cm_conv_workspace_size(*(_u32("conv arg", v) for v in args)))
+
+
 def MatmulKernel(a, b, c, n, k, m, batch=1, a_batch_stride=0, b_batch_stride=0,
-                 c_batch_stride=0, stream=None, add=None, add_column=False, act=ACT_NONE) -> None:
+                 c_batch_stride=0, stream=None, add=None, add_column=False, act=ACT_NONE,
+                 workspace=None) -> None:
     """C_bi = sat16(wrap32(A_bi @ B_bi) >> 8), A_bi = a + bi*a_batch_stride, ...
 
     Optional fused epilogue: C = act(sat16(C + add)) with `add` laid out like C
-    (or, with add_column, one value per column j), act = ACT_RELU / ACT_RELU6."""
+    (or, with add_column, one value per column j), act = ACT_RELU / ACT_RELU6.
+    `workspace`: a device tensor for split-K partial sums (see
+    matmul_workspace_size); without one the call does not split."""
     n, k, m, batch = (_u32(x, v) for x, v in (("n", n), ("k", k), ("m", m), ("batch", batch)))
     a_bs, b_bs, c_bs = (_u32(x, v) for x, v in (("a_batch_stride", a_batch_stride),
                                                   ("b_batch_stride", b_batch_stride),
                                                   ("c_batch_stride", c_batch_stride)))
     if batch == 0 or n == 0 or m == 0:
         return
-    pa = _dev_ptr(a, (batch - 1) * a_bs + n * k, "a")
-    pb = _dev_ptr(b, (batch - 1) * b_bs + k * m, "b")
+    pa = _dev_ptr(a, (batch - 1) * a_bs + n * k, "a") if k else None
+    pb = _dev_ptr(b, (batch - 1) * b_bs + k * m, "b") if k else None
     pc = _dev_ptr(c, (batch - 1) * c_bs + n * m, "c")
     epi = _epilogue(add, add_column, act, m if add_column else (batch - 1) * c_bs + n * m)
-    if epi is None:
-        _native.call("cm_matmul", pa, pb, pc, n, k, m, batch, a_bs, b_bs, c_bs, _stream(stream))
-    else:
-        _native.call("cm_matmul_ex", pa, pb, pc, n, k, m, batch, a_bs, b_bs, c_bs,
-                     ctypes.byref(epi), _stream(stream))
+    ws, ws_bytes = _workspace(workspace)
+    _native.call("cm_matmul_ex", pa, pb, pc, n, k, m, batch, a_bs, b_bs, c_bs,
+                 ctypes.byref(epi) if epi is not None else None, ws, ws_bytes, _stream(stream))
 
 
 def ConvKernel(x, weight, bias, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw,
                stride_h=1, stride_w=1, dilation_h=1, dilation_w=1, pad_top=0, pad_left=0,
-               has_bias=0, is_depthwise=0, stream=None, add=None, act=ACT_NONE) -> None:
+               has_bias=0, is_depthwise=0, stream=None, add=None, act=ACT_NONE,
+               workspace=None) -> None:
     """ONNX Conv (group 1 or depthwise), NCHW, implicit bottom/right padding.
 
-    Optional fused epilogue: y = act(sat16(y + add)), add shaped like y."""
+    Optional fused epilogue: y = act(sat16(y + add)), add shaped like y.
+    `workspace`: a device tensor for split-K partial sums (see
+    conv_workspace_size); without one the call does not split."""
     args = [batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w,
             dilation_h, dilation_w, pad_top, pad_left, int(bool(has_bias)), int(bool(is_depthwise))]
     args = [_u32("conv arg", v) for v in args]
@@ -123,10 +153,9 @@ def ConvKernel(x, weight, bias, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_
     pbias = _dev_ptr(bias, out_ch, "bias") if has_bias else None
     py = _dev_ptr(y, batch * out_ch * out_h * out_w, "y")
     epi = _epilogue(add, False, act, batch * out_ch * out_h * out_w)
-    if epi is None:
-        _native.call("cm_conv", px, pw, pbias, py, *args, _stream(stream))
-    else:
-        _native.call("cm_conv_ex", px, pw, pbias, py, *args, ctypes.byref(epi), _stream(stream))
+    ws, ws_bytes = _workspace(workspace)
+    _native.call("cm_conv_ex", px, pw, pbias, py, *args,
+                 ctypes.byref(epi) if epi is not None else None, ws, ws_bytes, _stream(stream))
 
 
 def PoolingKernel(x, y, batch, channels, in_h, in_w, out_h, out_w, pool_h, pool_w,

@@ -5,8 +5,9 @@ inference-scheduler/src/codegen/_source.py:475-791) with calls into
 libcormorant_amd.so:
 
 * init: one ``cm_buf_alloc`` for the pool (weights + intermediates, 64-byte
-  aligned slots, intermediates with disjoint lifetimes sharing a slot), one
-  buffer per graph input and output, weights copied in once;
+  aligned slots, intermediates with disjoint lifetimes sharing a slot, then
+  the split-K workspace the MatMul / Conv calls share), one buffer per graph
+  input and output, weights copied in once;
 * run: graph inputs copied to the device, every kernel call enqueued in graph
   order on one in-order stream, graph outputs copied back (the only host
   synchronisation, as in the reference's sync_from_device).
@@ -34,6 +35,7 @@ from .plan import BufferPlan
 
 _FUNCS = {"op": "cm_vectorop", "matmul": "cm_matmul", "matmul_at": "cm_matmul",
           "conv": "cm_conv", "pool": "cm_pool"}
+_EX_FUNCS = {"matmul": "cm_matmul_ex", "matmul_at": "cm_matmul_ex", "conv": "cm_conv_ex"}
 
 
 class InferenceSession:
@@ -53,11 +55,22 @@ class InferenceSession:
         self.stream = int(stream)
         _native.call("cm_buf_pool_init")
         self._bufs: Dict[Tuple[str, str], object] = {}
+        self.workspace_bytes = 0
+        self._ws_ptr: Optional[int] = None
         try:
-            if self.plan.pool_elems:
-                pool = self._alloc(("pool", ""), self.plan.pool_elems)
-                self._host(pool, self.plan.pool_elems)[:] = self.plan.pool_image()
+            # split-K workspace: one region after the pool's tensors, as large as
+            # the largest need over the launch list (the calls run one after
+            # another on one stream, so they share it)
+            self.workspace_bytes = max((self._workspace_need(c) for c in self.launch_list),
+                                       default=0)
+            ws_off = -(-self.plan.pool_elems // 128) * 128   # 256-byte aligned
+            total = ws_off + self.workspace_bytes // 2 if self.workspace_bytes else self.plan.pool_elems
+            if total:
+                pool = self._alloc(("pool", ""), total)
+                self._host(pool, total)[:self.plan.pool_elems] = self.plan.pool_image()
                 _native.call("cm_buf_sync_to_device", pool)
+                if self.workspace_bytes:
+                    self._ws_ptr = int(pool.contents.dev) + 2 * ws_off
             for t in self.graph.input_tensors:
                 self._alloc(("input", t.onnx_name), self.plan.layouts[t.onnx_name].alloc)
             for t in self.graph.output_tensors:
@@ -102,7 +115,16 @@ class InferenceSession:
             ptrs.append(p)
         return ptrs
 
+    def _workspace_need(self, item) -> int:
+        call = item.call if isinstance(item, _fuse.FusedCall) else item
+        if call.kernel in ("matmul", "matmul_at"):
+            return int(self._lib.cm_matmul_workspace_size(*call.args))
+        if call.kernel == "conv":
+            return int(self._lib.cm_conv_workspace_size(*call.args))
+        return 0
+
     def _prepare(self, item):
+        ws = (self._ws_ptr, self.workspace_bytes) if self._ws_ptr else (None, 0)
         if isinstance(item, _fuse.FusedCall):
             call = item.call
             name = "cm_conv_ex" if call.kernel == "conv" else "cm_matmul_ex"
@@ -114,7 +136,11 @@ class InferenceSession:
             epi.act = item.act
             # the epilogue object rides along in the tuple so it outlives the pointer
             return getattr(self._lib, name), name, tuple(ptrs) + tuple(call.args) + (
-                ctypes.byref(epi),), epi
+                ctypes.byref(epi),) + ws, epi
+        if item.kernel in _EX_FUNCS:   # MatMul / Conv: the _ex form carries the workspace
+            name = _EX_FUNCS[item.kernel]
+            return (getattr(self._lib, name), name,
+                    tuple(self._pointers(item)) + tuple(item.args) + (None,) + ws, None)
         fn = getattr(self._lib, _FUNCS[item.kernel])
         return fn, _FUNCS[item.kernel], tuple(self._pointers(item)) + tuple(item.args), None
 

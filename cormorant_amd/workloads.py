@@ -140,14 +140,21 @@ class PoolCase:
         return conv_out(hw, self.k, self.stride, 1, self.pad)
 
 
-# Pools run on conv A's output [32, 128, 56, 56].  AvgPool takes pad 1 so that
-# count_include_pad matters; MaxPool and LpPool use no padding.
+# The pools run on each convolution's output: conv A's [32, 128, 56, 56] and
+# conv B's [32, 128, 28, 28].  AvgPool takes pad 1 so that count_include_pad
+# matters; MaxPool and LpPool use no padding.
 POOL_CASES = (
     PoolCase("maxpool_3x3_s2", 0, 3, 2, 0),
     PoolCase("avgpool_3x3_s2_p1_cip", 1, 3, 2, 1, cip=1),
     PoolCase("lppool_p2_2x2_s2", 2, 2, 2, 0, lp_order=2),
     PoolCase("globalavgpool", 1, 0, 1, 0),
 )
+
+
+def block_pools():
+    """(conv case, pool case) pairs of the conv + pool block: the four pools after each
+    convolution, named '<pool>_on_<conv>'."""
+    return [(cv, pc, f"{pc.name}_on_{cv.name[:6]}") for cv in CONV_CASES for pc in POOL_CASES]
 
 
 def pool_args(case: PoolCase, n: int, c: int, hw: int):

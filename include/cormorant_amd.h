@@ -19,15 +19,18 @@
  *     calling thread.  Where the reference has undefined behaviour (shapes
  *     beyond its compile-time kMax* limits) this library computes the exact
  *     result instead, or returns CM_ERR_RANGE if a size exceeds its indexing.
- *   - The caller owns every buffer it passes.  The one allocation the library
- *     makes itself is a split-K workspace: a MatMul / Conv call whose output
- *     tiles are too few to fill the GPU splits its k range over extra blocks
- *     and adds the partial sums in a second pass, through a workspace owned by
- *     the library, one per (device, stream), allocated by the first such call
- *     on that stream (8-64 MiB, kept until the process ends).  Inside a stream
- *     capture nothing is allocated: if the stream has no workspace yet the
- *     call runs unsplit (same result, slower), so run a call once on the
- *     capture stream before capturing it.
+ *   - The caller owns every buffer, and no entry point allocates device
+ *     memory (cm_buf_alloc is the allocator, as inference_buf_alloc is in the
+ *     reference).  A MatMul / Conv call whose output tiles are too few to
+ *     fill the GPU can split its k range over extra blocks and add the
+ *     partial sums in a second pass; the partials go to a WORKSPACE the
+ *     caller provides: per call (cm_matmul_ex / cm_conv_ex) or as the default
+ *     for calls that take none (cm_set_workspace).  The size a call would use
+ *     is returned by cm_matmul_workspace_size / cm_conv_workspace_size; a
+ *     smaller workspace gives fewer splits, none gives none -- the result is
+ *     the same bit for bit, only the speed differs.  Calls that may run at
+ *     the same time (different streams, a replayed HIP graph beside eager
+ *     work) must not share a workspace; calls queued on one stream may.
  *
  * Reference interfaces replaced (paths relative to the reference root):
  *   kernels/vectorop/include/VectorOP.h:86-95        VectorOPKernel
@@ -41,6 +44,7 @@
 #ifndef CORMORANT_AMD_H
 #define CORMORANT_AMD_H
 
+#include <stddef.h>
 #include <stdint.h>
 #include <hip/hip_runtime_api.h>
 
@@ -82,7 +86,10 @@ int cm_vectorop(const int16_t *a, const int16_t *b, int16_t *c, uint32_t size, u
  *   C_bi[n][m] = sat16(wrap32(sum_k A_bi[n][k] * B_bi[k][m]) >> 8)
  * with A_bi = a + bi*a_stride, B_bi = b + bi*b_stride, C_bi = c + bi*c_stride
  * (element strides; 0 broadcasts).  No limit on k (the reference's kMaxK=2048
- * static buffer is not needed). */
+ * static buffer is not needed); k = 0 gives 0.  Batches run in order: where
+ * the outputs of two batches overlap (c_stride < n*m) an element keeps the
+ * value of the last batch that writes it, as in the reference's sequential
+ * batch loop (MatmulKernel.cpp:108-111).  Uses the default workspace. */
 int cm_matmul(const int16_t *a, const int16_t *b, int16_t *c, uint32_t n, uint32_t k,
               uint32_t m, uint32_t batch, uint32_t a_stride, uint32_t b_stride,
               uint32_t c_stride, hipStream_t stream);
@@ -96,7 +103,7 @@ int cm_matmul_at(const int16_t *a, uint32_t a_off, const int16_t *b, uint32_t b_
 /* ConvKernel (ConvKernel.h:79-101): NCHW, weights [out_ch][in_ch][kh][kw]
  * (depthwise: [out_ch][1][kh][kw], output channel m reads input channel m),
  * bias [out_ch] (NULL allowed when has_bias == 0), pad_bottom/right implicit.
- * Depthwise requires out_ch <= in_ch. */
+ * Depthwise requires out_ch <= in_ch.  Uses the default workspace. */
 int cm_conv(const int16_t *x, const int16_t *weight, const int16_t *bias, int16_t *y,
             uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
             uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
@@ -136,19 +143,42 @@ typedef struct cm_epilogue {
     uint32_t act;
 } cm_epilogue_t;
 
-/* cm_matmul / cm_conv with an epilogue (epi may be NULL = none).  No reference
- * counterpart: they let a caller such as the scheduler's GPU backend fold the
- * run_op Add / Relu / Clip(0,6) that follows a run_matmul / run_conv into that
- * call, saving a launch and a round trip of the intermediate through memory. */
+/* cm_matmul / cm_conv with an epilogue (epi may be NULL = none) and a
+ * workspace of workspace_bytes bytes at device address `workspace` (NULL = no
+ * split-K).  No reference counterpart: they let a caller such as the
+ * scheduler's GPU backend fold the run_op Add / Relu / Clip(0,6) that follows
+ * a run_matmul / run_conv into that call, saving a launch and a round trip of
+ * the intermediate through memory, and keep split-K scratch in the caller's
+ * own pool (the reference's one-allocation buffer plan, _source.py:494-505). */
 int cm_matmul_ex(const int16_t *a, const int16_t *b, int16_t *c, uint32_t n, uint32_t k,
                  uint32_t m, uint32_t batch, uint32_t a_stride, uint32_t b_stride,
-                 uint32_t c_stride, const cm_epilogue_t *epi, hipStream_t stream);
+                 uint32_t c_stride, const cm_epilogue_t *epi, void *workspace,
+                 size_t workspace_bytes, hipStream_t stream);
 int cm_conv_ex(const int16_t *x, const int16_t *weight, const int16_t *bias, int16_t *y,
                uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
                uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride_h,
                uint32_t stride_w, uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
                uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise,
-               const cm_epilogue_t *epi, hipStream_t stream);
+               const cm_epilogue_t *epi, void *workspace, size_t workspace_bytes,
+               hipStream_t stream);
+
+/* Workspace bytes the call with these arguments uses for its split-K partial
+ * sums when given enough (0 = it never splits).  No reference counterpart; no
+ * GPU work.  A workspace of the largest size over a sequence of calls serves
+ * every call of the sequence on one stream. */
+size_t cm_matmul_workspace_size(uint32_t n, uint32_t k, uint32_t m, uint32_t batch,
+                                uint32_t a_stride, uint32_t b_stride, uint32_t c_stride);
+size_t cm_conv_workspace_size(uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                              uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh,
+                              uint32_t kw, uint32_t stride_h, uint32_t stride_w,
+                              uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
+                              uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise);
+
+/* Default workspace for cm_matmul / cm_matmul_at / cm_conv / cm_run_* (which
+ * take none), like cm_set_stream for the stream: device memory the caller
+ * allocated and keeps alive while calls may use it.  NULL / 0 = none (the
+ * default). */
+int cm_set_workspace(void *workspace, size_t bytes);
 
 /* ------------------------------------------------------------------ buffers */
 

@@ -169,7 +169,9 @@ void ora_matmul_omp(const int16_t *a, const int16_t *b, int16_t *c, uint32_t n, 
                     uint32_t m, uint32_t batch, uint32_t a_bs, uint32_t b_bs, uint32_t c_bs) {
     const int64_t n_tiles = (n + MM_TILE_N - 1) / MM_TILE_N;
     const int64_t units = (int64_t)batch * n_tiles;
-    if (c_bs == 0 && batch > 1) {   /* every batch writes the same C: keep order */
+    if (batch > 1 && (uint64_t)c_bs < (uint64_t)n * m) {
+        /* batch outputs overlap (c_bs = 0: every batch writes the same C): the
+         * sequential batch order decides each shared element */
         ora_matmul(a, b, c, n, k, m, batch, a_bs, b_bs, c_bs);
         return;
     }

@@ -61,10 +61,10 @@ def test_bad_epilogues_are_rejected_before_any_launch():
         return ctypes.byref(e)
 
     def mm(e):
-        return lib.cm_matmul_ex(fake, fake, fake, 2, 2, 2, 1, 0, 0, 0, e, None)
+        return lib.cm_matmul_ex(fake, fake, fake, 2, 2, 2, 1, 0, 0, 0, e, None, 0, None)
 
     def conv(e):
-        return lib.cm_conv_ex(fake, fake, None, fake, *([1] * 15), 0, 0, e, None)
+        return lib.cm_conv_ex(fake, fake, None, fake, *([1] * 15), 0, 0, e, None, 0, None)
 
     assert mm(epi(fake, 3, 0)) == _native.CM_ERR_INVALID
     assert mm(epi(fake, _native.CM_EPI_ADD_SAME, 3)) == _native.CM_ERR_INVALID
@@ -83,3 +83,28 @@ def test_missing_library_fails_loudly(tmp_path):
             _native.load(str(tmp_path / "nope.so"))
         finally:
             _native._lib = saved
+
+
+def test_workspace_size_queries():
+    """cm_*_workspace_size: a dry run of the launch decision (no GPU work).  Shapes
+    whose 128 x 128 output tiles fill the GPU never split; few tiles over a long k
+    range split into at most 16 parts of uint32 partials, rows x cols rounded up
+    to 8 columns."""
+    lib = _native.load()
+    assert lib.cm_matmul_workspace_size(4096, 4096, 4096, 1, 0, 0, 0) == 0
+    assert lib.cm_matmul_workspace_size(1024, 1024, 1024, 32, 1 << 20, 1 << 20, 1 << 20) == 0
+    # one tile, 79 k steps: 16 splits of 100 x 64 (60 rounded up) words
+    assert lib.cm_matmul_workspace_size(100, 5000, 60, 1, 0, 0, 0) == 16 * 100 * 64 * 4
+    # 16 x 1280 x 1000: 8 tiles, 20 k steps -> 20 splits wanted, at most 16, evened to 10
+    assert lib.cm_matmul_workspace_size(16, 1280, 1000, 1, 0, 0, 0) == 10 * 16 * 1000 * 4
+    # batched without overlap: one launch over every batch, no split
+    assert lib.cm_matmul_workspace_size(100, 5000, 60, 4, 500000, 300000, 6000) == 0
+    # batches whose outputs overlap run one launch each, each of which may split
+    assert lib.cm_matmul_workspace_size(100, 5000, 60, 3, 500000, 300000, 10) == 16 * 100 * 64 * 4
+    assert lib.cm_matmul_workspace_size(0, 5000, 60, 1, 0, 0, 0) == 0
+    # convolution: a 7x7x160 3x3 layer at batch 16 (the gather path over 784 columns)
+    conv = lib.cm_conv_workspace_size(16, 160, 7, 7, 160, 7, 7, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0)
+    assert conv > 0 and conv % (160 * 784 * 4) == 0
+    # conv A of the benchmark block: 784 tiles, no split; depthwise never splits
+    assert lib.cm_conv_workspace_size(32, 64, 56, 56, 128, 56, 56, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0) == 0
+    assert lib.cm_conv_workspace_size(1, 64, 56, 56, 64, 56, 56, 3, 3, 1, 1, 1, 1, 1, 1, 0, 1) == 0

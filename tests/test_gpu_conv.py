@@ -98,6 +98,23 @@ def test_geometries_full_range(geom):
     np.testing.assert_array_equal(got, want)
 
 
+@pytest.mark.parametrize("geom", [
+    # N, C, H, W, M, kh, kw, s, p: pointwise GEMM, implicit GEMM, direct path shapes
+    (2, 0, 16, 16, 24, 1, 1, 1, 0), (1, 0, 9, 11, 40, 3, 3, 2, 1), (2, 0, 160, 160, 8, 3, 3, 1, 1)])
+def test_zero_input_channels_give_bias(geom):
+    """in_ch = 0: the reference's channel loop is empty and y = bias (or 0)."""
+    N, C, H, W, M, kh, kw, s, p = geom
+    OH, OW = (H + 2 * p - kh) // s + 1, (W + 2 * p - kw) // s + 1
+    say(f"conv in_ch=0 {geom}")
+    b = wl.rng(832, M).integers(-32768, 32768, M, dtype=np.int16)
+    for bias in (1, 0):
+        got, want = conv_both(np.zeros(1, np.int16), np.zeros(1, np.int16), b, N, C, H, W, M, OH,
+                              OW, kh, kw, s, s, 1, 1, p, p, bias, 0)
+        np.testing.assert_array_equal(got, want)
+        np.testing.assert_array_equal(got.reshape(N, M, -1), np.broadcast_to(
+            (b if bias else np.zeros(M, np.int16))[None, :, None], (N, M, OH * OW)))
+
+
 @pytest.mark.parametrize("case", wl.CONV_CASES, ids=[c.name for c in wl.CONV_CASES])
 def test_config4_full_size(case):
     say(f"conv full-size {case.name}")

@@ -114,6 +114,37 @@ def test_same_output_every_batch_keeps_last():
     np.testing.assert_array_equal(got, want)
 
 
+def test_overlapping_batch_outputs_keep_the_last_batch():
+    """0 < c_stride < n*m: batch outputs overlap; the reference's sequential batch
+    loop leaves each shared element with the last writing batch's value."""
+    g = wl.rng(827)
+    for n, k, m, batch, c_bs in [(4, 32, 8, 5, 8), (16, 300, 40, 3, 1), (2, 64, 130, 4, 129)]:
+        say(f"matmul overlapping outputs {(n, k, m, batch, c_bs)}")
+        a = g.integers(-32768, 32768, batch * n * k, dtype=np.int16)
+        b = g.integers(-32768, 32768, batch * k * m, dtype=np.int16)
+        got, want = mm_both(a, b, n, k, m, batch, n * k, k * m, c_bs)
+        np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("n,m,batch", [(5, 7, 1), (130, 260, 3), (1, 1000, 1)])
+def test_k_zero_gives_zero(n, m, batch):
+    """k = 0: the reference's k loop is empty, every output is 0 (and the fused
+    column Add then gives the added row)."""
+    import torch
+    say(f"matmul k=0 {(n, m, batch)}")
+    c = empty_dev(batch * n * m)
+    K.MatmulKernel(None, None, c, n, 0, m, batch, 0, 0, n * m)
+    np.testing.assert_array_equal(host(c), np.zeros(batch * n * m, np.int16))
+    want = np.zeros(batch * n * m, np.int16)
+    oracle.matmul(np.zeros(1, np.int16), np.zeros(1, np.int16), want, n, 0, m, batch, 0, 0, n * m)
+    np.testing.assert_array_equal(want, 0)
+    add = wl.rng(828, n, m).integers(-32768, 32768, m, dtype=np.int16)
+    c2 = empty_dev(batch * n * m)
+    K.MatmulKernel(torch.zeros(1, dtype=torch.int16, device="cuda"), None, c2, n, 0, m, batch,
+                   0, 0, n * m, add=dev(add), add_column=True, act=K.ACT_RELU6)
+    np.testing.assert_array_equal(host(c2).reshape(-1, m), np.tile(np.clip(add, 0, 1536), (batch * n, 1)))
+
+
 def test_long_k_folds_partials():
     """K > 32768 takes the path that folds MFMA partials into a uint32 total."""
     n, k, m = 20, 70000, 24
@@ -134,18 +165,13 @@ def test_config3a_full():
     np.testing.assert_array_equal(got, want)
 
 
-def test_config3b_sampled_rows():
-    """4096^3: every output row compared is recomputed by the oracle's naive row loop;
-    128 rows spread over the matrix plus the first and last 8."""
+def test_config3b_full():
+    """4096^3 (K above the reference's kMaxK): the whole output against the oracle's
+    tiled kernel with OpenMP (itself pinned to the naive row loop and to Python
+    integers in test_oracle.py)."""
     case = wl.GEMM_CASES[1]
     say(f"matmul full-size {case.name}")
     a, b = wl.gemm_operands(case, 1)
     n, k, m = case.n, case.k, case.m
-    a2, b2 = a.reshape(n, k), b.reshape(k, m)
-    c = empty_dev(n * m)
-    K.MatmulKernel(dev(a2), dev(b2), c, n, k, m)
-    got = host(c).reshape(n, m)
-    rows = sorted(set(list(range(8)) + list(range(n - 8, n)) +
-                      list(wl.rng(826).choice(n, 128, replace=False))))
-    for r in rows:
-        np.testing.assert_array_equal(got[r], oracle.matmul_row(a2[r], b2, k, m), err_msg=f"row {r}")
+    got, want = mm_both(a.reshape(n, k), b.reshape(k, m), n, k, m)
+    np.testing.assert_array_equal(got, want)

@@ -70,19 +70,6 @@ def test_geometries_full_range_values(ptype, lp, cip, geom):
     np.testing.assert_array_equal(got, want)
 
 
-@pytest.mark.parametrize("case", wl.POOL_CASES, ids=[c.name for c in wl.POOL_CASES])
-def test_config4_pools_full_size(case):
-    """Pools of the benchmark block on a [32, 128, 56, 56] activation."""
-    say(f"pool full-size {case.name}")
-    x = wl.uniform_q88(wl.rng(811), (32, 128, 56, 56), -4.0, 4.0)
-    a = wl.pool_args(case, 32, 128, 56)
-    got, want = pool_both(x, a["batch"], a["channels"], a["in_h"], a["in_w"], a["out_h"],
-                          a["out_w"], a["pool_h"], a["pool_w"], a["stride_h"], a["stride_w"],
-                          a["pad_top"], a["pad_left"], a["dil_h"], a["dil_w"], a["pool_type"],
-                          a["lp_order"], a["count_include_pad"])
-    np.testing.assert_array_equal(got, want)
-
-
 def test_lp2_finalizer_all_accumulators():
     """LP p=2 finaliser (float32 convert + sqrt) for every A in [0, 2^31): checksums
     of GPU and host float32 paths agree, chunk by chunk."""

@@ -1,8 +1,10 @@
 """GPU parity of split-K launches: MatMul / Conv calls whose output tiles
 cannot fill the GPU are computed as k-split partial sums plus a reduction pass
 (the partials of every k range obey the same limb identity, and the uint32
-sum of the partials is the wrapping accumulator).  Compared bit for bit with
-the oracle, including full-range operands whose sums wrap."""
+sum of the partials is the wrapping accumulator).  The partials live in a
+workspace the caller passes; compared bit for bit with the oracle, including
+full-range operands whose sums wrap, with the full workspace, a smaller one
+(fewer splits) and none (no split)."""
 from __future__ import annotations
 
 import numpy as np
@@ -15,6 +17,14 @@ from tests.gpu_util import dev, empty_dev, host, oracle_threads, say
 from tests.test_gpu_epilogue import apply_epilogue, full_range
 
 pytestmark = pytest.mark.gpu
+
+
+def workspace(nbytes: int):
+    """A device workspace pre-filled with garbage (partials must not depend on it)."""
+    import torch
+    t = torch.empty(max(nbytes, 4) // 4, dtype=torch.int32, device="cuda")
+    t.fill_(0x3C5A7E11)
+    return t
 
 MM = [
     # name, n, k, m, operand range (None = full int16 range)
@@ -37,12 +47,17 @@ def test_matmul_split(case):
     else:
         a = wl.uniform_q88(g, n * k, -rng_, rng_)
         b = wl.uniform_q88(g, k * m, -rng_, rng_)
-    c = empty_dev(n * m)
-    K.MatmulKernel(dev(a), dev(b), c, n, k, m)
     want = np.zeros(n * m, np.int16)
     oracle.set_threads(oracle_threads())
     oracle.matmul(a, b, want, n, k, m, threads=True)
-    np.testing.assert_array_equal(host(c), want)
+    need = K.matmul_workspace_size(n, k, m)
+    assert need > 0, "the case is meant to split"
+    # the full workspace, one for two splits only, one too small to split, none
+    for ws_bytes in (need, 2 * n * ((m + 7) // 8 * 8) * 4, 4 * n, None):
+        c = empty_dev(n * m)
+        K.MatmulKernel(dev(a), dev(b), c, n, k, m,
+                       workspace=None if ws_bytes is None else workspace(ws_bytes))
+        np.testing.assert_array_equal(host(c), want, err_msg=f"workspace {ws_bytes}")
 
 
 @pytest.mark.parametrize("act", [K.ACT_NONE, K.ACT_RELU6])
@@ -54,7 +69,8 @@ def test_matmul_split_column_add(act):
     b = wl.uniform_q88(g, k * m, -0.5, 0.5)
     bias = full_range(g, m)
     c = empty_dev(n * m)
-    K.MatmulKernel(dev(a), dev(b), c, n, k, m, add=dev(bias), add_column=True, act=act)
+    K.MatmulKernel(dev(a), dev(b), c, n, k, m, add=dev(bias), add_column=True, act=act,
+                   workspace=workspace(K.matmul_workspace_size(n, k, m)))
     y = np.zeros(n * m, np.int16)
     oracle.matmul(a, b, y, n, k, m)
     np.testing.assert_array_equal(host(c), apply_epilogue(y, bias, True, act, n, m))
@@ -83,9 +99,13 @@ def test_conv_split(case):
     y = np.zeros(N * M * OH * OH, np.int16)
     oracle.set_threads(oracle_threads())
     oracle.conv(x, w, bias, y, *args, threads=True)
-    out = empty_dev(y.size)
-    K.ConvKernel(dev(x), dev(w), dev(bias), out, *args)
-    np.testing.assert_array_equal(host(out), y)
+    need = K.conv_workspace_size(*args)
+    assert need > 0, "the case is meant to split"
+    ws = workspace(need)
+    for w_ in (ws, None):
+        out = empty_dev(y.size)
+        K.ConvKernel(dev(x), dev(w), dev(bias), out, *args, workspace=w_)
+        np.testing.assert_array_equal(host(out), y)
     out2 = empty_dev(y.size)
-    K.ConvKernel(dev(x), dev(w), dev(bias), out2, *args, add=dev(res), act=K.ACT_RELU)
+    K.ConvKernel(dev(x), dev(w), dev(bias), out2, *args, add=dev(res), act=K.ACT_RELU, workspace=ws)
     np.testing.assert_array_equal(host(out2), apply_epilogue(y, res, False, K.ACT_RELU, 0, 0))

@@ -206,6 +206,67 @@ def test_matmul_accumulator_wraps_mod_2_32():
             assert c[i, j] == max(-32768, min(32767, w >> 8)), (i, j)
 
 
+@pytest.mark.parametrize("n,k,m,batch,c_bs", [(4, 32, 8, 5, 8), (16, 300, 40, 3, 1),
+                                               (2, 64, 130, 4, 129), (8, 16, 8, 4, 0)])
+def test_matmul_overlapping_outputs_sequential(n, k, m, batch, c_bs):
+    """Batches whose outputs overlap: each shared element holds the last writing
+    batch's value (MatmulKernel.cpp:108-111 runs batches in order), one thread and
+    OpenMP alike; checked against per-batch products written in order."""
+    g = wl.rng(907, n, c_bs)
+    a = g.integers(-32768, 32768, batch * n * k, dtype=np.int16)
+    b = g.integers(-32768, 32768, batch * k * m, dtype=np.int16)
+    size = (batch - 1) * c_bs + n * m
+    want = np.full(size, 77, np.int16)
+    for bi in range(batch):
+        A = a[bi * n * k:(bi + 1) * n * k].reshape(n, k)
+        B = b[bi * k * m:(bi + 1) * k * m].reshape(k, m)
+        want[bi * c_bs: bi * c_bs + n * m] = _closed_form_matmul(A, B).reshape(-1)
+    for threads in (False, True):
+        c = np.full(size, 77, np.int16)
+        oracle.matmul(a, b, c, n, k, m, batch, n * k, k * m, c_bs, threads=threads)
+        np.testing.assert_array_equal(c, want)
+
+
+def _closed_form_matmul(a, b):
+    """sat16(wrap32(sum a*b) >> 8) with Python integers (no fixed-width arithmetic)."""
+    s = a.astype(object) @ b.astype(object)
+    w = (s + 2**31) % 2**32 - 2**31
+    return np.vectorize(lambda v: max(-32768, min(32767, v >> 8)), otypes=[np.int64])(w)
+
+
+@pytest.mark.parametrize("shape", [(1, 1, 1), (3, 300, 5), (7, 257, 33), (4, 2049, 17)])
+def test_matmul_row_closed_form(shape):
+    """The naive row loop (TestMatmulSim.cpp:65-82 order) against Python big integers
+    on full-range operands whose sums wrap, row by row."""
+    n, k, m = shape
+    g = wl.rng(905, n, k, m)
+    a = g.integers(-32768, 32768, size=(n, k)).astype(np.int16)
+    b = g.integers(-32768, 32768, size=(k, m)).astype(np.int16)
+    a[0, :] = -32768
+    b[:, 0] = -32768                     # row 0 x col 0 = k * 2^30: wraps for k >= 2
+    want = _closed_form_matmul(a, b)
+    for r in range(n):
+        np.testing.assert_array_equal(oracle.matmul_row(a[r], b, k, m), want[r], err_msg=f"row {r}")
+
+
+@pytest.mark.parametrize("shape", [(5, 17, 3), (64, 784, 256), (33, 4096, 70), (9, 300, 1000)])
+def test_matmul_tiled_equals_naive_rows(shape):
+    """The reference's own invariant (TestMatmulSim.cpp:111-122): the tiled kernel
+    equals the naive product exactly; here ora_matmul (tile loops of the HLS kernel,
+    one thread and OpenMP) against ora_matmul_row on every row, full-range values."""
+    n, k, m = shape
+    g = wl.rng(906, n, k, m)
+    a = g.integers(-32768, 32768, size=(n, k)).astype(np.int16)
+    b = g.integers(-32768, 32768, size=(k, m)).astype(np.int16)
+    c1 = np.zeros((n, m), np.int16)
+    c2 = np.zeros((n, m), np.int16)
+    oracle.matmul(a, b, c1, n, k, m)
+    oracle.matmul(a, b, c2, n, k, m, threads=True)
+    rows = np.stack([oracle.matmul_row(a[r], b, k, m) for r in range(n)])
+    np.testing.assert_array_equal(c1, rows)
+    np.testing.assert_array_equal(c2, rows)
+
+
 # --------------------------------------------------------------------- Conv --
 
 def _conv_case(geom, seed):
