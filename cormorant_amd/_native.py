@@ -21,6 +21,7 @@ EXPORTS = (
     "cm_run_pool", "cm_set_stream", "cm_get_stream", "cm_sync", "cm_last_error", "cm_version",
     "cm_selftest_div", "cm_selftest_finalize", "cm_matmul_ex", "cm_conv_ex",
     "cm_matmul_workspace_size", "cm_conv_workspace_size", "cm_set_workspace",
+    "cm_matmul_noalloc",
 )
 
 CM_OK = 0
@@ -107,6 +108,7 @@ _SIGS = {
     "cm_matmul_workspace_size": (ctypes.c_size_t, [_u32] * 7),
     "cm_conv_workspace_size": (ctypes.c_size_t, [_u32] * 17),
     "cm_set_workspace": (_i, [_vp, ctypes.c_size_t]),
+    "cm_matmul_noalloc": (_i, [_vp, _vp, _vp] + [_u32] * 7 + [ctypes.POINTER(CmEpilogue), _vp]),
 }
 
 _lib = None

@@ -174,6 +174,18 @@ size_t cm_conv_workspace_size(uint32_t batch, uint32_t in_ch, uint32_t in_h, uin
                               uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
                               uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise);
 
+/* cm_matmul_ex for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
+ * counterpart in the reference.  Same arguments and result as cm_matmul_ex
+ * without the workspace: its split-K partial sums go to a static 16 MiB
+ * device array the library holds on each GPU until the process ends.  A shape
+ * whose partials would need more returns CM_ERR_RANGE (launching nothing).
+ * Every call on one GPU shares that GPU's array, so calls that overlap in time
+ * on one GPU (different streams, a replayed graph beside eager work) race. */
+int cm_matmul_noalloc(const int16_t *a, const int16_t *b, int16_t *c, uint32_t n, uint32_t k,
+                      uint32_t m, uint32_t batch, uint32_t a_stride, uint32_t b_stride,
+                      uint32_t c_stride, const cm_epilogue_t *epi, hipStream_t stream);
+
 /* Default workspace for cm_matmul / cm_matmul_at / cm_conv / cm_run_* (which
  * take none), like cm_set_stream for the stream: device memory the caller
  * allocated and keeps alive while calls may use it.  NULL / 0 = none (the
