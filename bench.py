@@ -182,9 +182,11 @@ def bench_block(steps: int, warmup: int):
     for case in wl.CONV_CASES:
         o = case.out_hw
         dy = torch.empty(case.batch * case.out_ch * o * o, dtype=torch.int16, device="cuda")
-        fn = lambda case=case, o=o, dy=dy: K.ConvKernel(
-            dx, dw_, db, dy, case.batch, case.in_ch, case.hw, case.hw, case.out_ch, o, o, case.k,
-            case.k, case.stride, case.stride, case.dil, case.dil, case.pad, case.pad, 1, 0)
+        args = (case.batch, case.in_ch, case.hw, case.hw, case.out_ch, o, o, case.k, case.k,
+                case.stride, case.stride, case.dil, case.dil, case.pad, case.pad, 1, 0)
+        need = K.conv_workspace_size(*args)   # the caller-owned scratch the call uses
+        ws = torch.empty(max(need, 4) // 4, dtype=torch.int32, device="cuda")
+        fn = lambda args=args, dy=dy, ws=ws: K.ConvKernel(dx, dw_, db, dy, *args, workspace=ws)
         for _ in range(warmup):
             fn()
         ms = time_launches([fn], steps)
@@ -194,7 +196,8 @@ def bench_block(steps: int, warmup: int):
                   f"s{case.stride} d{case.dil} p{case.pad} bias -> {o}x{o}",
             ms=round(ms, 5), gops=round(gops, 1),
             mfma_int8_tops=round(LIMB_PRODUCTS * gops / 1e3, 2),
-            mfma_frac=round(LIMB_PRODUCTS * gops / 1e3 / INT8_PEAK_TOPS, 4))
+            mfma_frac=round(LIMB_PRODUCTS * gops / 1e3 / INT8_PEAK_TOPS, 4),
+            workspace_bytes=need)
         out[case.name]["_dev"] = (dx, dw_, db, dy, x, w, b)
         conv_out[case.name] = (dy, o)
     ceilings = {}

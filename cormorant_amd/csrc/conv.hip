@@ -1,11 +1,16 @@
 // conv.hip -- ConvKernel for gfx950 (kernels/conv/kernel/ConvKernel.cpp:46-343).
 //
-// Dispatch:
-//   * standard conv, 1x1 / stride 1 / no padding, planes that fill 128-column
-//     tiles: batched GEMM Y[n] = W[out_ch][in_ch] x X[n][in_ch][h*w] on the
-//     int8-limb MFMA core;
-//   * any other standard conv: implicit GEMM on the same core, im2col gathered
-//     straight from NCHW x while the B tile is built (no im2col buffer);
+// Dispatch (standard convolutions, first match):
+//   * few output channels, K <= 32, many pixels: direct vector-ALU kernel;
+//   * 3x3, <= 64 channels in and out, stride 1 or 2: conv_patch (input patch and
+//     all weights in LDS);
+//   * windows of >= 2 taps over tiles of 128 pixels that fill the GPU, when the
+//     caller's workspace holds the packed weights: conv_pgemm (input patch in
+//     LDS, weights pre-split into limb planes);
+//   * 1x1 / stride 1 / no padding, planes that fill 128-column tiles: batched
+//     GEMM Y[n] = W[out_ch][in_ch] x X[n][in_ch][h*w] on the int8-limb MFMA core;
+//   * any other: implicit GEMM on the same core, im2col gathered straight from
+//     NCHW x while the B tile is built (no im2col buffer);
 //   * depthwise (is_depthwise = 1, weights [out_ch][1][kh][kw]): direct kernel,
 //     one thread per output, uint32 wrapping accumulator (ConvKernel.cpp:251-319).
 // All paths: acc = wrap32((has_bias ? bias << 8 : 0) + sum x*w), y = sat16(acc >> 8),
@@ -21,6 +26,11 @@ int cm_conv_gemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias,
 int cm_conv_pointwise_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
                              uint32_t batch, uint32_t in_ch, uint32_t out_ch, uint32_t hw,
                              const cm_epilogue_t* epi, const LaunchCtx& lc);
+int cm_conv_pgemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
+                         uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                         uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
+                         uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
+                         uint32_t pad_left, const cm_epilogue_t* epi, const LaunchCtx& lc);
 
 namespace {
 
@@ -304,9 +314,14 @@ int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int1
             default: return launch_direct<32>(g, s);
         }
     }
-    {
+    {   // 3x3 with <= 64 channels in and out: all weights staged per block
         const int rc = cm_conv_patch_launch(x, w, b, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w,
                                             kh, kw, sh, sw, dh, dw, pad_top, pad_left, epi, lc);
+        if (rc != 1) return rc;
+    }
+    if (kh * kw > 1) {   // patch GEMM: needs the caller's workspace for the packed weights
+        const int rc = cm_conv_pgemm_launch(x, w, b, y, batch, in_ch, in_h, in_w, out_ch, out_h,
+                                            out_w, kh, kw, sh, sw, dh, dw, pad_top, pad_left, epi, lc);
         if (rc != 1) return rc;
     }
     // 1x1 / stride 1 / no padding as one GEMM per image, when an image's

@@ -19,13 +19,16 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("case", wl.CONV_CASES, ids=[c.name for c in wl.CONV_CASES])
 def test_conv_then_pools_chained(case):
+    import torch
     say(f"block: {case.name} then the four pools")
     x, w, b = wl.conv_operands(case)
     o = case.out_hw
     args = (case.batch, case.in_ch, case.hw, case.hw, case.out_ch, o, o, case.k, case.k,
             case.stride, case.stride, case.dil, case.dil, case.pad, case.pad, 1, 0)
     y = empty_dev(case.batch * case.out_ch * o * o)
-    K.ConvKernel(dev(x), dev(w), dev(b), y, *args)
+    need = K.conv_workspace_size(*args)
+    ws = torch.empty(max(need, 4) // 4, dtype=torch.int32, device="cuda")
+    K.ConvKernel(dev(x), dev(w), dev(b), y, *args, workspace=ws)
     oracle.set_threads(oracle_threads())
     y_ref = np.zeros(y.numel(), np.int16)
     oracle.conv(x.reshape(-1), w.reshape(-1), b, y_ref, *args, threads=True)

@@ -13,10 +13,19 @@ from tests.gpu_util import dev, empty_dev, host, oracle_threads, say
 pytestmark = pytest.mark.gpu
 
 
-def conv_both(x, w, b, N, C, H, W, M, OH, OW, kh, kw, sh, sw, dh, dw, pt, pl, bias, dwise):
+def workspace_for(*args):
+    """A device workspace of the size the call asks for (None when it needs none)."""
+    import torch
+    need = K.conv_workspace_size(*args)
+    return torch.empty(max(need, 16) // 4, dtype=torch.int32, device="cuda").fill_(0x13572468) \
+        if need else None
+
+
+def conv_both(x, w, b, N, C, H, W, M, OH, OW, kh, kw, sh, sw, dh, dw, pt, pl, bias, dwise,
+              ws=False):
     y = empty_dev(N * M * OH * OW)
-    K.ConvKernel(dev(x), dev(w), dev(b), y, N, C, H, W, M, OH, OW, kh, kw, sh, sw, dh, dw, pt, pl,
-                 bias, dwise)
+    args = (N, C, H, W, M, OH, OW, kh, kw, sh, sw, dh, dw, pt, pl, bias, dwise)
+    K.ConvKernel(dev(x), dev(w), dev(b), y, *args, workspace=workspace_for(*args) if ws else None)
     want = np.zeros(N * M * OH * OW, np.int16)
     oracle.set_threads(oracle_threads())
     oracle.conv(np.ascontiguousarray(x.reshape(-1)), np.ascontiguousarray(w.reshape(-1)),
@@ -115,15 +124,65 @@ def test_zero_input_channels_give_bias(geom):
             (b if bias else np.zeros(M, np.int16))[None, :, None], (N, M, OH * OW)))
 
 
+@pytest.mark.parametrize("ws", [False, True], ids=["no_workspace", "workspace"])
 @pytest.mark.parametrize("case", wl.CONV_CASES, ids=[c.name for c in wl.CONV_CASES])
-def test_config4_full_size(case):
-    say(f"conv full-size {case.name}")
+def test_config4_full_size(case, ws):
+    say(f"conv full-size {case.name} workspace={ws}")
     x, w, b = wl.conv_operands(case)
     o = case.out_hw
     got, want = conv_both(x, w, b, case.batch, case.in_ch, case.hw, case.hw, case.out_ch, o, o,
                           case.k, case.k, case.stride, case.stride, case.dil, case.dil, case.pad,
-                          case.pad, 1, 0)
+                          case.pad, 1, 0, ws=ws)
     np.testing.assert_array_equal(got, want)
+
+
+def pgemm_need(C, M, kh, kw):
+    """Workspace of the patch-GEMM path: packed weight limb planes (128 rows x 64 k x 2
+    per row tile and k step) and one uint32 row sum per padded row."""
+    taps, mt, nch = kh * kw, -(-M // 128), -(-C // 64)
+    steps = (nch - 1) * taps + (taps * -(-(C - (nch - 1) * 64) // 16) + 3) // 4
+    return mt * steps * 2 * 128 * 64 + 4 * 128 * mt
+
+
+PGEMM = [
+    # N, C, H, W, M, kh, kw, s, d, p: every shape fills >= 200 blocks
+    (32, 64, 56, 56, 128, 3, 3, 1, 1, 1),      # conv A
+    (32, 64, 56, 56, 128, 3, 3, 2, 2, 2),      # conv B
+    (24, 70, 40, 36, 130, 3, 3, 1, 1, 1),      # two channel chunks, two row tiles
+    (64, 24, 30, 40, 8, 3, 3, 2, 2, 2),        # stride = dilation 2, 24 channels
+    (60, 16, 33, 40, 5, 5, 5, 2, 1, 2),        # 5x5, stride 2, dilation 1
+    (160, 130, 11, 11, 40, 3, 3, 1, 2, 2),     # three chunks (64, 64, 2 channels), dilation 2
+    (48, 8, 26, 22, 3, 3, 1, 1, 3, 1),         # 3x1 window, dilation 3
+]
+
+
+@pytest.mark.parametrize("geom", PGEMM, ids=[str(g) for g in PGEMM])
+def test_patch_gemm_full_range(geom):
+    """The patch-GEMM path (taken when a workspace holds the packed weights):
+    full-range operands whose sums wrap, with bias, a fused Add and an activation."""
+    N, C, H, W, M, kh, kw, s, d, p = geom
+    OH, OW = (H + 2 * p - d * (kh - 1) - 1) // s + 1, (W + 2 * p - d * (kw - 1) - 1) // s + 1
+    args = (N, C, H, W, M, OH, OW, kh, kw, s, s, d, d, p, p, 1, 0)
+    assert K.conv_workspace_size(*args) == pgemm_need(C, M, kh, kw), "expected the patch-GEMM path"
+    say(f"conv patch gemm {geom}")
+    g = wl.rng(833, *geom)
+    x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
+    w = g.integers(-32768, 32768, M * C * kh * kw, dtype=np.int16)
+    b = g.integers(-32768, 32768, M, dtype=np.int16)
+    add = g.integers(-32768, 32768, N * M * OH * OW, dtype=np.int16)
+    want = np.zeros(N * M * OH * OW, np.int16)
+    oracle.set_threads(oracle_threads())
+    oracle.conv(x, w, b, want, *args, threads=True)
+    y = empty_dev(want.size)
+    ws = workspace_for(*args)
+    K.ConvKernel(dev(x), dev(w), dev(b), y, *args, workspace=ws)
+    np.testing.assert_array_equal(host(y), want)
+    for act in (K.ACT_RELU, K.ACT_RELU6):
+        y2 = empty_dev(want.size)
+        K.ConvKernel(dev(x), dev(w), dev(b), y2, *args, add=dev(add), act=act, workspace=ws)
+        exp = np.clip(want.astype(np.int32) + add, -32768, 32767)
+        exp = np.clip(exp, 0, 32767 if act == K.ACT_RELU else 1536)
+        np.testing.assert_array_equal(host(y2).astype(np.int32), exp)
 
 
 @pytest.mark.parametrize("seed", range(16))
