@@ -60,7 +60,8 @@ inline FastDiv make_fastdiv(uint32_t d) {
 }
 
 __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
-    const uint64_t t = (uint64_t)n * f.m_lo + (f.m_hi ? (uint64_t)n << 32 : 0ull);
+    // m_hi is 0 or 1: n * m_hi selects without a branch on the divisor
+    const uint64_t t = (uint64_t)n * f.m_lo + ((uint64_t)(n * f.m_hi) << 32);
     return (uint32_t)(t >> f.p);
 }
 

@@ -8,15 +8,17 @@
 //   conv_wpack  splits the weights once per call into int8 limb planes in the
 //               caller's workspace, in the k order the main kernel consumes, and
 //               sums each output channel's weights (the limb identity's row sums);
-//   conv_pgemm  one block per (128 output channels, 128 consecutive output
-//               pixels of one image).  The input rows those pixels' windows touch
+//   conv_pgemm  one block per (128 output channels, range of L consecutive
+//               output pixels of one image; L is chosen so the blocks spread
+//               evenly over the CUs).  The input rows the range's windows touch
 //               are loaded once per chunk of 64 channels and stored in LDS
 //               channel-minor as limb planes, so the 16 k values one MFMA lane
 //               supplies (16 channels of one tap at one pixel) are one 16-byte
 //               LDS read: the B operand needs no per-step staging and no gather.
-//               The per-step A tile is two 16-byte loads per thread from the
-//               packed planes (L2-resident) straight into LDS.  No limb split,
-//               transposition or load-address arithmetic runs in the k loop.
+//               Each wave's A fragments are 16-byte loads from the packed planes
+//               (L2-resident).  No limb split, transposition, column sum or
+//               load-address arithmetic beyond one add per tile runs in the k
+//               loop.
 //
 // Limbs and the exact sum are the GEMM kernel's: v = 256*vh + vl + 128 with
 // vh = v >> 8, vl = (v & 255) - 128 (both int8), and
@@ -34,6 +36,10 @@
 // those: row r, column col hold x[c][ih_first + g*r][g*col - pad_left]; pixel
 // (oh, ow) at tap (kh_i, kw_i) reads row (oh - oh_first)*S' + kh_i*D', column
 // ow*S' + kw_i*D' (S' = stride/g, D' = dilation/g).
+#include <algorithm>
+#include <atomic>
+#include <type_traits>
+
 #include "cm_internal.h"
 #include "q88.h"
 
@@ -44,27 +50,32 @@ typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
 constexpr int BM = 128;
 constexpr uint32_t kPackTile = 2u * BM * 64u; // packed bytes per (row tile, step): hi then lo
+constexpr uint32_t kPackTile8 = BM * 64u;     // int8 plane bytes per (row tile, step)
 constexpr int kMaxQ = 256;                    // q table entries (taps * 4 <= 256)
 
 struct PgArgs {
     const int16_t* x;
     const uint8_t* wpk;          // packed weight limb planes
     const uint32_t* wsum;        // [M] sum of each output channel's weights (wrapping)
+    const uint32_t* wfit;        // [M] 1 when every weight of the row is in [-128, 127]
     const int16_t* bias;
     int16_t* y;
     uint32_t C, H, W, M, OH, OW, P;   // P = OH * OW
     uint32_t KW, taps, S, Sg, Dg, g, pt, pl;
+    uint32_t khspan;             // patch rows one output row's windows span: (KH - 1) * D' + 1
     uint32_t nchunks, steps;     // channel chunks; k steps over all chunks
     uint32_t PW, ppitch;         // patch positions per row; LDS bytes per position
-    uint32_t prows, npos;        // patch rows / positions staged per block (the most any block needs)
+    uint32_t prows, npos;        // patch rows / positions the LDS holds (the most any block needs)
     uint32_t p_plane;            // LDS bytes of one patch limb plane (the zero slot included)
     uint32_t zslot;              // byte offset in each plane of 16 bytes holding the limbs of 0
+    uint32_t spos_off, epi_off;  // LDS byte offsets of the position sums and the epilogue tiles
     uint32_t lhc, wr, nh;        // padding columns: left [0, lhc), right [wr, wr + nh - lhc)
     uint32_t cpt_last;           // 16-channel groups of the last chunk
-    uint32_t R, bands;           // output rows per block; bands per image
-    FastDiv div_bands, div_ow, div_npos, div_pw, div_nv, div_prows, div_nh, div_kw, div_cpt4, div_cpt_last;
+    uint32_t L, rpi, rpi_n;      // output pixels per block; ranges per image; ranges per row tile
+    FastDiv div_nbm, div_rpi, div_ow, div_npos, div_pw, div_nv, div_prows, div_nh, div_kw, div_cpt4, div_cpt_last;
     uint32_t vw;                 // output / Add access width in elements (8 or 1)
-    uint32_t x_img_bytes, pk_bytes;
+    uint32_t x_img_bytes, pk_bytes;   // pk_bytes: both packed layouts (limb planes, then int8)
+    uint32_t pk8_off;            // byte offset of the int8 plane
     uint64_t x_img, y_img;
     EpiArgs epi;
 };
@@ -84,11 +95,15 @@ __device__ __forceinline__ uint32_t pack2(uint32_t lo, uint32_t hi) {
 // One block per output channel row m of a 128-row tile (rows past M are packed
 // as zeros).  Word w of a (row tile, step) plane row covers k bytes 4w..4w+3 of
 // the step: sub-chunk q = 4*step_in_chunk + w/4, channels 16*(q % cpt) + 4*(w%4)
-// + 0..3 of the chunk, tap q / cpt.
+// + 0..3 of the chunk, tap q / cpt.  Besides the two limb planes the row is
+// written as int8 values (w8 plane: meaningful when every weight of the row
+// lies in [-128, 127], which wfit records).
 struct PackArgs {
     const int16_t* w;
     uint8_t* wpk;
+    uint8_t* wpk8;
     uint32_t* wsum;
+    uint32_t* wfit;
     uint32_t C, M, taps, nchunks, steps, steps_full;   // steps_full = taps (a full chunk)
 };
 
@@ -97,7 +112,7 @@ __global__ __launch_bounds__(256) void conv_wpack(PackArgs a) {
     const uint32_t mt = m / BM, r = m % BM;
     const bool mok = m < a.M;
     const int16_t* wrow = a.w + (uint64_t)(mok ? m : 0u) * a.C * a.taps;
-    uint32_t sum = 0;
+    uint32_t sum = 0, fit = 1u;
     const uint32_t words = a.steps * 16u;
     for (uint32_t i = threadIdx.x; i < words; i += 256) {
         const uint32_t gs = i >> 4, wd = i & 15u;
@@ -108,19 +123,22 @@ __global__ __launch_bounds__(256) void conv_wpack(PackArgs a) {
         const uint32_t cpt = (cc + 15u) / 16u;
         const uint32_t q = ls * 4u + (wd >> 2);
         const uint32_t tap = q / cpt, cg = q - tap * cpt;
-        uint32_t hw = 0, lw = 0;
+        uint32_t hw = 0, lw = 0, bw = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint32_t cl = cg * 16u + (wd & 3u) * 4u + j;
             const bool ok = mok && tap < a.taps && cl < cc;
             const int32_t v = ok ? (int32_t)wrow[(uint64_t)(c0 + cl) * a.taps + tap] : 0;
             sum += (uint32_t)v;
+            fit &= (uint32_t)(v >= -128 && v <= 127);
             hw |= hi_byte(v) << (8 * j);
             lw |= lo_byte(v) << (8 * j);
+            bw |= ((uint32_t)v & 0xFFu) << (8 * j);
         }
         uint8_t* dst = a.wpk + (uint64_t)(mt * a.steps + gs) * kPackTile + r * 64u + wd * 4u;
         *reinterpret_cast<uint32_t*>(dst) = hw;
         *reinterpret_cast<uint32_t*>(dst + BM * 64u) = lw;
+        *reinterpret_cast<uint32_t*>(a.wpk8 + (uint64_t)(mt * a.steps + gs) * kPackTile8 + r * 64u + wd * 4u) = bw;
     }
     // row sum (every real weight once; padding adds 0)
     __shared__ uint32_t red[256];
@@ -131,76 +149,111 @@ __global__ __launch_bounds__(256) void conv_wpack(PackArgs a) {
         __syncthreads();
     }
     if (threadIdx.x == 0 && mok) a.wsum[m] = red[0];
+    const int all_fit = __syncthreads_and((int)fit);
+    if (threadIdx.x == 0) a.wfit[m] = all_fit ? 1u : 0u;
 }
 
 // ------------------------------------------------------------- main kernel --
-// Block: 256 threads = 4 waves (2 x 2), 128 output channels of one band of R
-// output rows of one image, computed in sub-tiles of 64 pixels (flattened over
-// the band); wave tile 64 channels x 32 pixels (4 x 2 MFMA 16x16x64 tiles,
-// three accumulator sets).  With one channel chunk the band's input rows are
-// staged into the LDS patch once and every sub-tile reads them; with more
-// chunks each sub-tile restages every chunk.  Each wave loads its A fragments
-// straight from the packed planes (a row tile of one limb is 16 rows x 64
-// bytes, 1 KB contiguous: one 16-byte load per lane), one step ahead, so the k
-// loop has no barrier and no LDS writes.  A sub-tile's results go out through
-// a 64-row LDS tile in two halves, as 16-byte stores of 8 neighbouring pixels.
+// Block: 256 threads = 4 waves, 128 output channels (wave w: channels 32w ..
+// 32w+31) of one range of L consecutive output pixels of one image, computed
+// in sub-tiles of 64 pixels; wave tile 32 channels x 64 pixels (2 x 4 MFMA
+// 16x16x64 tiles, three accumulator sets).  Every wave reads its own weight
+// rows (no two waves load the same A data) and all 64 pixels of the patch.
+// With one channel chunk the input rows of the range are staged into the LDS
+// patch once and every sub-tile reads them; with more chunks each sub-tile
+// restages every chunk.  After staging, each patch position's channel sum is
+// kept in LDS, so a pixel's window sum (the limb identity's column sum) is a
+// sum over taps, read outside the k loop.  A fragments come straight from the
+// packed planes (a row tile of one limb is 16 rows x 64 bytes, 1 KB
+// contiguous: one 16-byte load per lane), one step ahead, so the k loop has
+// no barrier and no LDS writes.  Each wave finishes its own outputs through a
+// private 16-row LDS tile (no block barrier) and stores rows of 8 pixels as
+// 16-byte writes.
 constexpr int kPgThreads = 256;
-constexpr int PBN = 64;          // pixels per sub-tile
-constexpr int kTilePitch = 68;   // epilogue half tile: words per row (64 + 4)
+constexpr int PBN = 64;                                 // pixels per sub-tile
+constexpr uint32_t kEpiPitch = 72;                      // int16 per row of a wave's epilogue tile
+constexpr uint32_t kEpiBytes = 16u * kEpiPitch * 2u;    // 16 channel rows x 64 pixels (+ pad)
+constexpr int kMaxTaps = kMaxQ / 4;
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 // VEC: patch rows loaded 16 bytes at a time with g = VEC; 0 = per element.
 // MULTI: more than one channel chunk (restaged inside the k loop, with fewer
 // loads in flight while the accumulators are live).
-template <bool HAS_BIAS, int VEC, bool MULTI>
+// NS: A fragment sets in flight (3: two steps of prefetch, for one chunk whose
+// step count is a multiple of 3; else 2: one step).
+template <bool HAS_BIAS, int VEC, bool MULTI, int NS>
 __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
-    constexpr int kPB = MULTI ? 1 : 3;   // 16-byte staging tasks per thread in flight
+    static_assert(NS == 2 || (NS == 3 && !MULTI), "three A sets need one chunk");
+    constexpr int kPB = MULTI ? 1 : 4;   // 16-byte staging tasks per thread in flight
     extern __shared__ __align__(16) uint8_t lds[];
-    __shared__ uint32_t colterm_s[PBN];                // 128 * column sum - 16384 * Kp
-    __shared__ __align__(16) uint32_t rowterm_s[BM];   // 128 * row sum + bias << 8
-    __shared__ int32_t qtab[kMaxQ];   // per sub-chunk q: patch byte offset of its tap and group
+    __shared__ int32_t qtab[kMaxQ + 4];  // per sub-chunk q: patch byte offset of its tap and group
+    __shared__ uint32_t tpos[kMaxTaps];  // per tap: patch position offset from a window origin
+    __shared__ uint32_t rowterm_s[BM];   // per output channel of the row tile: the row term
     uint8_t* p_hi = lds;
     uint8_t* p_lo = lds + g.p_plane;
-    uint32_t* tile = reinterpret_cast<uint32_t*>(lds + 2 * g.p_plane);   // [64][kTilePitch]
+    uint32_t* spos = reinterpret_cast<uint32_t*>(lds + g.spos_off);   // per position: channel sum
 
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t wrow = (wave >> 1) * 64, wcol = (wave & 1) * 32;
-    const uint32_t mt = blockIdx.y, row0 = mt * BM;
-    const uint32_t n = fdiv(blockIdx.x, g.div_bands);
-    const uint32_t oh0 = (blockIdx.x - n * g.bands) * g.R;
-    const uint32_t bp0 = oh0 * g.OW;                              // the band's first pixel
-    const uint32_t bp1 = min(oh0 + g.R, g.OH) * g.OW;             // one past its last
-    const int32_t ih_first = (int32_t)(oh0 * g.S) - (int32_t)g.pt;
+    int16_t* et = reinterpret_cast<int16_t*>(lds + g.epi_off + wave * kEpiBytes);
+    // Workgroups are dealt to the 8 XCDs round robin; block b of XCD x takes the
+    // x-th contiguous share of the (row tile, image, range) order, so ranges
+    // that share input rows (and blocks that share weights) meet in one L2.
+    const uint32_t nb = gridDim.x, per = nb >> 3, rem = nb & 7u, xcd = blockIdx.x & 7u, idx = blockIdx.x >> 3;
+    const uint32_t lg = xcd < rem ? xcd * (per + 1u) + idx : rem * (per + 1u) + (xcd - rem) * per + idx;
+    const uint32_t mt = fdiv(lg, g.div_nbm), rest = lg - mt * g.rpi_n;
+    const uint32_t row0 = mt * BM, wrow = row0 + wave * 32;
+    const uint32_t n = fdiv(rest, g.div_rpi);
+    const uint32_t pb = (rest - n * g.rpi) * g.L;                       // the range's first pixel
+    const uint32_t pe = min(pb + g.L, g.P);                             // one past its last
+    const uint32_t oh_a = fdiv(pb, g.div_ow), oh_b = fdiv(pe - 1u, g.div_ow);
+    const uint32_t prows_b = (oh_b - oh_a) * g.Sg + g.khspan;          // patch rows this range reads
+    const int32_t ih_first = (int32_t)(oh_a * g.S) - (int32_t)g.pt;
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(g.x + (uint64_t)n * g.x_img, g.x_img_bytes);
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(reinterpret_cast<const int16_t*>(g.wpk), g.pk_bytes);
     const uint32_t hw_in = g.H * g.W;
 
-    if (tid < BM) {
-        const uint32_t m = row0 + tid;
-        const uint32_t b = HAS_BIAS && m < g.M ? (uint32_t)((int32_t)g.bias[m] * 256) : 0u;
-        rowterm_s[tid] = (m < g.M ? 128u * g.wsum[m] : 0u) + b;
-    }
     if (tid == 0) {   // the zero slot: 16 bytes of each plane holding the limbs of 0
         *reinterpret_cast<v4u*>(p_hi + g.zslot) = v4u{0u, 0u, 0u, 0u};
         *reinterpret_cast<v4u*>(p_lo + g.zslot) = v4u{0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
     }
 
-    // A fragments of step gs: row tile i of the wave's 64 rows, hi and lo planes
+    // A fragments of step gs: row tile i of the wave's 32 rows, hi and lo planes
     // (steps past the last one read another row tile's data or, past the buffer,
     // 0; neither is used)
-    const uint32_t a_src = (mt * g.steps) * kPackTile + (wrow + (lane & 15)) * 64u + (lane >> 4) * 16u;
-    auto a_load = [&](uint32_t gs, v4i (&ah)[4], v4i (&al)[4]) {
+    const uint32_t a_src = (mt * g.steps) * kPackTile + (wave * 32u + (lane & 15)) * 64u + (lane >> 4) * 16u;
+    auto a_load = [&](uint32_t gs, v4i (&ah)[2], v4i (&al)[2]) {
         const uint32_t off = a_src + gs * kPackTile;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 2; ++i) {
             ah[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wrs, off + i * 1024u, 0, 0));
             al[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
                 wrs, off + BM * 64u + i * 1024u, 0, 0));
         }
     };
+    // the int8 plane's A fragments of step gs (rows whose weights all fit int8)
+    const uint32_t a8_src = g.pk8_off + (mt * g.steps) * kPackTile8 + (wave * 32u + (lane & 15)) * 64u +
+                            (lane >> 4) * 16u;
+    auto a_load8 = [&](uint32_t gs, v4i (&a8)[2]) {
+        const uint32_t off = a8_src + gs * kPackTile8;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            a8[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wrs, off + i * 1024u, 0, 0));
+    };
+    // Row terms and int8 flags of the block's 128 output channels: loaded here,
+    // used after the patch is staged (128 * row sum + bias << 8)
+    const uint32_t rm = min(row0 + (tid & (BM - 1)), g.M - 1u);
+    const uint32_t ld_wsum = g.wsum[rm], ld_fit = g.wfit[rm];
+    const int32_t ld_bias = HAS_BIAS ? (int32_t)g.bias[rm] : 0;
 
-    // Patch staging of one chunk (the band's rows).  Rows outside the image and
-    // channels past C read 0 through the buffer range.
-    auto stage_patch = [&](uint32_t c0, uint32_t cpt, const FastDiv& div_cpt) {
+    // Patch staging of one chunk (the range's rows; tasks past prows_b are
+    // skipped).  Rows outside the image and channels past C read 0 through the
+    // buffer range.
+    auto stage_patch = [&](uint32_t c0, uint32_t cpt) {
         const uint32_t ncq = cpt * 4u;
         if constexpr (VEC == 0) {
             // per element: task e = (channel quad cq, position), position fastest
@@ -216,11 +269,11 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
                     const uint32_t r = fdiv(pos, g.div_pw), col = pos - r * g.PW;
                     const int32_t ih = ih_first + (int32_t)(r * g.g);
                     const int32_t iw = (int32_t)(col * g.g) - (int32_t)g.pl;
-                    const uint32_t okp = (uint32_t)(e < ntask) & (uint32_t)((uint32_t)ih < g.H) &
-                                         (uint32_t)((uint32_t)iw < g.W);
+                    const uint32_t live = (uint32_t)(e < ntask) & (uint32_t)(r < prows_b);
+                    const uint32_t okp = live & (uint32_t)((uint32_t)ih < g.H) & (uint32_t)((uint32_t)iw < g.W);
                     const uint32_t c = c0 + cq * 4u;
                     const uint32_t base = (c * hw_in + (uint32_t)ih * g.W + (uint32_t)iw) * 2u;
-                    dst[u] = e < ntask ? pos * g.ppitch + cq * 4u : 0xFFFFFFFFu;
+                    dst[u] = live ? pos * g.ppitch + cq * 4u : 0xFFFFFFFFu;
 #pragma unroll
                     for (int jj = 0; jj < 4; ++jj) {
                         const uint32_t ok = okp & (uint32_t)(c + jj < g.C);
@@ -261,11 +314,11 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
                     const uint32_t cqr = fdiv(e, g.div_nv), vv = e - cqr * nv;
                     const uint32_t cq = fdiv(cqr, g.div_prows), r = cqr - cq * g.prows;
                     const int32_t ih = ih_first + (int32_t)(r * VEC);
-                    const uint32_t okr = (uint32_t)(e < ntask) & (uint32_t)((uint32_t)ih < g.H);
+                    const uint32_t live = (uint32_t)(e < ntask) & (uint32_t)(r < prows_b);
+                    const uint32_t okr = live & (uint32_t)((uint32_t)ih < g.H);
                     const uint32_t c = c0 + cq * 4u;
                     const uint32_t base = (c * hw_in + (uint32_t)ih * g.W + vv * 8u) * 2u;
-                    dst0[u] = e < ntask ? (r * g.PW + vv * (8u / VEC) + lh) * g.ppitch + cq * 4u
-                                        : 0xFFFFFFFFu;
+                    dst0[u] = live ? (r * g.PW + vv * (8u / VEC) + lh) * g.ppitch + cq * 4u : 0xFFFFFFFFu;
 #pragma unroll
                     for (int jj = 0; jj < 4; ++jj) {
                         const uint32_t ok = okr & (uint32_t)(c + jj < g.C);
@@ -301,166 +354,279 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
             for (uint32_t e = tid; e < nhalo; e += kPgThreads) {
                 const uint32_t cqr = fdiv(e, g.div_nh), hcol = e - cqr * g.nh;
                 const uint32_t cq = fdiv(cqr, g.div_prows), r = cqr - cq * g.prows;
+                if (r >= prows_b) continue;
                 const uint32_t col = hcol < g.lhc ? hcol : g.wr + (hcol - g.lhc);
                 const uint32_t dst = (r * g.PW + col) * g.ppitch + cq * 4u;
                 *reinterpret_cast<uint32_t*>(p_hi + dst) = 0u;
                 *reinterpret_cast<uint32_t*>(p_lo + dst) = 0x80808080u;
             }
         }
-        // q table of the chunk: q = tap * cpt + cg -> byte offset of (tap, group)
-        // from a pixel's window origin; -1 past the chunk's last sub-chunk
-        for (uint32_t q = tid; q < (uint32_t)kMaxQ; q += kPgThreads) {
+    };
+
+    // After a chunk is staged: each position's sum over the chunk's channel
+    // slots (x = 256 * high + low + 128 per slot; a zero slot adds 0), and the
+    // chunk's q table: q = tap * cpt + cg -> byte offset of (tap, group) from a
+    // pixel's window origin, -1 past the chunk's last sub-chunk.
+    auto chunk_tables = [&](uint32_t cpt, const FastDiv& div_cpt, bool sums) {
+        const uint32_t np = sums ? prows_b * g.PW : 0u;
+        const uint32_t base = 128u * 16u * cpt;
+        for (uint32_t pos = tid; pos < np; pos += kPgThreads) {
+            int32_t sh = 0, sl = 0;
+            for (uint32_t c = 0; c < cpt; ++c) {
+                sh = bsum16(*reinterpret_cast<const v4i*>(p_hi + pos * g.ppitch + c * 16u), sh);
+                sl = bsum16(*reinterpret_cast<const v4i*>(p_lo + pos * g.ppitch + c * 16u), sl);
+            }
+            spos[pos] = 256u * (uint32_t)sh + (uint32_t)sl + base;
+        }
+        for (uint32_t q = tid; q < (uint32_t)kMaxQ + 4u; q += kPgThreads) {
             const uint32_t tap = fdiv(q, div_cpt), cg = q - tap * cpt;
             const uint32_t khi = fdiv(tap, g.div_kw), kwi = tap - khi * g.KW;
-            qtab[q] = tap < g.taps ? (int32_t)(((khi * g.PW + kwi) * g.Dg) * g.ppitch + cg * 16u) : -1;
+            const uint32_t tp = (khi * g.PW + kwi) * g.Dg;
+            qtab[q] = tap < g.taps ? (int32_t)(tp * g.ppitch + cg * 16u) : -1;
+            if (cg == 0 && tap < (uint32_t)kMaxTaps) tpos[tap] = tap < g.taps ? tp : 0u;
         }
     };
 
-    const bool sums = (wave >> 1) == 0;   // one wave row publishes the column sums
-    const uint32_t kp128 = 128u * 64u * g.steps;
     const uint32_t kp_term = 16384u * 64u * g.steps;
     const int32_t lo = q88::act_lo(g.epi.act), hi = q88::act_hi(g.epi.act);
-    const uint32_t nsub = (bp1 - bp0 + PBN - 1) / PBN;
-    v4i fa_h[2][4], fa_l[2][4];
+    const bool plain = g.epi.add_mode == 0u && g.epi.act == 0u;   // no Add, no activation
+    const uint32_t nsub = (pe - pb + PBN - 1) / PBN;
+    // A fragment sets: the set of global step gs is gs % NS, and the next NS - 1
+    // steps' sets are in flight while a step's MFMAs run
+    v4i fa_h[NS][2], fa_l[NS][2];
     uint32_t gs = 0;   // global k step of the next MFMA step, over all sub-tiles
+    // every weight of the row tile fits int8: two limb products (w * x_hi and
+    // w * x_lo) instead of four, and no column term
+    bool fast = false;
+    // step ks + d of a sub-tile, wrapping into the next sub-tile's steps
+    auto ks_plus = [&](uint32_t ks, uint32_t d) {
+        uint32_t k = ks + d;
+        k = k >= g.steps ? k - g.steps : k;
+        return k >= g.steps ? k - g.steps : k;
+    };
 
     for (uint32_t sub = 0; sub < nsub; ++sub) {
-        const uint32_t p0 = bp0 + sub * PBN;
+        const uint32_t p0 = pb + sub * PBN;
+        const uint32_t pn = min((uint32_t)PBN, pe - p0);   // pixels of this sub-tile
+        const uint32_t nj = (pn + 15u) / 16u;              // 16-pixel column tiles in use
         // the first chunk's patch (with one chunk: staged once for every sub-tile),
         // before the accumulators and A fragments of this sub-tile are live
         if (sub == 0 || MULTI) {
             if (sub) __syncthreads();   // every wave is done with the previous patch
-            stage_patch(0u, MULTI ? 4u : g.cpt_last, MULTI ? g.div_cpt4 : g.div_cpt_last);
-            __syncthreads();
-        }
-        if (sub == 0) a_load(0, fa_h[0], fa_l[0]);
-        // byte offset in the patch of the window origin of this lane's pixel in
-        // each column tile: row (oh - oh0) * S', column ow * S'
-        uint32_t pbase[2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t px = min(p0 + wcol + j * 16 + (lane & 15), bp1 - 1u);   // past the band: any of its pixels
-            const uint32_t oh = fdiv(px, g.div_ow), ow = px - oh * g.OW;
-            pbase[j] = (((oh - oh0) * g.PW + ow) * g.Sg) * g.ppitch;
-        }
-        v4i hh[4][2], mid[4][2], ll[4][2];
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                hh[i][j] = v4i{0, 0, 0, 0}; mid[i][j] = v4i{0, 0, 0, 0}; ll[i][j] = v4i{0, 0, 0, 0};
-            }
-        int32_t csh[2] = {0, 0}, csl[2] = {0, 0};
-
-        auto mfma_step = [&](uint32_t ls, const v4i (&ah)[4], const v4i (&al)[4]) {
-            const int32_t qo = qtab[ls * 4u + (lane >> 4)];
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                // past the chunk's last sub-chunk: the zero slot (the limbs of 0)
-                const uint32_t a = qo >= 0 ? pbase[j] + (uint32_t)qo : g.zslot;
-                const v4i bh = *reinterpret_cast<const v4i*>(p_hi + a);
-                const v4i bl = *reinterpret_cast<const v4i*>(p_lo + a);
-                if (sums) {
-                    csh[j] = bsum16(bh, csh[j]);
-                    csl[j] = bsum16(bl, csl[j]);
-                }
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    hh[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bh, hh[i][j], 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    mid[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bl, mid[i][j], 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    ll[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], bl, ll[i][j], 0, 0, 0);
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    mid[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], bh, mid[i][j], 0, 0, 0);
-            }
-        };
-
-        // k loop over the chunks (steps gs of the packed planes restart at 0 for
-        // each sub-tile: the A fragments of the next step load while this step's
-        // MFMAs run; the pairs keep the register sets fixed at compile time)
-        uint32_t ks = 0;   // k step within this sub-tile
-        for (uint32_t ch = 0; ch < (MULTI ? g.nchunks : 1u); ++ch) {
-            const uint32_t c0 = ch * 64u;
-            const bool last = ch + 1 == g.nchunks;
-            const uint32_t cpt = last ? g.cpt_last : 4u;
-            const uint32_t nst = (g.taps * cpt + 3u) / 4u;
-            if (MULTI && ch) {   // later chunks: restaged here
-                __syncthreads();   // every wave is done with the previous chunk's patch
-                stage_patch(c0, cpt, last ? g.div_cpt_last : g.div_cpt4);
+            stage_patch(0u, MULTI ? 4u : g.cpt_last);
+            if (sub == 0) {
+                const bool real = row0 + tid < g.M;
+                if (tid < BM) rowterm_s[tid] = real ? 128u * ld_wsum + (uint32_t)ld_bias * 256u : 0u;
+                fast = __syncthreads_and(tid >= BM || !real || ld_fit != 0u) != 0;
+            } else {
                 __syncthreads();
             }
-            uint32_t ls = 0;
-            if (gs & 1u) {
-                a_load(ks + 1 < g.steps ? ks + 1 : 0u, fa_h[0], fa_l[0]);
-                mfma_step(ls, fa_h[1], fa_l[1]);
-                ++ls; ++gs; ++ks;
-            }
-            for (; ls + 2 <= nst; ls += 2, gs += 2, ks += 2) {
-                a_load(ks + 1 < g.steps ? ks + 1 : 0u, fa_h[1], fa_l[1]);
-                mfma_step(ls, fa_h[0], fa_l[0]);
-                a_load(ks + 2 < g.steps ? ks + 2 : ks + 2 - g.steps, fa_h[0], fa_l[0]);
-                mfma_step(ls + 1, fa_h[1], fa_l[1]);
-            }
-            if (ls < nst) {
-                a_load(ks + 1 < g.steps ? ks + 1 : 0u, fa_h[1], fa_l[1]);
-                mfma_step(ls, fa_h[0], fa_l[0]);
-                ++gs; ++ks;
-            }
-        }
-
-        // column terms of this sub-tile (sums of values over the four lane
-        // groups: 256 * high + low + 128 per k position); the barrier keeps the
-        // previous sub-tile's epilogue reads ahead of these writes
-        __syncthreads();
-        if (sums) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                uint32_t cs = 256u * (uint32_t)csh[j] + (uint32_t)csl[j];
-                cs += (uint32_t)__shfl_xor((int)cs, 16, 64);
-                cs += (uint32_t)__shfl_xor((int)cs, 32, 64);
-                if (lane < 16) colterm_s[wcol + j * 16 + lane] = 128u * (cs + kp128) - kp_term;
-            }
-        }
-
-        // epilogue: two halves of 64 output channels through the LDS tile; thread t
-        // then finishes pixels [c8, c8 + 8) of channels rb and rb + 32 of the half
-        const uint32_t c8 = (tid & 7) * 8, rb = tid >> 3;
-        const uint32_t px0 = p0 + c8;
-        const uint32_t ncol = px0 < bp1 ? (bp1 - px0 < 8u ? bp1 - px0 : 8u) : 0u;
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-            __syncthreads();   // column terms published; the tile is free again
-            if ((wave >> 1) == (uint32_t)half) {
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int j = 0; j < 2; ++j)
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            const uint32_t v = ((uint32_t)hh[i][j][e] << 16) +
-                                               ((uint32_t)mid[i][j][e] << 8) + (uint32_t)ll[i][j][e];
-                            tile[(i * 16 + (lane >> 4) * 4 + e) * kTilePitch + wcol + j * 16 + (lane & 15)] = v;
-                        }
-            }
+            chunk_tables(MULTI ? 4u : g.cpt_last, MULTI ? g.div_cpt4 : g.div_cpt_last, !fast);
             __syncthreads();
+        }
+        if (sub == 0) {
+            if (fast) {
+                a_load8(0, fa_h[0]);
+                if constexpr (NS == 3) a_load8(ks_plus(0, 1), fa_h[1]);
+            } else {
+                a_load(0, fa_h[0], fa_l[0]);
+                if constexpr (NS == 3) a_load(ks_plus(0, 1), fa_h[1], fa_l[1]);
+            }
+        }
+        // patch position of the window origin of this lane's pixel in each column
+        // tile (row (oh - oh_a) * S', column ow * S') and its byte offset
+        uint32_t ppos[4], pbase[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t px = min(p0 + j * 16 + (lane & 15), pe - 1u);   // past the range: any of its pixels
+            const uint32_t oh = fdiv(px, g.div_ow), ow = px - oh * g.OW;
+            ppos[j] = ((oh - oh_a) * g.PW + ow) * g.Sg;
+            pbase[j] = ppos[j] * g.ppitch;
+        }
+        // accumulators: the low set starts at the row and constant terms; each
+        // chunk adds 128 * its window sums (the column term)
+        v4i hh[2][4], mid[2][4], ll[2][4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                hh[i][j] = v4i{0, 0, 0, 0};
+                mid[i][j] = v4i{0, 0, 0, 0};
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    ll[i][j][e] = (int32_t)(rowterm_s[wave * 32 + i * 16 + (lane >> 4) * 4 + e] - (fast ? 0u : kp_term));
+            }
+        auto window_sums = [&]() {
+            uint32_t cs[4] = {0u, 0u, 0u, 0u};
+            for (uint32_t t = 0; t < g.taps; ++t) {
+                const uint32_t tp = tpos[t];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) cs[j] += spos[ppos[j] + tp];
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) ll[i][j][e] = (int32_t)((uint32_t)ll[i][j][e] + 128u * cs[j]);
+        };
+
+        // k loop over the chunks.  Software pipeline: the B fragments of column
+        // tile j + 1 (of the next step's tile 0 after tile 3) are read from the
+        // patch while tile j's MFMAs run, and the A fragments NS - 1 steps ahead
+        // load while a step runs.  FULL: all four column tiles in use.  FAST:
+        // int8 weights, sum w*x = 256 * sum w*x_hi + sum w*x_lo + 128 * sum w
+        // (the last term is in the row term): mid gathers w*x_hi, ll w*x_lo.
+        auto k_loop = [&](auto full, auto fastc) {
+            constexpr bool FULL = decltype(full)::value;
+            constexpr bool FAST = decltype(fastc)::value;
+            v4i bh[2], bl[2];
+            auto b_load = [&](int32_t qo, int j, v4i& h, v4i& l) {
+                // past the chunk's last sub-chunk: the zero slot (the limbs of 0)
+                const uint32_t a = qo >= 0 ? pbase[j] + (uint32_t)qo : g.zslot;
+                h = *reinterpret_cast<const v4i*>(p_hi + a);
+                l = *reinterpret_cast<const v4i*>(p_lo + a);
+            };
+            auto mfma_tile = [&](int j, const v4i& b_h, const v4i& b_l, const v4i (&ah)[2], const v4i (&al)[2]) {
+                if constexpr (FAST) {
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+                        mid[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], b_h, mid[i][j], 0, 0, 0);
+#pragma unroll
+                    for (int i = 0; i < 2; ++i)
+                        ll[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], b_l, ll[i][j], 0, 0, 0);
+                    return;
+                }
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    hh[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], b_h, hh[i][j], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    mid[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], b_l, mid[i][j], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    ll[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], b_l, ll[i][j], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+                    mid[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], b_h, mid[i][j], 0, 0, 0);
+            };
+            // one step with A set S.  FULL: on entry bh[0] / bl[0] hold tile 0 of
+            // this step, and tile 3 prefetches the next step's tile 0; otherwise
+            // the step reads its own tile 0 first.
+            auto step = [&](auto set, uint32_t ls, uint32_t ks, int32_t& qo) {
+                constexpr int S = decltype(set)::value;
+                constexpr int SL = (S + NS - 1) % NS;   // the set of step ks + NS - 1
+                if constexpr (FAST) a_load8(ks_plus(ks, NS - 1), fa_h[SL]);
+                else a_load(ks_plus(ks, NS - 1), fa_h[SL], fa_l[SL]);
+                const int32_t qn = qtab[(ls + 1u) * 4u + (lane >> 4)];   // next step's sub-chunk
+                if constexpr (!FULL) b_load(qo, 0, bh[0], bl[0]);
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (!FULL && (uint32_t)j >= nj) continue;
+                    const int jn = j + 1;
+                    if constexpr (FULL) {
+                        if (jn < 4) b_load(qo, jn, bh[jn & 1], bl[jn & 1]);
+                        else b_load(qn, 0, bh[0], bl[0]);
+                    } else {
+                        if (jn < 4 && (uint32_t)jn < nj) b_load(qo, jn, bh[jn & 1], bl[jn & 1]);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                    mfma_tile(j, bh[j & 1], bl[j & 1], fa_h[S], fa_l[S]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                qo = qn;
+            };
+            uint32_t ks = 0;   // k step within this sub-tile
+            for (uint32_t ch = 0; ch < (MULTI ? g.nchunks : 1u); ++ch) {
+                const uint32_t c0 = ch * 64u;
+                const bool last = ch + 1 == g.nchunks;
+                const uint32_t cpt = last ? g.cpt_last : 4u;
+                const uint32_t nst = (g.taps * cpt + 3u) / 4u;
+                if (MULTI && ch) {   // later chunks: restaged here
+                    __syncthreads();   // every wave is done with the previous chunk's patch
+                    stage_patch(c0, cpt);
+                    __syncthreads();
+                    chunk_tables(cpt, last ? g.div_cpt_last : g.div_cpt4, !FAST);
+                    __syncthreads();
+                }
+                if constexpr (!FAST) window_sums();
+                int32_t qo = qtab[lane >> 4];
+                if constexpr (FULL) b_load(qo, 0, bh[0], bl[0]);
+                using S0 = std::integral_constant<int, 0>;
+                using S1 = std::integral_constant<int, 1>;
+                if constexpr (NS == 3) {   // every sub-tile starts at set 0 (steps % 3 == 0)
+                    for (uint32_t ls = 0; ls < nst; ls += 3, gs += 3, ks += 3) {
+                        step(S0{}, ls, ks, qo);
+                        step(S1{}, ls + 1, ks + 1, qo);
+                        step(std::integral_constant<int, 2>{}, ls + 2, ks + 2, qo);
+                    }
+                } else {
+                    uint32_t ls = 0;
+                    if (gs & 1u) {
+                        step(S1{}, ls, ks, qo);
+                        ++ls; ++gs; ++ks;
+                    }
+                    for (; ls + 2 <= nst; ls += 2, gs += 2, ks += 2) {
+                        step(S0{}, ls, ks, qo);
+                        step(S1{}, ls + 1, ks + 1, qo);
+                    }
+                    if (ls < nst) {
+                        step(S0{}, ls, ks, qo);
+                        ++gs; ++ks;
+                    }
+                }
+            }
+        };
+        if (fast) {
+            if (nj == 4u) k_loop(std::true_type{}, std::true_type{});
+            else k_loop(std::false_type{}, std::true_type{});
+        } else {
+            if (nj == 4u) k_loop(std::true_type{}, std::false_type{});
+            else k_loop(std::false_type{}, std::false_type{});
+        }
+
+        // epilogue, per wave: each 16-channel half of the wave's rows is finished
+        // into its LDS tile (row 4*(lane/16)+e, pixel column of the lane), then
+        // read back as 8-pixel runs: lane -> (row lane/8 + 8t, pixels 8*(lane%8)..)
+        const uint32_t c8 = (lane & 7) * 8;
+        const uint32_t ncol = c8 < pn ? min(8u, pn - c8) : 0u;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if ((uint32_t)j >= nj) continue;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t v = ((uint32_t)hh[i][j][e] << 16) + ((uint32_t)mid[i][j][e] << 8) +
+                                       (uint32_t)ll[i][j][e];
+                    et[((lane >> 4) * 4 + e) * kEpiPitch + j * 16 + (lane & 15)] = q88::acc_to_data(v);
+                }
+            }
+            wave_sync();
             if (ncol) {
-                uint32_t cterm[8];
 #pragma unroll
-                for (int q = 0; q < 8; ++q) cterm[q] = colterm_s[c8 + q];
-#pragma unroll
-                for (int rr = 0; rr < 2; ++rr) {
-                    const uint32_t r = rb + rr * 32;             // row within the half
-                    const uint32_t m = row0 + half * 64 + r;
+                for (int t = 0; t < 2; ++t) {
+                    const uint32_t r = (lane >> 3) + 8 * t;
+                    const uint32_t m = wrow + i * 16 + r;
                     if (m >= g.M) continue;
-                    const uint64_t o = (uint64_t)n * g.y_img + (uint64_t)m * g.P + px0;
-                    int32_t add[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                    const uint64_t o = (uint64_t)n * g.y_img + (uint64_t)m * g.P + p0 + c8;
+                    const v4u tv = *reinterpret_cast<const v4u*>(et + r * kEpiPitch + c8);
+                    int16_t* yp = g.y + o;
+                    const bool vec8 = ncol == 8u && g.vw == 8u;
+                    if (plain && vec8) {
+                        *reinterpret_cast<v4u*>(yp) = tv;
+                        continue;
+                    }
+                    int32_t yv[8];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        yv[2 * q] = (int32_t)(int16_t)(tv[q] & 0xFFFFu);
+                        yv[2 * q + 1] = (int32_t)tv[q] >> 16;
+                    }
                     if (g.epi.add_mode == 1u) {
                         const int16_t* ap = g.epi.add + o;
-                        if (ncol == 8u && g.vw == 8u) {
+                        int32_t add[8];
+                        if (vec8) {
                             const v4u a = *reinterpret_cast<const v4u*>(ap);
 #pragma unroll
                             for (int q = 0; q < 4; ++q) {
@@ -471,18 +637,12 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
 #pragma unroll
                             for (int q = 0; q < 8; ++q) add[q] = (uint32_t)q < ncol ? ap[q] : 0;
                         }
-                    }
-                    const uint32_t rs = rowterm_s[half * 64 + r];
-                    const v4u t0 = *reinterpret_cast<const v4u*>(&tile[r * kTilePitch + c8]);
-                    const v4u t1 = *reinterpret_cast<const v4u*>(&tile[r * kTilePitch + c8 + 4]);
-                    int32_t yv[8];
 #pragma unroll
-                    for (int q = 0; q < 8; ++q) {
-                        const uint32_t v = (q < 4 ? t0[q] : t1[q - 4]) + cterm[q] + rs;
-                        yv[q] = q88::clamp(q88::add(q88::acc_to_data(v), add[q]), lo, hi);
+                        for (int q = 0; q < 8; ++q) yv[q] = q88::add(yv[q], add[q]);
                     }
-                    int16_t* yp = g.y + o;
-                    if (ncol == 8u && g.vw == 8u) {
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) yv[q] = q88::clamp(yv[q], lo, hi);
+                    if (vec8) {
                         *reinterpret_cast<v4u*>(yp) = v4u{pack2(yv[0], yv[1]), pack2(yv[2], yv[3]),
                                                           pack2(yv[4], yv[5]), pack2(yv[6], yv[7])};
                     } else {
@@ -492,6 +652,7 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
                     }
                 }
             }
+            wave_sync();   // the tile's reads are done before the next half overwrites it
         }
     }
 }
@@ -502,6 +663,26 @@ uint32_t gcd(uint32_t a, uint32_t b) {
     while (b) { const uint32_t t = a % b; a = b; b = t; }
     return a;
 }
+
+// Compute units of the current device (256 on MI355X), cached per device.
+uint32_t cu_count() {
+    static std::atomic<int> cache[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+        (void)hipGetLastError();
+        return 256u;
+    }
+    int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return (uint32_t)c;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) {
+        (void)hipGetLastError();
+        c = 256;
+    }
+    cache[dev].store(c, std::memory_order_relaxed);
+    return (uint32_t)c;
+}
+
+constexpr uint64_t kPgLdsMax = 78u * 1024u;   // dynamic LDS per block: two blocks per CU
 
 }  // namespace
 
@@ -539,38 +720,56 @@ int cm_conv_pgemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias
     const uint32_t nchunks = (in_ch + 63) / 64;
     const uint32_t cpt_max = nchunks > 1 ? 4u : (in_ch + 15) / 16;
     const uint32_t ppitch = cpt_max % 2 ? cpt_max * 16 : cpt_max * 16 + 16;   // odd multiple of 16
-    const uint64_t tile_bytes = 64ull * kTilePitch * 4;
-    // Band of R output rows per block: the most rows (up to 8) that keep two
-    // blocks per CU in LDS and the grid at >= 400 blocks (else >= 200); sub-tiles
-    // of 64 pixels must be mostly full (>= 3/4 of the lanes over the whole band)
-    uint32_t R = 0;
-    uint64_t best_lds = 0;
-    for (uint32_t min_blocks : {400u, 200u}) {
-        for (uint32_t r = 1; r <= 8 && r <= out_h; ++r) {
-            const uint64_t px = (uint64_t)r * out_w;
-            const uint64_t bands = (out_h + r - 1) / r;
-            const uint64_t blocks = bands * batch * mtiles;
-            const uint64_t prows = (uint64_t)(r - 1) * Sg + (uint64_t)(kh - 1) * Dg + 1;
-            const uint64_t lds = 2 * (prows * PW * ppitch + 16) + tile_bytes;
-            const bool fill = px * 4 >= ((px + PBN - 1) / PBN) * PBN * 3;
-            if (blocks < min_blocks || lds > 76u * 1024u || !fill) continue;
-            R = r;
-            best_lds = lds;
-        }
-        if (R) break;
-    }
-    if (R == 0) return 1;
-    const uint32_t bands = (out_h + R - 1) / R;
-    const uint64_t blocks = (uint64_t)bands * batch * mtiles;
-    if (blocks > 0x7FFFFFFFull) return 1;
-    const uint32_t prmax = (R - 1) * Sg + (kh - 1) * Dg + 1;
-    const uint64_t zslot = (uint64_t)prmax * PW * ppitch;
-    const uint64_t p_plane = zslot + 16;
-    const uint64_t lds = best_lds;
+    const uint32_t khspan = (kh - 1) * Dg + 1;
     const uint32_t last_cpt = (in_ch - (nchunks - 1) * 64 + 15) / 16;
     const uint32_t steps = (nchunks - 1) * taps + (taps * last_cpt + 3) / 4;
-    const uint64_t pk_bytes = (uint64_t)mtiles * steps * kPackTile;
-    const uint64_t need = pk_bytes + 4ull * mtiles * BM;
+    auto a16 = [](uint64_t v) { return (v + 15) & ~15ull; };
+    auto layout = [&](uint64_t prows, uint64_t& spos_off, uint64_t& epi_off) {
+        const uint64_t p_plane = prows * PW * ppitch + 16;
+        spos_off = a16(2 * p_plane);
+        epi_off = spos_off + a16(prows * PW * 4);
+        return epi_off + 4ull * kEpiBytes;
+    };
+    // Pixels per block L (a multiple of 16): the fewest modelled cycles per CU,
+    // with blocks dealt over the CUs two at a time.  A 16-pixel column tile costs
+    // 128 MFMA cycles per k step; staging a patch row costs about one cycle per
+    // 16 bytes loaded, once per block pair (the second block's staging overlaps
+    // the first one's MFMAs) and once per sub-tile and chunk with several chunks;
+    // a lone block per CU keeps one wave per SIMD and runs at about 70%.  With
+    // fewer blocks than CUs at every L the shape goes to another path.
+    const uint64_t cus = cu_count();
+    const uint64_t c_tile = 128ull * steps;
+    const uint64_t c_row = (uint64_t)PW * cpt_max * 2;
+    uint32_t L = 0;
+    uint64_t best = ~0ull, prows = 0;
+    const uint64_t lcap = nchunks > 1 ? 128u : 512u;
+    for (uint64_t l = 16; l <= lcap; l += 16) {
+        const uint64_t rows = std::min<uint64_t>(out_h, (l - 1 + out_w - 1) / out_w + 1);
+        const uint64_t pr = (rows - 1) * Sg + khspan;
+        uint64_t so, eo;
+        if (layout(pr, so, eo) > kPgLdsMax) break;   // grows with l
+        const uint64_t rpi = (P + l - 1) / l;
+        const uint64_t blocks = rpi * batch * mtiles;
+        if (blocks > 0x7FFFFFFFull) continue;
+        if (blocks < cus) break;   // fewer blocks than CUs: another path suits better
+        const uint64_t k = (blocks + cus - 1) / cus;
+        const uint64_t u = l / 16;
+        const uint64_t stage = pr * c_row * (nchunks > 1 ? nchunks * ((l + PBN - 1) / PBN) : 1u);
+        uint64_t t = k * u * c_tile + ((k + 1) / 2) * stage;
+        if (k == 1) t = t * 10 / 7;
+        if (t < best) { best = t; L = (uint32_t)l; prows = pr; }
+        if (l >= P) break;
+    }
+    if (L == 0) return 1;
+    uint64_t spos_off = 0, epi_off = 0;
+    const uint64_t lds = layout(prows, spos_off, epi_off);
+    const uint32_t rpi = (uint32_t)((P + L - 1) / L);
+    const uint64_t zslot = prows * PW * ppitch;
+    const uint64_t p_plane = zslot + 16;
+    // workspace: limb planes, int8 plane, row sums, int8 flags
+    const uint64_t pk_limb = (uint64_t)mtiles * steps * kPackTile;
+    const uint64_t pk_bytes = pk_limb + (uint64_t)mtiles * steps * kPackTile8;
+    const uint64_t need = pk_bytes + 8ull * mtiles * BM;
     if (pk_bytes >= 0x80000000ull) return 1;
     if (lc.need) {
         if (need > *lc.need) *lc.need = need;
@@ -580,55 +779,58 @@ int cm_conv_pgemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias
 
     uint8_t* wpk = static_cast<uint8_t*>(lc.ws);
     uint32_t* wsum = reinterpret_cast<uint32_t*>(wpk + pk_bytes);
-    PackArgs pa{w, wpk, wsum, in_ch, out_ch, taps, nchunks, steps, taps};
+    uint32_t* wfit = wsum + mtiles * BM;
+    PackArgs pa{w, wpk, wpk + pk_limb, wsum, wfit, in_ch, out_ch, taps, nchunks, steps, taps};
     hipLaunchKernelGGL(conv_wpack, dim3(mtiles * BM), dim3(256), 0, lc.s, pa);
     int rc = cm_check_launch("conv_wpack");
     if (rc) return rc;
 
     PgArgs g{};
-    g.x = x; g.wpk = wpk; g.wsum = wsum; g.bias = bias; g.y = y;
+    g.x = x; g.wpk = wpk; g.wsum = wsum; g.wfit = wfit; g.bias = bias; g.y = y;
     g.C = in_ch; g.H = in_h; g.W = in_w; g.M = out_ch; g.OH = out_h; g.OW = out_w; g.P = (uint32_t)P;
     g.KW = kw; g.taps = taps; g.S = sh; g.Sg = Sg; g.Dg = Dg; g.g = gg; g.pt = pad_top; g.pl = pad_left;
+    g.khspan = khspan;
     g.nchunks = nchunks; g.steps = steps;
     g.PW = PW; g.ppitch = ppitch; g.p_plane = (uint32_t)p_plane; g.zslot = (uint32_t)zslot;
+    g.spos_off = (uint32_t)spos_off; g.epi_off = (uint32_t)epi_off;
     g.lhc = lhc; g.wr = wr; g.nh = nh;
     g.cpt_last = last_cpt;
-    g.R = R; g.bands = bands;
-    g.prows = prmax;
-    g.npos = prmax * PW;
-    g.div_bands = make_fastdiv(bands);
+    g.L = L; g.rpi = rpi; g.rpi_n = rpi * batch;
+    g.div_nbm = make_fastdiv(rpi * batch);
+    g.prows = (uint32_t)prows;
+    g.npos = (uint32_t)prows * PW;
+    g.div_rpi = make_fastdiv(rpi);
     g.div_ow = make_fastdiv(out_w);
     g.div_npos = make_fastdiv(g.npos);
     g.div_pw = make_fastdiv(PW);
     g.div_nv = make_fastdiv(in_w / 8 ? in_w / 8 : 1);
-    g.div_prows = make_fastdiv(prmax);
+    g.div_prows = make_fastdiv((uint32_t)prows);
     g.div_nh = make_fastdiv(nh ? nh : 1);
     g.div_kw = make_fastdiv(kw);
     g.div_cpt4 = make_fastdiv(4);
     g.div_cpt_last = make_fastdiv(last_cpt);
     g.x_img_bytes = (uint32_t)(2 * x_img);
     g.pk_bytes = (uint32_t)pk_bytes;
+    g.pk8_off = (uint32_t)pk_limb;
     g.x_img = x_img;
     g.y_img = (uint64_t)out_ch * P;
     g.epi = ea;
     // 16-byte output accesses: every run of 8 pixels starts 16-byte aligned
-    // (bands start at multiples of R * OW pixels, sub-tiles at multiples of 64)
-    g.vw = P % 8 == 0 && (uint64_t)R * out_w % 8 == 0 && aligned(y, 16) &&
-                   (ea.add_mode != 1u || aligned(ea.add, 16))
-               ? 8u
-               : 1u;
+    // (ranges start at multiples of L, sub-tiles at multiples of 64 pixels)
+    g.vw = P % 8 == 0 && aligned(y, 16) && (ea.add_mode != 1u || aligned(ea.add, 16)) ? 8u : 1u;
     const void* k = nullptr;
-#define CM_PG_PICK(B, M) (vec == 1 ? (const void*)conv_pgemm<B, 1, M> \
-                          : vec == 2 ? (const void*)conv_pgemm<B, 2, M> : (const void*)conv_pgemm<B, 0, M>)
-    if (nchunks > 1) k = bias ? CM_PG_PICK(true, true) : CM_PG_PICK(false, true);
-    else k = bias ? CM_PG_PICK(true, false) : CM_PG_PICK(false, false);
+#define CM_PG_PICK(B, M, NS) (vec == 1 ? (const void*)conv_pgemm<B, 1, M, NS> \
+                              : vec == 2 ? (const void*)conv_pgemm<B, 2, M, NS> : (const void*)conv_pgemm<B, 0, M, NS>)
+    if (nchunks > 1) k = bias ? CM_PG_PICK(true, true, 2) : CM_PG_PICK(false, true, 2);
+    else if (steps % 3 == 0) k = bias ? CM_PG_PICK(true, false, 3) : CM_PG_PICK(false, false, 3);
+    else k = bias ? CM_PG_PICK(true, false, 2) : CM_PG_PICK(false, false, 2);
 #undef CM_PG_PICK
     if (lds > 65536u &&
         hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
         (void)hipGetLastError();
         return cm_set_error(CM_ERR_HIP, "conv_pgemm: %llu bytes of LDS refused", (unsigned long long)lds);
     }
-    const dim3 grid((uint32_t)(bands * batch), mtiles);
+    const dim3 grid(rpi * batch * mtiles);
     void* kargs[] = {&g};
     const hipError_t e = hipLaunchKernel(k, grid, dim3(kPgThreads), kargs, (size_t)lds, lc.s);
     if (e != hipSuccess) return cm_set_error(CM_ERR_HIP, "conv_pgemm: %s", hipGetErrorString(e));

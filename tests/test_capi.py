@@ -106,8 +106,8 @@ def test_workspace_size_queries():
     conv = lib.cm_conv_workspace_size(16, 160, 7, 7, 160, 7, 7, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0)
     assert conv > 0 and conv % (160 * 784 * 4) == 0
     # conv A of the benchmark block: the patch-GEMM path, whose workspace holds the
-    # weights as int8 limb planes (9 k steps x 128 rows x 64 k x 2) and 128 row sums;
-    # depthwise never uses a workspace
+    # weights as two int8 limb planes and one int8 plane (9 k steps x 128 rows x 64 k
+    # x 3), 128 row sums and 128 int8 flags; depthwise never uses a workspace
     assert lib.cm_conv_workspace_size(32, 64, 56, 56, 128, 56, 56, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0) == \
-        9 * 128 * 64 * 2 + 128 * 4
+        9 * 128 * 64 * 3 + 128 * 8
     assert lib.cm_conv_workspace_size(1, 64, 56, 56, 64, 56, 56, 3, 3, 1, 1, 1, 1, 1, 1, 0, 1) == 0

@@ -137,11 +137,12 @@ def test_config4_full_size(case, ws):
 
 
 def pgemm_need(C, M, kh, kw):
-    """Workspace of the patch-GEMM path: packed weight limb planes (128 rows x 64 k x 2
-    per row tile and k step) and one uint32 row sum per padded row."""
+    """Workspace of the patch-GEMM path: packed weights (128 rows x 64 k as two limb
+    planes and one int8 plane per row tile and k step), and one uint32 row sum and
+    one int8 flag per padded row."""
     taps, mt, nch = kh * kw, -(-M // 128), -(-C // 64)
     steps = (nch - 1) * taps + (taps * -(-(C - (nch - 1) * 64) // 16) + 3) // 4
-    return mt * steps * 2 * 128 * 64 + 4 * 128 * mt
+    return mt * steps * 3 * 128 * 64 + 8 * 128 * mt
 
 
 PGEMM = [
@@ -183,6 +184,40 @@ def test_patch_gemm_full_range(geom):
         exp = np.clip(want.astype(np.int32) + add, -32768, 32767)
         exp = np.clip(exp, 0, 32767 if act == K.ACT_RELU else 1536)
         np.testing.assert_array_equal(host(y2).astype(np.int32), exp)
+
+
+@pytest.mark.parametrize("geom", PGEMM, ids=[str(g) for g in PGEMM])
+@pytest.mark.parametrize("mix", ["all", "first", "last"])
+def test_patch_gemm_int8_weights(geom, mix):
+    """Weights in [-128, 127] take the two-product path per 128-row tile: every
+    tile ("all"), or with one out-of-range weight in the first or last output
+    channel (that row's tile takes the four-product path).  Full-range inputs,
+    bias, fused Add and ReLU."""
+    N, C, H, W, M, kh, kw, s, d, p = geom
+    OH, OW = (H + 2 * p - d * (kh - 1) - 1) // s + 1, (W + 2 * p - d * (kw - 1) - 1) // s + 1
+    args = (N, C, H, W, M, OH, OW, kh, kw, s, s, d, d, p, p, 1, 0)
+    assert K.conv_workspace_size(*args) == pgemm_need(C, M, kh, kw), "expected the patch-GEMM path"
+    say(f"conv patch gemm int8 weights {geom} {mix}")
+    g = wl.rng(834, *geom, len(mix))
+    x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
+    w = g.integers(-128, 128, M * C * kh * kw, dtype=np.int16)
+    if mix == "first":
+        w[int(g.integers(0, C * kh * kw))] = -129
+    elif mix == "last":
+        w[(M - 1) * C * kh * kw + int(g.integers(0, C * kh * kw))] = 128
+    b = g.integers(-32768, 32768, M, dtype=np.int16)
+    add = g.integers(-32768, 32768, N * M * OH * OW, dtype=np.int16)
+    want = np.zeros(N * M * OH * OW, np.int16)
+    oracle.set_threads(oracle_threads())
+    oracle.conv(x, w, b, want, *args, threads=True)
+    ws = workspace_for(*args)
+    y = empty_dev(want.size)
+    K.ConvKernel(dev(x), dev(w), dev(b), y, *args, workspace=ws)
+    np.testing.assert_array_equal(host(y), want)
+    y2 = empty_dev(want.size)
+    K.ConvKernel(dev(x), dev(w), dev(b), y2, *args, add=dev(add), act=K.ACT_RELU, workspace=ws)
+    exp = np.clip(np.clip(want.astype(np.int32) + add, -32768, 32767), 0, 32767)
+    np.testing.assert_array_equal(host(y2).astype(np.int32), exp)
 
 
 @pytest.mark.parametrize("seed", range(16))
