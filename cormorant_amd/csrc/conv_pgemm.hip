@@ -70,9 +70,10 @@ struct PgArgs {
     uint32_t zslot;              // byte offset in each plane of 16 bytes holding the limbs of 0
     uint32_t spos_off, epi_off;  // LDS byte offsets of the position sums and the epilogue tiles
     uint32_t lhc, wr, nh;        // padding columns: left [0, lhc), right [wr, wr + nh - lhc)
+    uint32_t stage_g;            // 16-byte staging: (row, column group) pair groups per block
     uint32_t cpt_last;           // 16-channel groups of the last chunk
     uint32_t L, rpi, rpi_n;      // output pixels per block; ranges per image; ranges per row tile
-    FastDiv div_nbm, div_rpi, div_ow, div_npos, div_pw, div_nv, div_prows, div_nh, div_kw, div_cpt4, div_cpt_last;
+    FastDiv div_npr, div_nbm, div_rpi, div_ow, div_npos, div_pw, div_nv, div_prows, div_nh, div_kw, div_cpt4, div_cpt_last;
     uint32_t vw;                 // output / Add access width in elements (8 or 1)
     uint32_t x_img_bytes, pk_bytes;   // pk_bytes: both packed layouts (limb planes, then int8)
     uint32_t pk8_off;            // byte offset of the int8 plane
@@ -302,33 +303,42 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
             // col = (iw + pl) / VEC for iw = pl (mod VEC).  Input rows are 16-byte
             // aligned (W % 8 == 0), and patch rows are wide enough for all of
             // them (PW >= lh + W / VEC), so no write needs a condition.
+            // Each thread takes one (patch row r, 8-column group vv) pair and every
+            // G-th channel quad from g0 (G = pair groups that fit the block), so a
+            // task's addresses are the previous task's plus constant steps.
             const uint32_t nv = g.W / 8u;
-            const uint32_t ntask = ncq * g.prows * nv;
+            const uint32_t npr = g.prows * nv;
+            const uint32_t G = g.stage_g;
             const uint32_t lh = (g.pl + VEC - 1u) / VEC;   // patch column of the first input column used
-            for (uint32_t b0 = 0; b0 < ntask; b0 += kPgThreads * kPB) {
+            const uint32_t plane2 = hw_in * 2u;             // bytes of one input channel plane
+            const uint32_t src_step = G * 4u * plane2, dst_step = G * 4u;
+            for (uint32_t v = tid; v < G * npr; v += kPgThreads) {
+                const uint32_t g0 = fdiv(v, g.div_npr), pr = v - g0 * npr;
+                const uint32_t r = fdiv(pr, g.div_nv), vv = pr - r * nv;
+                if (r >= prows_b) continue;
+                const int32_t ih = ih_first + (int32_t)(r * VEC);
+                const uint32_t okr = (uint32_t)((uint32_t)ih < g.H);
+                uint32_t src = ((c0 + g0 * 4u) * hw_in + (uint32_t)ih * g.W + vv * 8u) * 2u;
+                uint32_t dst = (r * g.PW + vv * (8u / VEC) + lh) * g.ppitch + g0 * 4u;
+                uint32_t c = c0 + g0 * 4u;
+                for (uint32_t cq = g0; cq < ncq; cq += kPB * G) {
                 v4u d[kPB][4];
-                uint32_t dst0[kPB];
 #pragma unroll
                 for (int u = 0; u < kPB; ++u) {
-                    const uint32_t e = b0 + u * kPgThreads + tid;
-                    const uint32_t cqr = fdiv(e, g.div_nv), vv = e - cqr * nv;
-                    const uint32_t cq = fdiv(cqr, g.div_prows), r = cqr - cq * g.prows;
-                    const int32_t ih = ih_first + (int32_t)(r * VEC);
-                    const uint32_t live = (uint32_t)(e < ntask) & (uint32_t)(r < prows_b);
-                    const uint32_t okr = live & (uint32_t)((uint32_t)ih < g.H);
-                    const uint32_t c = c0 + cq * 4u;
-                    const uint32_t base = (c * hw_in + (uint32_t)ih * g.W + vv * 8u) * 2u;
-                    dst0[u] = live ? (r * g.PW + vv * (8u / VEC) + lh) * g.ppitch + cq * 4u : 0xFFFFFFFFu;
+                    const uint32_t cu = c + u * 4u * G;
 #pragma unroll
                     for (int jj = 0; jj < 4; ++jj) {
-                        const uint32_t ok = okr & (uint32_t)(c + jj < g.C);
-                        const uint32_t off = ((base + jj * hw_in * 2u) & 0x7FFFFFFFu) | ((ok ^ 1u) << 31);
+                        const uint32_t ok = okr & (uint32_t)(cu + jj < g.C) & (uint32_t)(cq + u * G < ncq);
+                        const uint32_t off = ((src + u * src_step + jj * plane2) & 0x7FFFFFFFu) | ((ok ^ 1u) << 31);
                         d[u][jj] = __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0);
                     }
                 }
+                uint32_t dst0[kPB];
+#pragma unroll
+                for (int u = 0; u < kPB; ++u) dst0[u] = dst + u * dst_step;
 #pragma unroll
                 for (int u = 0; u < kPB; ++u) {
-                    if (dst0[u] == 0xFFFFFFFFu) continue;
+                    if (cq + u * G >= ncq) continue;
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {   // dword k holds input columns 8v+2k, 8v+2k+1
                         const uint32_t d0 = d[u][0][k], d1 = d[u][1][k], d2 = d[u][2][k], d3 = d[u][3][k];
@@ -346,6 +356,10 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
                                 __builtin_amdgcn_perm(u23, u01, sel) ^ 0x80808080u;
                         }
                     }
+                }
+                src += kPB * src_step;
+                dst += kPB * dst_step;
+                c += kPB * 4u * G;
                 }
             }
             // padding columns (input columns outside the row) that a window reads:
@@ -804,6 +818,11 @@ int cm_conv_pgemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias
     g.div_npos = make_fastdiv(g.npos);
     g.div_pw = make_fastdiv(PW);
     g.div_nv = make_fastdiv(in_w / 8 ? in_w / 8 : 1);
+    {
+        const uint32_t npr = (uint32_t)prows * (in_w / 8 ? in_w / 8 : 1);
+        g.stage_g = npr < kPgThreads ? kPgThreads / npr : 1u;
+        g.div_npr = make_fastdiv(npr);
+    }
     g.div_prows = make_fastdiv((uint32_t)prows);
     g.div_nh = make_fastdiv(nh ? nh : 1);
     g.div_kw = make_fastdiv(kw);
