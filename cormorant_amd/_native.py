@@ -21,7 +21,7 @@ EXPORTS = (
     "cm_run_pool", "cm_set_stream", "cm_get_stream", "cm_sync", "cm_last_error", "cm_version",
     "cm_selftest_div", "cm_selftest_finalize", "cm_matmul_ex", "cm_conv_ex",
     "cm_matmul_workspace_size", "cm_conv_workspace_size", "cm_set_workspace",
-    "cm_matmul_noalloc",
+    "cm_matmul_noalloc", "cm_conv_packed_size", "cm_conv_pack", "cm_conv_packed_ex",
 )
 
 CM_OK = 0
@@ -109,6 +109,9 @@ _SIGS = {
     "cm_conv_workspace_size": (ctypes.c_size_t, [_u32] * 17),
     "cm_set_workspace": (_i, [_vp, ctypes.c_size_t]),
     "cm_matmul_noalloc": (_i, [_vp, _vp, _vp] + [_u32] * 7 + [ctypes.POINTER(CmEpilogue), _vp]),
+    "cm_conv_packed_size": (ctypes.c_size_t, [_u32] * 17),
+    "cm_conv_pack": (_i, [_vp] + [_u32] * 17 + [_vp, ctypes.c_size_t, _vp]),
+    "cm_conv_packed_ex": (_i, [_vp, _vp, _vp, _vp] + [_u32] * 17 + [ctypes.POINTER(CmEpilogue), _vp]),
 }
 
 _lib = None

@@ -190,6 +190,53 @@ size_t cm_conv_workspace_size(uint32_t batch, uint32_t in_ch, uint32_t in_h, uin
     return need;
 }
 
+size_t cm_conv_packed_size(uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                           uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh,
+                           uint32_t kw, uint32_t stride_h, uint32_t stride_w,
+                           uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
+                           uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise) {
+    (void)has_bias;
+    if ((uint64_t)batch * out_ch * out_h * out_w == 0) return 0;
+    return cm_conv_packed_bytes(batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h,
+                                stride_w, dilation_h, dilation_w, pad_top, pad_left, is_depthwise);
+}
+
+int cm_conv_pack(const int16_t* weight, uint32_t batch, uint32_t in_ch, uint32_t in_h,
+                 uint32_t in_w, uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh,
+                 uint32_t kw, uint32_t stride_h, uint32_t stride_w, uint32_t dilation_h,
+                 uint32_t dilation_w, uint32_t pad_top, uint32_t pad_left, uint32_t has_bias,
+                 uint32_t is_depthwise, void* packed, size_t packed_bytes, hipStream_t stream) {
+    if (!weight || !packed) return cm_set_error(CM_ERR_INVALID, "conv pack: null weight or packed");
+    if (cm_conv_packed_size(batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h,
+                            stride_w, dilation_h, dilation_w, pad_top, pad_left, has_bias,
+                            is_depthwise) == 0)
+        return cm_set_error(CM_ERR_INVALID, "conv pack: the shape does not take the patch-GEMM path");
+    return cm_conv_pgemm_pack(weight, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw,
+                              stride_h, stride_w, dilation_h, dilation_w, pad_top, pad_left, packed,
+                              packed_bytes, pick(stream));
+}
+
+int cm_conv_packed_ex(const int16_t* x, const void* packed, const int16_t* bias, int16_t* y,
+                      uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                      uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
+                      uint32_t stride_h, uint32_t stride_w, uint32_t dilation_h,
+                      uint32_t dilation_w, uint32_t pad_top, uint32_t pad_left,
+                      uint32_t has_bias, uint32_t is_depthwise, const cm_epilogue_t* epi,
+                      hipStream_t stream) {
+    if ((uint64_t)batch * out_ch * out_h * out_w == 0) return CM_OK;
+    if (!x || !packed || !y) return cm_set_error(CM_ERR_INVALID, "conv packed: null x, packed or y");
+    if (has_bias && !bias) return cm_set_error(CM_ERR_INVALID, "conv packed: has_bias with null bias");
+    const int rc = check_epilogue(epi, false, "conv");
+    if (rc) return rc;
+    if (cm_conv_packed_size(batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h,
+                            stride_w, dilation_h, dilation_w, pad_top, pad_left, has_bias,
+                            is_depthwise) == 0)
+        return cm_set_error(CM_ERR_INVALID, "conv packed: the shape does not take the patch-GEMM path");
+    return cm_conv_pgemm_run_packed(x, packed, has_bias ? bias : nullptr, y, batch, in_ch, in_h, in_w,
+                                    out_ch, out_h, out_w, kh, kw, stride_h, stride_w, dilation_h,
+                                    dilation_w, pad_top, pad_left, epi, pick(stream));
+}
+
 int cm_pool(const int16_t* x, int16_t* y, uint32_t batch, uint32_t channels, uint32_t in_h,
             uint32_t in_w, uint32_t out_h, uint32_t out_w, uint32_t pool_h, uint32_t pool_w,
             uint32_t stride_h, uint32_t stride_w, uint32_t pad_top, uint32_t pad_left,

@@ -97,6 +97,26 @@ int cm_finalize_sweep_launch(uint32_t mode, uint32_t lo, uint32_t count, uint32_
 int cm_matmul_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
                      uint32_t m, uint32_t batch, uint32_t a_bs, uint32_t b_bs, uint32_t c_bs,
                      const cm_epilogue_t* epi, const LaunchCtx& lc);
+// Convolution weights packed once for the patch-GEMM path (conv.hip,
+// conv_pgemm.hip): the packed bytes for a shape (0 when cm_conv would not run
+// it on that path), the pack, and a call that runs with packed weights.
+size_t cm_conv_packed_bytes(uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                            uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh,
+                            uint32_t kw, uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw,
+                            uint32_t pad_top, uint32_t pad_left, uint32_t is_dw);
+size_t cm_conv_pgemm_packed_bytes(uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                                  uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh,
+                                  uint32_t kw, uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw,
+                                  uint32_t pad_top, uint32_t pad_left);
+int cm_conv_pgemm_pack(const int16_t* w, uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                       uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
+                       uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
+                       uint32_t pad_left, void* dst, size_t bytes, hipStream_t s);
+int cm_conv_pgemm_run_packed(const int16_t* x, const void* packed, const int16_t* bias, int16_t* y,
+                             uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                             uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
+                             uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
+                             uint32_t pad_left, const cm_epilogue_t* epi, hipStream_t s);
 // 3x3 convolution through an LDS-staged input patch (conv_patch.hip); returns
 // 1, launching nothing, for shapes it does not take.
 int cm_conv_patch_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,

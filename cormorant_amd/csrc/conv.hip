@@ -2,11 +2,11 @@
 //
 // Dispatch (standard convolutions, first match):
 //   * few output channels, K <= 32, many pixels: direct vector-ALU kernel;
+//   * windows of >= 2 taps, the same stride and dilation on both axes, when the
+//     caller's workspace holds the packed weights: conv_pgemm (input patch in
+//     LDS, weights pre-split into limb planes; conv_pgemm.hip);
 //   * 3x3, <= 64 channels in and out, stride 1 or 2: conv_patch (input patch and
 //     all weights in LDS);
-//   * windows of >= 2 taps over tiles of 128 pixels that fill the GPU, when the
-//     caller's workspace holds the packed weights: conv_pgemm (input patch in
-//     LDS, weights pre-split into limb planes);
 //   * 1x1 / stride 1 / no padding, planes that fill 128-column tiles: batched
 //     GEMM Y[n] = W[out_ch][in_ch] x X[n][in_ch][h*w] on the int8-limb MFMA core;
 //   * any other: implicit GEMM on the same core, im2col gathered straight from
@@ -268,6 +268,38 @@ int launch_direct(const DirArgs& g, hipStream_t s) {
 
 }  // namespace
 
+// The patch GEMM's 16-byte row staging: rows of whole 16-byte groups, x
+// aligned, and gcd(stride, dilation) 1 or 2.
+bool pgemm_row_loads(const int16_t* x, uint32_t in_w, uint32_t sh, uint32_t dh) {
+    uint32_t a = sh, c = dh;
+    while (c) { const uint32_t t = a % c; a = c; c = t; }
+    return in_w % 8 == 0 && ((uintptr_t)x & 15) == 0 && (a == 1 || a == 2);
+}
+
+size_t cm_conv_packed_bytes(uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                            uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh,
+                            uint32_t kw, uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw,
+                            uint32_t pad_top, uint32_t pad_left, uint32_t is_dw) {
+    // the dispatch below: the patch-GEMM path comes after the direct one and
+    // takes windows of two or more taps
+    if (is_dw || kh * kw < 2) return 0;
+    const uint64_t K = (uint64_t)in_ch * kh * kw;
+    if (direct_channels(K, out_ch, kh * kw, (uint64_t)batch * out_h * out_w,
+                        2ull * in_ch * in_h * in_w * batch))
+        return 0;
+    alignas(16) static const int16_t probe[8] = {};   // an aligned stand-in, never read
+    if (!pgemm_row_loads(probe, in_w, sh, dh)) {
+        size_t need = 0;
+        const LaunchCtx lc{nullptr, nullptr, 0, &need};
+        if (cm_conv_patch_launch(probe, probe, probe, const_cast<int16_t*>(probe), batch, in_ch, in_h,
+                                 in_w, out_ch, out_h, out_w, kh, kw, sh, sw, dh, dw, pad_top, pad_left,
+                                 nullptr, lc) == CM_OK)
+            return 0;
+    }
+    return cm_conv_pgemm_packed_bytes(batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, sh, sw,
+                                      dh, dw, pad_top, pad_left);
+}
+
 int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
                    uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
                    uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
@@ -314,14 +346,26 @@ int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int1
             default: return launch_direct<32>(g, s);
         }
     }
-    {   // 3x3 with <= 64 channels in and out: all weights staged per block
-        const int rc = cm_conv_patch_launch(x, w, b, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w,
-                                            kh, kw, sh, sw, dh, dw, pad_top, pad_left, epi, lc);
-        if (rc != 1) return rc;
-    }
-    if (kh * kw > 1) {   // patch GEMM: needs the caller's workspace for the packed weights
+    // The patch GEMM (it needs the caller's workspace for the packed weights)
+    // stages input rows 16 bytes at a time when they allow it; where they do
+    // not, conv_patch comes first when it takes the shape
+    bool patch_tried = false;
+    auto try_patch = [&]() {
+        patch_tried = true;
+        return cm_conv_patch_launch(x, w, b, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw,
+                                    sh, sw, dh, dw, pad_top, pad_left, epi, lc);
+    };
+    if (kh * kw > 1) {
+        if (!pgemm_row_loads(x, in_w, sh, dh)) {
+            const int rc = try_patch();
+            if (rc != 1) return rc;
+        }
         const int rc = cm_conv_pgemm_launch(x, w, b, y, batch, in_ch, in_h, in_w, out_ch, out_h,
                                             out_w, kh, kw, sh, sw, dh, dw, pad_top, pad_left, epi, lc);
+        if (rc != 1) return rc;
+    }
+    if (!patch_tried) {   // 3x3 with <= 64 channels in and out: all weights staged per block
+        const int rc = try_patch();
         if (rc != 1) return rc;
     }
     // 1x1 / stride 1 / no padding as one GEMM per image, when an image's

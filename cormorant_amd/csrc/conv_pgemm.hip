@@ -48,9 +48,7 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
-constexpr int BM = 128;
-constexpr uint32_t kPackTile = 2u * BM * 64u; // packed bytes per (row tile, step): hi then lo
-constexpr uint32_t kPackTile8 = BM * 64u;     // int8 plane bytes per (row tile, step)
+constexpr uint32_t kMaxTB = 128;   // output channels per row tile: 32, 64 or 128
 constexpr int kMaxQ = 256;                    // q table entries (taps * 4 <= 256)
 
 struct PgArgs {
@@ -106,11 +104,13 @@ struct PackArgs {
     uint32_t* wsum;
     uint32_t* wfit;
     uint32_t C, M, taps, nchunks, steps, steps_full;   // steps_full = taps (a full chunk)
+    uint32_t tb;                                         // rows per row tile
 };
 
 __global__ __launch_bounds__(256) void conv_wpack(PackArgs a) {
     const uint32_t m = blockIdx.x;   // 0 .. Mpad-1
-    const uint32_t mt = m / BM, r = m % BM;
+    const uint32_t mt = m / a.tb, r = m % a.tb;
+    const uint32_t tile = 2u * a.tb * 64u, tile8 = a.tb * 64u;   // bytes per (row tile, step)
     const bool mok = m < a.M;
     const int16_t* wrow = a.w + (uint64_t)(mok ? m : 0u) * a.C * a.taps;
     uint32_t sum = 0, fit = 1u;
@@ -136,10 +136,10 @@ __global__ __launch_bounds__(256) void conv_wpack(PackArgs a) {
             lw |= lo_byte(v) << (8 * j);
             bw |= ((uint32_t)v & 0xFFu) << (8 * j);
         }
-        uint8_t* dst = a.wpk + (uint64_t)(mt * a.steps + gs) * kPackTile + r * 64u + wd * 4u;
+        uint8_t* dst = a.wpk + (uint64_t)(mt * a.steps + gs) * tile + r * 64u + wd * 4u;
         *reinterpret_cast<uint32_t*>(dst) = hw;
-        *reinterpret_cast<uint32_t*>(dst + BM * 64u) = lw;
-        *reinterpret_cast<uint32_t*>(a.wpk8 + (uint64_t)(mt * a.steps + gs) * kPackTile8 + r * 64u + wd * 4u) = bw;
+        *reinterpret_cast<uint32_t*>(dst + a.tb * 64u) = lw;
+        *reinterpret_cast<uint32_t*>(a.wpk8 + (uint64_t)(mt * a.steps + gs) * tile8 + r * 64u + wd * 4u) = bw;
     }
     // row sum (every real weight once; padding adds 0)
     __shared__ uint32_t red[256];
@@ -155,11 +155,12 @@ __global__ __launch_bounds__(256) void conv_wpack(PackArgs a) {
 }
 
 // ------------------------------------------------------------- main kernel --
-// Block: 256 threads = 4 waves, 128 output channels (wave w: channels 32w ..
-// 32w+31) of one range of L consecutive output pixels of one image, computed
-// in sub-tiles of 64 pixels; wave tile 32 channels x 64 pixels (2 x 4 MFMA
-// 16x16x64 tiles, three accumulator sets).  Every wave reads its own weight
-// rows (no two waves load the same A data) and all 64 pixels of the patch.
+// Block: 256 threads = 4 waves as WR rows x 4/WR columns; a row tile of 32*WR
+// output channels of one range of L consecutive output pixels of one image,
+// computed in sub-tiles of 64*4/WR pixels; wave tile 32 channels x 64 pixels
+// (2 x 4 MFMA 16x16x64 tiles, three accumulator sets).  Waves of one row read
+// their own weight rows; waves of one column read their own 64 pixels of the
+// patch.  (WR = 4 for more than 64 output channels, 2 for 33-64, 1 for <= 32.)
 // With one channel chunk the input rows of the range are staged into the LDS
 // patch once and every sub-tile reads them; with more chunks each sub-tile
 // restages every chunk.  After staging, each patch position's channel sum is
@@ -171,7 +172,6 @@ __global__ __launch_bounds__(256) void conv_wpack(PackArgs a) {
 // private 16-row LDS tile (no block barrier) and stores rows of 8 pixels as
 // 16-byte writes.
 constexpr int kPgThreads = 256;
-constexpr int PBN = 64;                                 // pixels per sub-tile
 constexpr uint32_t kEpiPitch = 72;                      // int16 per row of a wave's epilogue tile
 constexpr uint32_t kEpiBytes = 16u * kEpiPitch * 2u;    // 16 channel rows x 64 pixels (+ pad)
 constexpr int kMaxTaps = kMaxQ / 4;
@@ -187,18 +187,34 @@ __device__ __forceinline__ void wave_sync() {
 // loads in flight while the accumulators are live).
 // NS: A fragment sets in flight (3: two steps of prefetch, for one chunk whose
 // step count is a multiple of 3; else 2: one step).
-template <bool HAS_BIAS, int VEC, bool MULTI, int NS>
+// WR: wave rows (row tile of 32 * WR output channels).
+template <int VEC, bool MULTI, int NS, int WR>
 __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
     static_assert(NS == 2 || (NS == 3 && !MULTI), "three A sets need one chunk");
+    constexpr uint32_t TB = 32u * WR;             // output channels per row tile
+    constexpr uint32_t WC = 4u / WR;              // wave columns
+    constexpr uint32_t SPX = 64u * WC;            // pixels per sub-tile
+    constexpr uint32_t PT = 2u * TB * 64u;        // limb-plane bytes per (row tile, k step)
+    constexpr uint32_t PT8 = TB * 64u;            // int8-plane bytes per (row tile, k step)
     constexpr int kPB = MULTI ? 1 : 4;   // 16-byte staging tasks per thread in flight
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ int32_t qtab[kMaxQ + 4];  // per sub-chunk q: patch byte offset of its tap and group
     __shared__ uint32_t tpos[kMaxTaps];  // per tap: patch position offset from a window origin
-    __shared__ uint32_t rowterm_s[BM];   // per output channel of the row tile: the row term
+    __shared__ uint32_t rowterm_s[kMaxTB];   // per output channel of the row tile: the row term
     uint8_t* p_hi = lds;
     uint8_t* p_lo = lds + g.p_plane;
     uint32_t* spos = reinterpret_cast<uint32_t*>(lds + g.spos_off);   // per position: channel sum
 
+    // Touch every 64-byte line of the arguments at once: they arrive cold from
+    // device memory, and fetched one at a time behind the branches that use
+    // them they cost a memory round trip each.
+    {
+        uint32_t touch = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < (sizeof(PgArgs) + 63) / 64; ++i)
+            touch ^= reinterpret_cast<const uint32_t*>(&g)[i * 16];
+        asm volatile("" ::"s"(touch));
+    }
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     int16_t* et = reinterpret_cast<int16_t*>(lds + g.epi_off + wave * kEpiBytes);
     // Workgroups are dealt to the 8 XCDs round robin; block b of XCD x takes the
@@ -207,7 +223,8 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
     const uint32_t nb = gridDim.x, per = nb >> 3, rem = nb & 7u, xcd = blockIdx.x & 7u, idx = blockIdx.x >> 3;
     const uint32_t lg = xcd < rem ? xcd * (per + 1u) + idx : rem * (per + 1u) + (xcd - rem) * per + idx;
     const uint32_t mt = fdiv(lg, g.div_nbm), rest = lg - mt * g.rpi_n;
-    const uint32_t row0 = mt * BM, wrow = row0 + wave * 32;
+    const uint32_t wr = wave / WC, wc = wave - wr * WC;   // the wave's row / column
+    const uint32_t row0 = mt * TB, wrow = row0 + wr * 32;
     const uint32_t n = fdiv(rest, g.div_rpi);
     const uint32_t pb = (rest - n * g.rpi) * g.L;                       // the range's first pixel
     const uint32_t pe = min(pb + g.L, g.P);                             // one past its last
@@ -226,30 +243,30 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
     // A fragments of step gs: row tile i of the wave's 32 rows, hi and lo planes
     // (steps past the last one read another row tile's data or, past the buffer,
     // 0; neither is used)
-    const uint32_t a_src = (mt * g.steps) * kPackTile + (wave * 32u + (lane & 15)) * 64u + (lane >> 4) * 16u;
+    const uint32_t a_src = (mt * g.steps) * PT + (wr * 32u + (lane & 15)) * 64u + (lane >> 4) * 16u;
     auto a_load = [&](uint32_t gs, v4i (&ah)[2], v4i (&al)[2]) {
-        const uint32_t off = a_src + gs * kPackTile;
+        const uint32_t off = a_src + gs * PT;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             ah[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wrs, off + i * 1024u, 0, 0));
             al[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
-                wrs, off + BM * 64u + i * 1024u, 0, 0));
+                wrs, off + TB * 64u + i * 1024u, 0, 0));
         }
     };
     // the int8 plane's A fragments of step gs (rows whose weights all fit int8)
-    const uint32_t a8_src = g.pk8_off + (mt * g.steps) * kPackTile8 + (wave * 32u + (lane & 15)) * 64u +
+    const uint32_t a8_src = g.pk8_off + (mt * g.steps) * PT8 + (wr * 32u + (lane & 15)) * 64u +
                             (lane >> 4) * 16u;
     auto a_load8 = [&](uint32_t gs, v4i (&a8)[2]) {
-        const uint32_t off = a8_src + gs * kPackTile8;
+        const uint32_t off = a8_src + gs * PT8;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
             a8[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(wrs, off + i * 1024u, 0, 0));
     };
     // Row terms and int8 flags of the block's 128 output channels: loaded here,
     // used after the patch is staged (128 * row sum + bias << 8)
-    const uint32_t rm = min(row0 + (tid & (BM - 1)), g.M - 1u);
+    const uint32_t rm = min(row0 + (tid & (TB - 1)), g.M - 1u);
     const uint32_t ld_wsum = g.wsum[rm], ld_fit = g.wfit[rm];
-    const int32_t ld_bias = HAS_BIAS ? (int32_t)g.bias[rm] : 0;
+    const int32_t ld_bias = g.bias ? (int32_t)g.bias[rm] : 0;
 
     // Patch staging of one chunk (the range's rows; tasks past prows_b are
     // skipped).  Rows outside the image and channels past C read 0 through the
@@ -404,7 +421,7 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
     const uint32_t kp_term = 16384u * 64u * g.steps;
     const int32_t lo = q88::act_lo(g.epi.act), hi = q88::act_hi(g.epi.act);
     const bool plain = g.epi.add_mode == 0u && g.epi.act == 0u;   // no Add, no activation
-    const uint32_t nsub = (pe - pb + PBN - 1) / PBN;
+    const uint32_t nsub = (pe - pb + SPX - 1) / SPX;
     // A fragment sets: the set of global step gs is gs % NS, and the next NS - 1
     // steps' sets are in flight while a step's MFMAs run
     v4i fa_h[NS][2], fa_l[NS][2];
@@ -420,9 +437,9 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
     };
 
     for (uint32_t sub = 0; sub < nsub; ++sub) {
-        const uint32_t p0 = pb + sub * PBN;
-        const uint32_t pn = min((uint32_t)PBN, pe - p0);   // pixels of this sub-tile
-        const uint32_t nj = (pn + 15u) / 16u;              // 16-pixel column tiles in use
+        const uint32_t p0 = pb + sub * SPX + wc * 64u;      // this wave's first pixel of the sub-tile
+        const uint32_t pn = p0 < pe ? min(64u, pe - p0) : 0u;   // the wave's pixels of this sub-tile
+        const uint32_t nj = (pn + 15u) / 16u;              // 16-pixel column tiles in use (0 - 4)
         // the first chunk's patch (with one chunk: staged once for every sub-tile),
         // before the accumulators and A fragments of this sub-tile are live
         if (sub == 0 || MULTI) {
@@ -430,8 +447,8 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
             stage_patch(0u, MULTI ? 4u : g.cpt_last);
             if (sub == 0) {
                 const bool real = row0 + tid < g.M;
-                if (tid < BM) rowterm_s[tid] = real ? 128u * ld_wsum + (uint32_t)ld_bias * 256u : 0u;
-                fast = __syncthreads_and(tid >= BM || !real || ld_fit != 0u) != 0;
+                if (tid < TB) rowterm_s[tid] = real ? 128u * ld_wsum + (uint32_t)ld_bias * 256u : 0u;
+                fast = __syncthreads_and(tid >= TB || !real || ld_fit != 0u) != 0;
             } else {
                 __syncthreads();
             }
@@ -468,7 +485,7 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
                 mid[i][j] = v4i{0, 0, 0, 0};
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    ll[i][j][e] = (int32_t)(rowterm_s[wave * 32 + i * 16 + (lane >> 4) * 4 + e] - (fast ? 0u : kp_term));
+                    ll[i][j][e] = (int32_t)(rowterm_s[wr * 32 + i * 16 + (lane >> 4) * 4 + e] - (fast ? 0u : kp_term));
             }
         auto window_sums = [&]() {
             uint32_t cs[4] = {0u, 0u, 0u, 0u};
@@ -700,13 +717,20 @@ constexpr uint64_t kPgLdsMax = 78u * 1024u;   // dynamic LDS per block: two bloc
 
 }  // namespace
 
-// Returns 1 (launching nothing) when the shape does not suit this path or the
-// workspace is too small; with lc.need set, records the workspace it needs.
-int cm_conv_pgemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
-                         uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
-                         uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
-                         uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
-                         uint32_t pad_left, const cm_epilogue_t* epi, const LaunchCtx& lc) {
+namespace {
+
+enum PgMode { kPackAndRun, kPackOnly, kRunPacked };
+
+// One patch-GEMM call: pack the weights into lc.ws and run (kPackAndRun), only
+// pack them into `dst` (kPackOnly), or run with weights packed earlier
+// (kRunPacked, `packed`).  Returns 1 (launching nothing) when the shape does
+// not suit this path or the workspace is too small; with lc.need set, records
+// the bytes the packed weights take.
+int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y, uint32_t batch,
+              uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch, uint32_t out_h,
+              uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t sh, uint32_t sw, uint32_t dh,
+              uint32_t dw, uint32_t pad_top, uint32_t pad_left, const cm_epilogue_t* epi,
+              const LaunchCtx& lc, PgMode mode, const void* packed, void* dst, size_t dst_bytes) {
     const EpiArgs ea = cm_epi_args(epi);
     if (in_ch == 0 || out_ch == 0 || kh == 0 || kw == 0 || sh == 0 || dh == 0) return 1;
     // one stride / dilation pair for both axes keeps the patch rows and columns alike
@@ -718,7 +742,11 @@ int cm_conv_pgemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias
     if (P == 0 || 2 * x_img >= 0x80000000ull || P >= (1u << 24) || in_h >= (1u << 20) ||
         in_w >= (1u << 20) || out_w > 4096 || pad_top >= in_h + kh * dh || pad_left >= in_w + kw * dw)
         return 1;
-    const uint32_t mtiles = (out_ch + BM - 1) / BM;
+    const uint32_t nchunks = (in_ch + 63) / 64;
+    // row tile: 32, 64 or 128 output channels (128 with several channel chunks)
+    const uint32_t wrows = nchunks > 1 || out_ch > 64 ? 4u : out_ch > 32 ? 2u : 1u;
+    const uint32_t TB = 32u * wrows, SPX = 256u / wrows;
+    const uint32_t mtiles = (out_ch + TB - 1) / TB;
     const uint32_t gg = gcd(sh, dh), Sg = sh / gg, Dg = dh / gg;
     if ((uint64_t)out_ch * P * 2 >= 0x80000000ull) return 1;
     // 16-byte patch loads: rows 16-byte aligned, and g = 1 or 2
@@ -731,7 +759,6 @@ int cm_conv_pgemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias
     const uint32_t PW = vec && wr > PWr ? wr : PWr;
     const uint32_t lhc = lh < PWr ? lh : PWr;
     const uint32_t nh = lhc + (PWr > wr ? PWr - wr : 0u);
-    const uint32_t nchunks = (in_ch + 63) / 64;
     const uint32_t cpt_max = nchunks > 1 ? 4u : (in_ch + 15) / 16;
     const uint32_t ppitch = cpt_max % 2 ? cpt_max * 16 : cpt_max * 16 + 16;   // odd multiple of 16
     const uint32_t khspan = (kh - 1) * Dg + 1;
@@ -745,12 +772,13 @@ int cm_conv_pgemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias
         return epi_off + 4ull * kEpiBytes;
     };
     // Pixels per block L (a multiple of 16): the fewest modelled cycles per CU,
-    // with blocks dealt over the CUs two at a time.  A 16-pixel column tile costs
-    // 128 MFMA cycles per k step; staging a patch row costs about one cycle per
-    // 16 bytes loaded, once per block pair (the second block's staging overlaps
-    // the first one's MFMAs) and once per sub-tile and chunk with several chunks;
-    // a lone block per CU keeps one wave per SIMD and runs at about 70%.  With
-    // fewer blocks than CUs at every L the shape goes to another path.
+    // with blocks dealt over the CUs two at a time.  A wave's 16-pixel column
+    // tile costs 128 MFMA cycles per k step, and a block takes as long as its
+    // busiest wave (sub-tiles of 64 pixels per wave column); staging a patch
+    // row costs about one cycle per 16 bytes loaded, once per block pair (the
+    // second block's staging overlaps the first one's MFMAs) and once per
+    // sub-tile and chunk with several chunks; a lone block per CU keeps one
+    // wave per SIMD and runs at about 70%.
     const uint64_t cus = cu_count();
     const uint64_t c_tile = 128ull * steps;
     const uint64_t c_row = (uint64_t)PW * cpt_max * 2;
@@ -765,10 +793,10 @@ int cm_conv_pgemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias
         const uint64_t rpi = (P + l - 1) / l;
         const uint64_t blocks = rpi * batch * mtiles;
         if (blocks > 0x7FFFFFFFull) continue;
-        if (blocks < cus) break;   // fewer blocks than CUs: another path suits better
         const uint64_t k = (blocks + cus - 1) / cus;
-        const uint64_t u = l / 16;
-        const uint64_t stage = pr * c_row * (nchunks > 1 ? nchunks * ((l + PBN - 1) / PBN) : 1u);
+        const uint64_t rem = l % SPX;
+        const uint64_t u = (l / SPX) * 4 + (std::min<uint64_t>(rem, 64) + 15) / 16;
+        const uint64_t stage = pr * c_row * (nchunks > 1 ? nchunks * ((l + SPX - 1) / SPX) : 1u);
         uint64_t t = k * u * c_tile + ((k + 1) / 2) * stage;
         if (k == 1) t = t * 10 / 7;
         if (t < best) { best = t; L = (uint32_t)l; prows = pr; }
@@ -781,23 +809,36 @@ int cm_conv_pgemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias
     const uint64_t zslot = prows * PW * ppitch;
     const uint64_t p_plane = zslot + 16;
     // workspace: limb planes, int8 plane, row sums, int8 flags
-    const uint64_t pk_limb = (uint64_t)mtiles * steps * kPackTile;
-    const uint64_t pk_bytes = pk_limb + (uint64_t)mtiles * steps * kPackTile8;
-    const uint64_t need = pk_bytes + 8ull * mtiles * BM;
+    const uint64_t pk_limb = (uint64_t)mtiles * steps * (2u * TB * 64u);
+    const uint64_t pk_bytes = pk_limb + (uint64_t)mtiles * steps * (TB * 64u);
+    const uint64_t need = pk_bytes + 8ull * mtiles * TB;
     if (pk_bytes >= 0x80000000ull) return 1;
     if (lc.need) {
         if (need > *lc.need) *lc.need = need;
         return CM_OK;
     }
-    if (!lc.ws || lc.ws_bytes < need || !aligned(lc.ws, 16)) return 1;
-
-    uint8_t* wpk = static_cast<uint8_t*>(lc.ws);
-    uint32_t* wsum = reinterpret_cast<uint32_t*>(wpk + pk_bytes);
-    uint32_t* wfit = wsum + mtiles * BM;
-    PackArgs pa{w, wpk, wpk + pk_limb, wsum, wfit, in_ch, out_ch, taps, nchunks, steps, taps};
-    hipLaunchKernelGGL(conv_wpack, dim3(mtiles * BM), dim3(256), 0, lc.s, pa);
-    int rc = cm_check_launch("conv_wpack");
-    if (rc) return rc;
+    uint8_t* wbuf = nullptr;
+    if (mode == kRunPacked) {
+        if (!packed || !aligned(packed, 16)) return cm_set_error(CM_ERR_INVALID, "conv packed: weights not 16-byte aligned");
+    } else {
+        wbuf = static_cast<uint8_t*>(mode == kPackOnly ? dst : lc.ws);
+        const size_t have = mode == kPackOnly ? dst_bytes : lc.ws_bytes;
+        if (!wbuf || have < need || !aligned(wbuf, 16)) {
+            if (mode == kPackOnly)
+                return cm_set_error(CM_ERR_RANGE, "conv pack: %zu bytes given, %llu needed", have,
+                                    (unsigned long long)need);
+            return 1;
+        }
+        PackArgs pa{w, wbuf, wbuf + pk_limb, reinterpret_cast<uint32_t*>(wbuf + pk_bytes),
+                    reinterpret_cast<uint32_t*>(wbuf + pk_bytes) + mtiles * TB,
+                    in_ch, out_ch, taps, nchunks, steps, taps, TB};
+        hipLaunchKernelGGL(conv_wpack, dim3(mtiles * TB), dim3(256), 0, lc.s, pa);
+        const int rc = cm_check_launch("conv_wpack");
+        if (rc || mode == kPackOnly) return rc;
+    }
+    const uint8_t* wpk = mode == kRunPacked ? static_cast<const uint8_t*>(packed) : wbuf;
+    const uint32_t* wsum = reinterpret_cast<const uint32_t*>(wpk + pk_bytes);
+    const uint32_t* wfit = wsum + mtiles * TB;
 
     PgArgs g{};
     g.x = x; g.wpk = wpk; g.wsum = wsum; g.wfit = wfit; g.bias = bias; g.y = y;
@@ -838,11 +879,14 @@ int cm_conv_pgemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias
     // (ranges start at multiples of L, sub-tiles at multiples of 64 pixels)
     g.vw = P % 8 == 0 && aligned(y, 16) && (ea.add_mode != 1u || aligned(ea.add, 16)) ? 8u : 1u;
     const void* k = nullptr;
-#define CM_PG_PICK(B, M, NS) (vec == 1 ? (const void*)conv_pgemm<B, 1, M, NS> \
-                              : vec == 2 ? (const void*)conv_pgemm<B, 2, M, NS> : (const void*)conv_pgemm<B, 0, M, NS>)
-    if (nchunks > 1) k = bias ? CM_PG_PICK(true, true, 2) : CM_PG_PICK(false, true, 2);
-    else if (steps % 3 == 0) k = bias ? CM_PG_PICK(true, false, 3) : CM_PG_PICK(false, false, 3);
-    else k = bias ? CM_PG_PICK(true, false, 2) : CM_PG_PICK(false, false, 2);
+#define CM_PG_PICK(M, NS, W) (vec == 1 ? (const void*)conv_pgemm<1, M, NS, W> \
+                              : vec == 2 ? (const void*)conv_pgemm<2, M, NS, W> : (const void*)conv_pgemm<0, M, NS, W>)
+#define CM_PG_PICK_W(M, NS) (wrows == 1 ? CM_PG_PICK(M, NS, 1) : wrows == 2 ? CM_PG_PICK(M, NS, 2) \
+                                                                     : CM_PG_PICK(M, NS, 4))
+    if (nchunks > 1) k = CM_PG_PICK(true, 2, 4);
+    else if (steps % 3 == 0) k = CM_PG_PICK_W(false, 3);
+    else k = CM_PG_PICK_W(false, 2);
+#undef CM_PG_PICK_W
 #undef CM_PG_PICK
     if (lds > 65536u &&
         hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
@@ -854,4 +898,58 @@ int cm_conv_pgemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias
     const hipError_t e = hipLaunchKernel(k, grid, dim3(kPgThreads), kargs, (size_t)lds, lc.s);
     if (e != hipSuccess) return cm_set_error(CM_ERR_HIP, "conv_pgemm: %s", hipGetErrorString(e));
     return cm_check_launch("conv_pgemm");
+}
+
+const int16_t* probe_ptr() {   // a 16-byte aligned stand-in for shape-only queries
+    alignas(16) static const int16_t probe[8] = {};
+    return probe;
+}
+
+}  // namespace
+
+int cm_conv_pgemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
+                         uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                         uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
+                         uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
+                         uint32_t pad_left, const cm_epilogue_t* epi, const LaunchCtx& lc) {
+    return pg_launch(x, w, bias, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, sh, sw, dh,
+                     dw, pad_top, pad_left, epi, lc, kPackAndRun, nullptr, nullptr, 0);
+}
+
+size_t cm_conv_pgemm_packed_bytes(uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                                  uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh,
+                                  uint32_t kw, uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw,
+                                  uint32_t pad_top, uint32_t pad_left) {
+    size_t need = 0;
+    const LaunchCtx lc{nullptr, nullptr, 0, &need};
+    const int16_t* p = probe_ptr();
+    const int rc = pg_launch(p, p, p, const_cast<int16_t*>(p), batch, in_ch, in_h, in_w, out_ch, out_h,
+                             out_w, kh, kw, sh, sw, dh, dw, pad_top, pad_left, nullptr, lc, kPackOnly,
+                             nullptr, nullptr, 0);
+    return rc == CM_OK ? need : 0u;
+}
+
+int cm_conv_pgemm_pack(const int16_t* w, uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                       uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
+                       uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
+                       uint32_t pad_left, void* dst, size_t bytes, hipStream_t s) {
+    const LaunchCtx lc{s, nullptr, 0, nullptr};
+    const int16_t* p = probe_ptr();
+    const int rc = pg_launch(p, w, nullptr, const_cast<int16_t*>(p), batch, in_ch, in_h, in_w, out_ch,
+                             out_h, out_w, kh, kw, sh, sw, dh, dw, pad_top, pad_left, nullptr, lc,
+                             kPackOnly, nullptr, dst, bytes);
+    return rc == 1 ? cm_set_error(CM_ERR_INVALID, "conv pack: the shape does not take the patch-GEMM path")
+                   : rc;
+}
+
+int cm_conv_pgemm_run_packed(const int16_t* x, const void* packed, const int16_t* bias, int16_t* y,
+                             uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                             uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
+                             uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
+                             uint32_t pad_left, const cm_epilogue_t* epi, hipStream_t s) {
+    const LaunchCtx lc{s, nullptr, 0, nullptr};
+    const int rc = pg_launch(x, nullptr, bias, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw,
+                             sh, sw, dh, dw, pad_top, pad_left, epi, lc, kRunPacked, packed, nullptr, 0);
+    return rc == 1 ? cm_set_error(CM_ERR_INVALID, "conv packed: the shape does not take the patch-GEMM path")
+                   : rc;
 }

@@ -158,6 +158,46 @@ def ConvKernel(x, weight, bias, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_
                  ctypes.byref(epi) if epi is not None else None, ws, ws_bytes, _stream(stream))
 
 
+def conv_packed_size(batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h=1,
+                     stride_w=1, dilation_h=1, dilation_w=1, pad_top=0, pad_left=0,
+                     has_bias=0, is_depthwise=0) -> int:
+    """Bytes of packed weights for ConvPackedKernel on this shape (0: the shape runs
+    on another path and cannot use packed weights)."""
+    args = [batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w,
+            dilation_h, dilation_w, pad_top, pad_left, int(bool(has_bias)), int(bool(is_depthwise))]
+    return int(_native.load().cm_conv_packed_size(*(_u32("conv arg", v) for v in args)))
+
+
+def conv_pack(weight, packed, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw,
+              stride_h=1, stride_w=1, dilation_h=1, dilation_w=1, pad_top=0, pad_left=0,
+              has_bias=0, is_depthwise=0, stream=None) -> None:
+    """Pack `weight` (the ConvKernel layout) into the device tensor `packed` once."""
+    args = [batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w,
+            dilation_h, dilation_w, pad_top, pad_left, int(bool(has_bias)), int(bool(is_depthwise))]
+    args = [_u32("conv arg", v) for v in args]
+    pw = _dev_ptr(weight, out_ch * in_ch * kh * kw, "weight")
+    pp, nbytes = _workspace(packed)
+    _native.call("cm_conv_pack", pw, *args, pp, nbytes, _stream(stream))
+
+
+def ConvPackedKernel(x, packed, bias, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw,
+                     stride_h=1, stride_w=1, dilation_h=1, dilation_w=1, pad_top=0, pad_left=0,
+                     has_bias=0, is_depthwise=0, stream=None, add=None, act=ACT_NONE) -> None:
+    """ConvKernel with weights packed earlier by conv_pack (same result bit for bit)."""
+    args = [batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, stride_h, stride_w,
+            dilation_h, dilation_w, pad_top, pad_left, int(bool(has_bias)), int(bool(is_depthwise))]
+    args = [_u32("conv arg", v) for v in args]
+    if batch * out_ch * out_h * out_w == 0:
+        return
+    px = _dev_ptr(x, batch * in_ch * in_h * in_w, "x")
+    pp, _ = _workspace(packed)
+    pbias = _dev_ptr(bias, out_ch, "bias") if has_bias else None
+    py = _dev_ptr(y, batch * out_ch * out_h * out_w, "y")
+    epi = _epilogue(add, False, act, batch * out_ch * out_h * out_w)
+    _native.call("cm_conv_packed_ex", px, pp, pbias, py, *args,
+                 ctypes.byref(epi) if epi is not None else None, _stream(stream))
+
+
 def PoolingKernel(x, y, batch, channels, in_h, in_w, out_h, out_w, pool_h, pool_w,
                   stride_h=1, stride_w=1, pad_top=0, pad_left=0, dil_h=1, dil_w=1,
                   pool_type=POOL_MAX, lp_order=2, count_include_pad=0, stream=None) -> None:

@@ -6,8 +6,9 @@ libcormorant_amd.so:
 
 * init: one ``cm_buf_alloc`` for the pool (weights + intermediates, 64-byte
   aligned slots, intermediates with disjoint lifetimes sharing a slot, then
-  the split-K workspace the MatMul / Conv calls share), one buffer per graph
-  input and output, weights copied in once;
+  the split-K workspace the MatMul / Conv calls share, then each patch-GEMM
+  convolution's packed weights), one buffer per graph input and output,
+  weights copied in once and packed once (``cm_conv_pack``);
 * run: graph inputs copied to the device, every kernel call enqueued in graph
   order on one in-order stream, graph outputs copied back (the only host
   synchronisation, as in the reference's sync_from_device).
@@ -57,26 +58,40 @@ class InferenceSession:
         self._bufs: Dict[Tuple[str, str], object] = {}
         self.workspace_bytes = 0
         self._ws_ptr: Optional[int] = None
+        self._packed: Dict[int, Tuple[int, int]] = {}   # launch index -> (pool byte offset, bytes)
         try:
+            # convolutions on the patch-GEMM path get their weights packed once
+            packed_sizes = [self._packed_size(c) for c in self.launch_list]
             # split-K workspace: one region after the pool's tensors, as large as
-            # the largest need over the launch list (the calls run one after
+            # the largest need over the other calls (the calls run one after
             # another on one stream, so they share it)
-            self.workspace_bytes = max((self._workspace_need(c) for c in self.launch_list),
-                                       default=0)
+            self.workspace_bytes = max((self._workspace_need(c) for c, ps in
+                                        zip(self.launch_list, packed_sizes) if not ps), default=0)
             ws_off = -(-self.plan.pool_elems // 128) * 128   # 256-byte aligned
-            total = ws_off + self.workspace_bytes // 2 if self.workspace_bytes else self.plan.pool_elems
+            end = 2 * ws_off + self.workspace_bytes
+            for i, ps in enumerate(packed_sizes):
+                if ps:
+                    end = -(-end // 256) * 256
+                    self._packed[i] = (end, ps)
+                    end += ps
+            total = -(-end // 2) if (self.workspace_bytes or self._packed) else self.plan.pool_elems
             if total:
                 pool = self._alloc(("pool", ""), total)
                 self._host(pool, total)[:self.plan.pool_elems] = self.plan.pool_image()
                 _native.call("cm_buf_sync_to_device", pool)
+                base = int(pool.contents.dev)
                 if self.workspace_bytes:
-                    self._ws_ptr = int(pool.contents.dev) + 2 * ws_off
+                    self._ws_ptr = base + 2 * ws_off
+                for i, (off, ps) in self._packed.items():
+                    call = self._call_of(self.launch_list[i])
+                    wptr = self.device_ptr(call.tensors[1]) + (2 * call.offsets[1] if call.offsets else 0)
+                    _native.call("cm_conv_pack", wptr, *call.args, base + off, ps, None)
             for t in self.graph.input_tensors:
                 self._alloc(("input", t.onnx_name), self.plan.layouts[t.onnx_name].alloc)
             for t in self.graph.output_tensors:
                 self._alloc(("output", t.onnx_name), self.plan.layouts[t.onnx_name].alloc)
             _native.call("cm_sync", None)
-            self._launches = [self._prepare(c) for c in self.launch_list]
+            self._launches = [self._prepare(c, i) for i, c in enumerate(self.launch_list)]
         except Exception:
             self.close()
             raise
@@ -115,6 +130,16 @@ class InferenceSession:
             ptrs.append(p)
         return ptrs
 
+    @staticmethod
+    def _call_of(item) -> KernelCall:
+        return item.call if isinstance(item, _fuse.FusedCall) else item
+
+    def _packed_size(self, item) -> int:
+        call = self._call_of(item)
+        if call.kernel != "conv":
+            return 0
+        return int(self._lib.cm_conv_packed_size(*call.args))
+
     def _workspace_need(self, item) -> int:
         call = item.call if isinstance(item, _fuse.FusedCall) else item
         if call.kernel in ("matmul", "matmul_at"):
@@ -123,8 +148,11 @@ class InferenceSession:
             return int(self._lib.cm_conv_workspace_size(*call.args))
         return 0
 
-    def _prepare(self, item):
+    def _prepare(self, item, index: int):
         ws = (self._ws_ptr, self.workspace_bytes) if self._ws_ptr else (None, 0)
+        packed = self._packed.get(index)
+        if packed is not None:   # packed weights in place of the weight tensor, no workspace
+            ws = ()
         if isinstance(item, _fuse.FusedCall):
             call = item.call
             name = "cm_conv_ex" if call.kernel == "conv" else "cm_matmul_ex"
@@ -134,9 +162,17 @@ class InferenceSession:
             epi.add = self.device_ptr(item.add) if item.add is not None else None
             epi.add_mode = item.add_mode
             epi.act = item.act
+            if packed is not None:
+                name = "cm_conv_packed_ex"
+                ptrs[1] = int(self._bufs[("pool", "")].contents.dev) + packed[0]
             # the epilogue object rides along in the tuple so it outlives the pointer
             return getattr(self._lib, name), name, tuple(ptrs) + tuple(call.args) + (
                 ctypes.byref(epi),) + ws, epi
+        if packed is not None:
+            name = "cm_conv_packed_ex"
+            ptrs = self._pointers(item)
+            ptrs[1] = int(self._bufs[("pool", "")].contents.dev) + packed[0]
+            return getattr(self._lib, name), name, tuple(ptrs) + tuple(item.args) + (None,), None
         if item.kernel in _EX_FUNCS:   # MatMul / Conv: the _ex form carries the workspace
             name = _EX_FUNCS[item.kernel]
             return (getattr(self._lib, name), name,

@@ -174,6 +174,36 @@ size_t cm_conv_workspace_size(uint32_t batch, uint32_t in_ch, uint32_t in_h, uin
                               uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
                               uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise);
 
+/* Weights packed once, for callers that run one convolution's weights many
+ * times (an inference session loading a model).  No reference counterpart:
+ * cm_conv / cm_conv_ex repack the weights on every call, as ConvKernel reads
+ * them on every call.  cm_conv_packed_size returns the bytes of the packed
+ * weights for a shape that cm_conv runs on its patch-GEMM path (windows of two
+ * or more taps, the same stride and dilation on both axes), and 0 for any
+ * other shape; cm_conv_pack writes them (into caller-owned, 16-byte aligned
+ * device memory); cm_conv_packed_ex then computes exactly what cm_conv_ex
+ * computes with the weights that were packed, without repacking.  The packed
+ * bytes depend on in_ch, out_ch, kh and kw only; any other argument may change
+ * between cm_conv_pack and cm_conv_packed_ex as long as the shape still takes
+ * the path (cm_conv_packed_size > 0). */
+size_t cm_conv_packed_size(uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                           uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh,
+                           uint32_t kw, uint32_t stride_h, uint32_t stride_w,
+                           uint32_t dilation_h, uint32_t dilation_w, uint32_t pad_top,
+                           uint32_t pad_left, uint32_t has_bias, uint32_t is_depthwise);
+int cm_conv_pack(const int16_t *weight, uint32_t batch, uint32_t in_ch, uint32_t in_h,
+                 uint32_t in_w, uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh,
+                 uint32_t kw, uint32_t stride_h, uint32_t stride_w, uint32_t dilation_h,
+                 uint32_t dilation_w, uint32_t pad_top, uint32_t pad_left, uint32_t has_bias,
+                 uint32_t is_depthwise, void *packed, size_t packed_bytes, hipStream_t stream);
+int cm_conv_packed_ex(const int16_t *x, const void *packed, const int16_t *bias, int16_t *y,
+                      uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                      uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
+                      uint32_t stride_h, uint32_t stride_w, uint32_t dilation_h,
+                      uint32_t dilation_w, uint32_t pad_top, uint32_t pad_left,
+                      uint32_t has_bias, uint32_t is_depthwise, const cm_epilogue_t *epi,
+                      hipStream_t stream);
+
 /* cm_matmul_ex for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
  * counterpart in the reference.  Same arguments and result as cm_matmul_ex

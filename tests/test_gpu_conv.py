@@ -3,8 +3,10 @@ from __future__ import annotations
 
 import numpy as np
 import pytest
+import torch
 
 import oracle
+from cormorant_amd import _native
 from cormorant_amd import kernels as K
 from cormorant_amd import workloads as wl
 from tests import refcases as rc
@@ -137,12 +139,14 @@ def test_config4_full_size(case, ws):
 
 
 def pgemm_need(C, M, kh, kw):
-    """Workspace of the patch-GEMM path: packed weights (128 rows x 64 k as two limb
-    planes and one int8 plane per row tile and k step), and one uint32 row sum and
-    one int8 flag per padded row."""
-    taps, mt, nch = kh * kw, -(-M // 128), -(-C // 64)
+    """Workspace of the patch-GEMM path: packed weights (row tiles of TB = 32, 64 or
+    128 output channels: TB x 64 k as two limb planes and one int8 plane per row tile
+    and k step), and one uint32 row sum and one int8 flag per padded row."""
+    taps, nch = kh * kw, -(-C // 64)
+    tb = 128 if nch > 1 or M > 64 else 64 if M > 32 else 32
+    mt = -(-M // tb)
     steps = (nch - 1) * taps + (taps * -(-(C - (nch - 1) * 64) // 16) + 3) // 4
-    return mt * steps * 3 * 128 * 64 + 8 * 128 * mt
+    return mt * steps * 3 * tb * 64 + 8 * tb * mt
 
 
 PGEMM = [
@@ -249,3 +253,62 @@ def test_patch_path_random(seed):
     K.ConvKernel(dev(x), dev(w), dev(b), y, N, C, H, W, M, OH, OW, 3, 3, S, S, 1, 1, pt, pl, bias, 0,
                  add=dev(add), act=act)
     np.testing.assert_array_equal(host(y).astype(np.int32), want)
+
+
+PACKED = [
+    # N, C, H, W, M, kh, kw, s, d, p
+    (8, 32, 28, 32, 32, 3, 3, 1, 1, 1),        # 32-channel row tile
+    (4, 48, 20, 24, 40, 3, 3, 2, 1, 1),        # 64-channel row tile, stride 2
+    (2, 130, 9, 9, 150, 3, 3, 1, 2, 2),        # three channel chunks, two row tiles
+    (16, 64, 14, 14, 64, 3, 3, 1, 1, 1),       # MobileNet-like 14x14 layer
+]
+
+
+@pytest.mark.parametrize("geom", PACKED, ids=[str(g) for g in PACKED])
+def test_conv_packed_weights(geom):
+    """cm_conv_pack once, then cm_conv_packed_ex on two inputs (and with a fused Add
+    and ReLU6): every output equals cm_conv_ex's, for int8-range and full-range
+    weights."""
+    N, C, H, W, M, kh, kw, s, d, p = geom
+    OH, OW = (H + 2 * p - d * (kh - 1) - 1) // s + 1, (W + 2 * p - d * (kw - 1) - 1) // s + 1
+    args = (N, C, H, W, M, OH, OW, kh, kw, s, s, d, d, p, p, 1, 0)
+    size = K.conv_packed_size(*args)
+    assert size == pgemm_need(C, M, kh, kw)
+    say(f"conv packed weights {geom}")
+    g = wl.rng(835, *geom)
+    for lo, hi in ((-128, 128), (-32768, 32768)):
+        w = g.integers(lo, hi, M * C * kh * kw, dtype=np.int16)
+        b = g.integers(-32768, 32768, M, dtype=np.int16)
+        packed = torch.empty(-(-size // 4), dtype=torch.int32, device="cuda")
+        K.conv_pack(dev(w), packed, *args)
+        for rep in range(2):
+            x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
+            add = g.integers(-32768, 32768, N * M * OH * OW, dtype=np.int16)
+            want = np.zeros(N * M * OH * OW, np.int16)
+            oracle.set_threads(oracle_threads())
+            oracle.conv(x, w, b, want, *args, threads=True)
+            y = empty_dev(want.size)
+            K.ConvPackedKernel(dev(x), packed, dev(b), y, *args)
+            np.testing.assert_array_equal(host(y), want)
+            y2 = empty_dev(want.size)
+            K.ConvPackedKernel(dev(x), packed, dev(b), y2, *args, add=dev(add), act=K.ACT_RELU6)
+            exp = np.clip(np.clip(want.astype(np.int32) + add, -32768, 32767), 0, 1536)
+            np.testing.assert_array_equal(host(y2).astype(np.int32), exp)
+
+
+def test_conv_packed_rejects_other_paths():
+    """Shapes cm_conv runs elsewhere report no packed size, and the packed calls
+    refuse them; a packed buffer that is too small is refused."""
+    one = (4, 32, 14, 14, 32, 14, 14, 1, 1, 1, 1, 1, 1, 0, 0, 1, 0)      # 1x1
+    dwc = (4, 32, 14, 14, 32, 14, 14, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1)      # depthwise
+    aniso = (4, 32, 14, 14, 32, 14, 7, 3, 3, 1, 2, 1, 1, 1, 1, 1, 0)     # strides differ
+    for a in (one, dwc, aniso):
+        assert K.conv_packed_size(*a) == 0
+    buf = torch.empty(16, dtype=torch.int32, device="cuda")
+    w = torch.zeros(32 * 32 * 9, dtype=torch.int16, device="cuda")
+    with pytest.raises(_native.CmError):
+        K.conv_pack(w, buf, *aniso)
+    ok = (4, 32, 14, 14, 32, 14, 14, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0)
+    assert K.conv_packed_size(*ok) > 64
+    with pytest.raises(_native.CmError):
+        K.conv_pack(w, buf, *ok)   # 64 bytes is too small
