@@ -151,6 +151,9 @@ struct BandGeom {
     uint32_t pitch, cofs, lds_rows;    // LDS tile: lds_rows x pitch elements (+ slack rows)
     uint32_t alloc_rows;               // rows allocated (slack for the last strip's reads)
     uint32_t vec;                      // 16-byte row copies
+    uint32_t span;                     // rows not 16-byte aligned: 16-byte loads of the
+                                       // aligned span around an item's rows, scattered
+    uint32_t x_bytes;                  // span loads: bytes of x rounded up to 16 (the buffer range)
     uint32_t n_strips;                 // pool_strip: strips of kStrip output rows per band
     FastDiv div_w;                     // division by in_w (element copies)
 };
@@ -266,9 +269,27 @@ __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict_
     const uint32_t rows_pp = g.out_w >= (uint32_t)kThreads ? 1u : (uint32_t)kThreads / g.out_w;
     const uint32_t cstep = g.out_w > kThreads ? kThreads : g.out_w;
 
-    // fetch: the real input rows of an item into registers
-    v8s pre[PRE];
+    // fetch: the real input rows of an item into registers (span: the 16-byte
+    // vectors that cover them, one more than a row-aligned copy at most)
+    v8s pre[PRE + 1];
+    const __amdgpu_buffer_rsrc_t xrs = make_rsrc(x, b.span ? b.x_bytes : 0u);
+    auto span_first = [&](const BandItem& it) {   // element index of the item's first real input
+        return it.plane * (uint64_t)g.in_h * g.in_w + (uint64_t)(it.ih_lo + (int32_t)it.r0) * g.in_w;
+    };
     auto fetch = [&](const BandItem& it) {
+        if (b.span) {
+            const uint64_t f0 = span_first(it), f1 = f0 + (uint64_t)(it.r1 - it.r0) * g.in_w;
+            const uint64_t v0 = f0 >> 3;
+            const uint32_t nv = (uint32_t)(((f1 + 7) >> 3) - v0);
+#pragma unroll
+            for (int u = 0; u < PRE + 1; ++u) {
+                const uint32_t v = u * kThreads + threadIdx.x;
+                if (v < nv)
+                    pre[u] = __builtin_bit_cast(v8s, __builtin_amdgcn_raw_buffer_load_b128(
+                                                         xrs, (uint32_t)((v0 + v) * 16u), 0, kNonTemporal));
+            }
+            return;
+        }
         if (!b.vec) return;
         const int16_t* xp = x + it.plane * (uint64_t)g.in_h * g.in_w;
         const uint32_t nv = (it.r1 - it.r0) * vpr;
@@ -299,6 +320,31 @@ __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict_
                 for (int u = 0; u < PRE; ++u) {
                     const uint32_t v = u * kThreads + threadIdx.x;
                     if (v < nv) *reinterpret_cast<v8s*>(lds + cur.r0 * b.pitch + vslot[u]) = pre[u];
+                }
+            } else if (b.span) {
+                // element e of vector v is item element l = 8v + e - lead; its row
+                // and column step along with e (one division per vector)
+                const uint64_t f0 = span_first(cur);
+                const uint32_t lead = (uint32_t)(f0 & 7u);
+                const uint32_t n = (cur.r1 - cur.r0) * g.in_w;
+                const uint32_t nv = (n + lead + 7) / 8;
+#pragma unroll
+                for (int u = 0; u < PRE + 1; ++u) {
+                    const uint32_t v = u * kThreads + threadIdx.x;
+                    if (v >= nv) continue;
+                    const uint32_t e0 = v == 0 ? lead : 0u;   // first element of the item in the vector
+                    const uint32_t l0 = v * 8 + e0 - lead;
+                    uint32_t r = fdiv(l0, b.div_w), c = l0 - r * g.in_w;
+                    int16_t* row = lds + (cur.r0 + r) * b.pitch + b.cofs;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        if ((uint32_t)e < e0 || v * 8 + e - lead >= n) continue;
+                        row[c] = pre[u][e];
+                        if (++c == g.in_w) {
+                            c = 0;
+                            row += b.pitch;
+                        }
+                    }
                 }
             } else {
                 const int16_t* xp = x + cur.plane * (uint64_t)g.in_h * g.in_w;
@@ -551,6 +597,105 @@ __global__ __launch_bounds__(kThreads) void pool_strip(const int16_t* __restrict
     }
 }
 
+// ----------------------------------------------------------------- plane --
+// Small planes (at most kPlaneMax elements): one wave per plane.  The wave
+// copies its plane into a private LDS slot (16-byte loads when the planes are
+// whole 16-byte vectors), then each lane reduces every 64th output window
+// from LDS with pool_direct's bounds checks.  No block barrier: a plane's
+// whole life is one memory round trip, and a block holds four planes.
+constexpr uint32_t kPlaneMax = 2048;   // elements per plane: 4 KB of LDS per wave
+
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// KW > 0: a KW x KW window with dilation 1, its taps unrolled (all of a window's
+// LDS reads in flight together).
+template <int KIND, int KW>
+__global__ __launch_bounds__(kThreads) void pool_plane(const int16_t* __restrict__ x,
+                                                       int16_t* __restrict__ y, PoolGeom g,
+                                                       uint64_t planes, uint32_t vec, float inv_full,
+                                                       FastDiv div_ow) {
+    __shared__ __align__(16) int16_t tile[kThreads / 64][kPlaneMax];
+    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const uint64_t plane = (uint64_t)blockIdx.x * (kThreads / 64) + w;
+    if (plane >= planes) return;   // the whole wave leaves; nothing waits for it
+    const uint32_t hw = g.in_h * g.in_w;
+    const int16_t* xp = x + plane * hw;
+    int16_t* t = tile[w];
+    if (vec) {
+        constexpr int NV = kPlaneMax / 8 / 64;   // 16-byte vectors per lane at most
+        const uint32_t nv = hw / 8;
+        const v8s* xv = reinterpret_cast<const v8s*>(xp);
+        v8s d[NV];
+#pragma unroll
+        for (int u = 0; u < NV; ++u) {
+            const uint32_t v = u * 64 + lane;
+            if (v < nv) d[u] = __builtin_nontemporal_load(xv + v);
+        }
+#pragma unroll
+        for (int u = 0; u < NV; ++u) {
+            const uint32_t v = u * 64 + lane;
+            if (v < nv) *reinterpret_cast<v8s*>(t + v * 8) = d[u];
+        }
+    } else {
+        for (uint32_t i = lane; i < hw; i += 64) t[i] = xp[i];
+    }
+    wave_sync();
+    const uint32_t ohw = g.out_h * g.out_w;
+    int16_t* yp = y + plane * ohw;
+#pragma unroll 4
+    for (uint32_t o = lane; o < ohw; o += 64) {
+        const uint32_t oh = fdiv(o, div_ow), ow = o - oh * g.out_w;
+        const int32_t ih0 = (int32_t)(oh * g.sh) - (int32_t)g.pt;
+        const int32_t iw0 = (int32_t)(ow * g.sw) - (int32_t)g.pl;
+        Acc<KIND> a;
+        uint32_t vh = 0;
+        if constexpr (KW > 0) {
+            // padded taps read a real element (clamped index) and add the pad value
+            int32_t v[KW][KW];
+            bool okw[KW];
+#pragma unroll
+            for (int kwi = 0; kwi < KW; ++kwi) okw[kwi] = (uint32_t)(iw0 + kwi) < g.in_w;
+#pragma unroll
+            for (int khi = 0; khi < KW; ++khi) {
+                const int32_t ih = ih0 + khi;
+                const bool okh = (uint32_t)ih < g.in_h;
+                vh += okh ? 1u : 0u;
+                const int16_t* row = t + (okh ? (uint32_t)ih : 0u) * g.in_w;
+#pragma unroll
+                for (int kwi = 0; kwi < KW; ++kwi) {
+                    const int32_t iw = iw0 + kwi;
+                    v[khi][kwi] = okh && okw[kwi] ? (int32_t)row[(uint32_t)iw] : Acc<KIND>::kPad;
+                }
+            }
+#pragma unroll
+            for (int khi = 0; khi < KW; ++khi)
+#pragma unroll
+                for (int kwi = 0; kwi < KW; ++kwi) a.add(v[khi][kwi]);
+        } else {
+            for (uint32_t khi = 0; khi < g.ph; ++khi) {
+                const int32_t ih = ih0 + (int32_t)(khi * g.dh);
+                if ((uint32_t)ih >= g.in_h) continue;   // a padded row: skipping it is the pad's effect
+                ++vh;
+                const int16_t* row = t + (uint32_t)ih * g.in_w;
+                for (uint32_t kwi = 0; kwi < g.pw; ++kwi) {
+                    const int32_t iw = iw0 + (int32_t)(kwi * g.dw);
+                    if ((uint32_t)iw < g.in_w) a.add(row[iw]);
+                }
+            }
+        }
+        float inv = inv_full;
+        if constexpr (KIND == K_AVG) {
+            if (!g.cip) inv = q88::inv_denom(vh * (uint32_t)valid_taps(iw0, (int32_t)g.pw, (int32_t)g.dw,
+                                                                       (int32_t)g.in_w));
+        }
+        yp[o] = a.finish(inv);
+    }
+}
+
 // ---------------------------------------------------------------- direct --
 template <int KIND>
 __global__ __launch_bounds__(kThreads) void pool_direct(const int16_t* __restrict__ x,
@@ -646,6 +791,25 @@ int pool_launch(const int16_t* x, int16_t* y, uint64_t planes, const PoolGeom& g
                        g.pw < (1u << 10) && (uint64_t)g.out_w * g.sw < (1u << 30) &&
                        (uint64_t)g.out_h * g.sh < (1u << 30) &&
                        (uint64_t)g.in_h * g.in_w < (1u << 30);
+    // small planes: one wave per plane, the plane in LDS
+    if (small && (uint64_t)g.in_h * g.in_w <= kPlaneMax && (uint64_t)g.out_h * g.out_w <= (1u << 24)) {
+        const uint64_t blocks = (planes + 3) / 4;
+        if (blocks <= 0x7FFFFFFFull) {
+            const uint32_t vec = ((uint64_t)g.in_h * g.in_w) % 8 == 0 && (((uintptr_t)x & 15u) == 0);
+            const uint32_t kwp = g.dh == 1 && g.dw == 1 && g.ph == g.pw && (g.ph == 2 || g.ph == 3) ? g.ph : 0;
+            const FastDiv dow = make_fastdiv(g.out_w);
+            if (kwp == 3)
+                hipLaunchKernelGGL((pool_plane<KIND, 3>), dim3((uint32_t)blocks), dim3(kThreads), 0, s, x, y,
+                                   g, planes, vec, inv_full, dow);
+            else if (kwp == 2)
+                hipLaunchKernelGGL((pool_plane<KIND, 2>), dim3((uint32_t)blocks), dim3(kThreads), 0, s, x, y,
+                                   g, planes, vec, inv_full, dow);
+            else
+                hipLaunchKernelGGL((pool_plane<KIND, 0>), dim3((uint32_t)blocks), dim3(kThreads), 0, s, x, y,
+                                   g, planes, vec, inv_full, dow);
+            return cm_check_launch("pool_plane");
+        }
+    }
     // Padded LDS tile: columns [-pl, in_w + pr) at offset cofs = round_up(pl, 8),
     // pitch a multiple of 8; rows = the window footprint of `band_h` output rows.
     const uint64_t pr_need = (uint64_t)(g.out_w - 1) * g.sw + (uint64_t)(g.pw - 1) * g.dw + 1;
@@ -681,6 +845,15 @@ int pool_launch(const int16_t* x, int16_t* y, uint64_t planes, const PoolGeom& g
             b.cofs = (uint32_t)cofs;
             b.lds_rows = (uint32_t)rows_needed(g, band_h);
             b.vec = vec;
+            {
+                // the range rounds up to 16 bytes: buffer loads check it per dword,
+                // and the last element may share a dword with bytes past x (the
+                // 16-byte chunk holding x's last byte lies in x's page, x being
+                // 16-byte aligned)
+                const uint64_t xb = ((uint64_t)g.in_h * g.in_w * 2 * planes + 15) & ~15ull;
+                b.span = !vec && ((uintptr_t)x & 15u) == 0 && xb < 0x80000000ull;
+                b.x_bytes = b.span ? (uint32_t)xb : 0u;
+            }
             b.n_strips = (band_h + kStrip - 1) / kStrip;
             b.div_w = make_fastdiv(g.in_w);
             b.alloc_rows = b.lds_rows + (sh ? (kStrip - 1) * sh : 0);
