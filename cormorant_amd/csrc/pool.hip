@@ -600,10 +600,30 @@ __global__ __launch_bounds__(kThreads) void pool_strip(const int16_t* __restrict
 // ----------------------------------------------------------------- plane --
 // Small planes (at most kPlaneMax elements): one wave per plane.  The wave
 // copies its plane into a private LDS slot (16-byte loads when the planes are
-// whole 16-byte vectors), then each lane reduces every 64th output window
-// from LDS with pool_direct's bounds checks.  No block barrier: a plane's
-// whole life is one memory round trip, and a block holds four planes.
+// whole 16-byte vectors), then reduces the plane's output windows from LDS.
+// No block barrier: a plane's whole life is one memory round trip, and a
+// block holds four planes.
+//
+// With a fixed KW x KW window (dilation 1) the outputs split in two sets:
+//   * the interior rectangle [oh_lo, oh_hi) x [ow_lo, ow_hi), whose windows
+//     lie inside the plane: no bounds checks, the window origin's LDS offset
+//     and the output offset advance by constants from one 64-output step to
+//     the next, the taps reduce on raw values (max3 / add3);
+//   * the ring of border outputs around it: pool_direct's bounds checks.
+// The reduction is VALU bound at these sizes (the plane is one load round
+// trip), so the interior path carries as few instructions per output as it can.
 constexpr uint32_t kPlaneMax = 2048;   // elements per plane: 4 KB of LDS per wave
+
+struct PlaneGeom {
+    uint32_t oh_lo, oh_hi, ow_lo, iw_n;   // interior rows [oh_lo, oh_hi), columns [ow_lo, ow_lo + iw_n)
+    uint32_t n_int, n_ring;               // interior and ring outputs
+    uint32_t top_n, side, mid_n;          // ring: outputs above the interior, beside each interior
+                                          // row, and beside all interior rows
+    uint32_t dc;                          // 64 = (64 / iw_n) * iw_n + dc
+    int32_t step_a, wrap_a;               // window origin (LDS elements): per step, per row wrap
+    uint32_t step_o, wrap_o;              // output offset: per step, per row wrap
+    FastDiv div_iw, div_ow, div_side;
+};
 
 __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -611,13 +631,112 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// KW > 0: a KW x KW window with dilation 1, its taps unrolled (all of a window's
-// LDS reads in flight together).
+// A KW x KW window entirely inside the plane, origin `w`, row pitch in_w:
+// the reduction on raw values equals Acc's on shifted ones (max(x << 8) =
+// max(x) << 8; sums of x << 8 mod 2^32 = (sum of x) << 8 mod 2^32, and a
+// window of at most 9 taps cannot overflow int32 before the shift).
+template <int KIND, int KW>
+__device__ __forceinline__ int16_t window_inside(const int16_t* w, uint32_t in_w, float inv_full) {
+    int32_t v[KW * KW];
+    // element reads: the compiler would otherwise pair neighbours into 4-byte
+    // reads, unaligned for every other window origin
+    typedef __attribute__((address_space(3))) const volatile int16_t lds_i16;
+    lds_i16* wv = (lds_i16*)w;
+#pragma unroll
+    for (int khi = 0; khi < KW; ++khi)
+#pragma unroll
+        for (int kwi = 0; kwi < KW; ++kwi) v[khi * KW + kwi] = wv[khi * in_w + kwi];
+    if constexpr (KIND == K_MAX) {
+        int32_t m = v[0];
+#pragma unroll
+        for (int i = 1; i < KW * KW; ++i) m = __builtin_elementwise_max(m, v[i]);
+        return (int16_t)m;
+    } else if constexpr (KIND == K_LP2) {
+        uint32_t a = 0;
+#pragma unroll
+        for (int i = 0; i < KW * KW; ++i) a += (uint32_t)(v[i] * v[i]);
+        return q88::lp2_finalize(a);
+    } else {
+        int32_t sum = 0;
+#pragma unroll
+        for (int i = 0; i < KW * KW; ++i) sum += KIND == K_LP1 ? __builtin_abs(v[i]) : v[i];
+        const uint32_t a = (uint32_t)sum << 8;
+        if constexpr (KIND == K_AVG) return q88::avg_finalize(a, inv_full);
+        else return q88::acc_to_data(a);
+    }
+}
+
+// One output through pool_direct's bounds checks (the ring, or any window
+// when KW == 0).
+template <int KIND, int KW>
+__device__ __forceinline__ int16_t window_checked(const int16_t* t, const PoolGeom& g, uint32_t oh,
+                                                  uint32_t ow, float inv_full) {
+    const int32_t ih0 = (int32_t)(oh * g.sh) - (int32_t)g.pt;
+    const int32_t iw0 = (int32_t)(ow * g.sw) - (int32_t)g.pl;
+    Acc<KIND> a;
+    uint32_t vh = 0;
+    if constexpr (KW > 0) {
+        // every tap read unconditionally at a clamped position (all KW*KW reads in
+        // flight together), then masked to the pad value
+        int32_t v[KW][KW];
+        int32_t mw[KW];
+        uint32_t iwc[KW], vw = 0;
+#pragma unroll
+        for (int kwi = 0; kwi < KW; ++kwi) {
+            const bool ok = (uint32_t)(iw0 + kwi) < g.in_w;
+            iwc[kwi] = ok ? (uint32_t)(iw0 + kwi) : 0u;
+            mw[kwi] = -(int32_t)ok;
+            vw += ok ? 1u : 0u;
+        }
+#pragma unroll
+        for (int khi = 0; khi < KW; ++khi) {
+            const int32_t ih = ih0 + khi;
+            const bool okh = (uint32_t)ih < g.in_h;
+            vh += okh ? 1u : 0u;
+            const int16_t* row = t + (okh ? (uint32_t)ih : 0u) * g.in_w;
+#pragma unroll
+            for (int kwi = 0; kwi < KW; ++kwi) {
+                // a mask, not a select: a select lets the compiler sink the read
+                // into a branch and wait for each read in turn
+                const int32_t m = mw[kwi] & -(int32_t)okh;
+                v[khi][kwi] = ((int32_t)row[iwc[kwi]] & m) | (Acc<KIND>::kPad & ~m);
+            }
+        }
+#pragma unroll
+        for (int khi = 0; khi < KW; ++khi)
+#pragma unroll
+            for (int kwi = 0; kwi < KW; ++kwi) a.add(v[khi][kwi]);
+        float inv = inv_full;
+        if constexpr (KIND == K_AVG) {
+            if (!g.cip) inv = q88::inv_denom(vh * vw);
+        }
+        return a.finish(inv);
+    }
+    for (uint32_t khi = 0; khi < g.ph; ++khi) {
+        const int32_t ih = ih0 + (int32_t)(khi * g.dh);
+        if ((uint32_t)ih >= g.in_h) continue;   // a padded row: skipping it is the pad's effect
+        ++vh;
+        const int16_t* row = t + (uint32_t)ih * g.in_w;
+        for (uint32_t kwi = 0; kwi < g.pw; ++kwi) {
+            const int32_t iw = iw0 + (int32_t)(kwi * g.dw);
+            if ((uint32_t)iw < g.in_w) a.add(row[iw]);
+        }
+    }
+    float inv = inv_full;
+    if constexpr (KIND == K_AVG) {
+        if (!g.cip)
+            inv = q88::inv_denom(vh * (uint32_t)valid_taps(iw0, (int32_t)g.pw, (int32_t)g.dw, (int32_t)g.in_w));
+    }
+    return a.finish(inv);
+}
+
+// KW > 0: a KW x KW window with dilation 1 (interior + ring); KW == 0: any
+// window, every output checked.
 template <int KIND, int KW>
 __global__ __launch_bounds__(kThreads) void pool_plane(const int16_t* __restrict__ x,
                                                        int16_t* __restrict__ y, PoolGeom g,
-                                                       uint64_t planes, uint32_t vec, float inv_full,
-                                                       FastDiv div_ow) {
+                                                       PlaneGeom p, uint64_t planes, uint32_t vec,
+                                                       float inv_full) {
     __shared__ __align__(16) int16_t tile[kThreads / 64][kPlaneMax];
     const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const uint64_t plane = (uint64_t)blockIdx.x * (kThreads / 64) + w;
@@ -627,14 +746,15 @@ __global__ __launch_bounds__(kThreads) void pool_plane(const int16_t* __restrict
     int16_t* t = tile[w];
     if (vec) {
         constexpr int NV = kPlaneMax / 8 / 64;   // 16-byte vectors per lane at most
+        // range-checked buffer loads (past the plane they return zero and touch no
+        // memory): no branch between them, so all NV are in flight together
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(xp, hw * 2u);
         const uint32_t nv = hw / 8;
-        const v8s* xv = reinterpret_cast<const v8s*>(xp);
         v8s d[NV];
 #pragma unroll
-        for (int u = 0; u < NV; ++u) {
-            const uint32_t v = u * 64 + lane;
-            if (v < nv) d[u] = __builtin_nontemporal_load(xv + v);
-        }
+        for (int u = 0; u < NV; ++u)
+            d[u] = __builtin_bit_cast(v8s, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rs, (u * 64 + lane) * 16u, 0, kNonTemporal));
 #pragma unroll
         for (int u = 0; u < NV; ++u) {
             const uint32_t v = u * 64 + lane;
@@ -644,56 +764,89 @@ __global__ __launch_bounds__(kThreads) void pool_plane(const int16_t* __restrict
         for (uint32_t i = lane; i < hw; i += 64) t[i] = xp[i];
     }
     wave_sync();
-    const uint32_t ohw = g.out_h * g.out_w;
-    int16_t* yp = y + plane * ohw;
-#pragma unroll 4
-    for (uint32_t o = lane; o < ohw; o += 64) {
-        const uint32_t oh = fdiv(o, div_ow), ow = o - oh * g.out_w;
-        const int32_t ih0 = (int32_t)(oh * g.sh) - (int32_t)g.pt;
-        const int32_t iw0 = (int32_t)(ow * g.sw) - (int32_t)g.pl;
-        Acc<KIND> a;
-        uint32_t vh = 0;
-        if constexpr (KW > 0) {
-            // padded taps read a real element (clamped index) and add the pad value
-            int32_t v[KW][KW];
-            bool okw[KW];
-#pragma unroll
-            for (int kwi = 0; kwi < KW; ++kwi) okw[kwi] = (uint32_t)(iw0 + kwi) < g.in_w;
-#pragma unroll
-            for (int khi = 0; khi < KW; ++khi) {
-                const int32_t ih = ih0 + khi;
-                const bool okh = (uint32_t)ih < g.in_h;
-                vh += okh ? 1u : 0u;
-                const int16_t* row = t + (okh ? (uint32_t)ih : 0u) * g.in_w;
-#pragma unroll
-                for (int kwi = 0; kwi < KW; ++kwi) {
-                    const int32_t iw = iw0 + kwi;
-                    v[khi][kwi] = okh && okw[kwi] ? (int32_t)row[(uint32_t)iw] : Acc<KIND>::kPad;
-                }
-            }
-#pragma unroll
-            for (int khi = 0; khi < KW; ++khi)
-#pragma unroll
-                for (int kwi = 0; kwi < KW; ++kwi) a.add(v[khi][kwi]);
-        } else {
-            for (uint32_t khi = 0; khi < g.ph; ++khi) {
-                const int32_t ih = ih0 + (int32_t)(khi * g.dh);
-                if ((uint32_t)ih >= g.in_h) continue;   // a padded row: skipping it is the pad's effect
-                ++vh;
-                const int16_t* row = t + (uint32_t)ih * g.in_w;
-                for (uint32_t kwi = 0; kwi < g.pw; ++kwi) {
-                    const int32_t iw = iw0 + (int32_t)(kwi * g.dw);
-                    if ((uint32_t)iw < g.in_w) a.add(row[iw]);
-                }
+    int16_t* yp = y + plane * (g.out_h * g.out_w);
+    if constexpr (KW > 0) {
+        // interior: lane's first output (r, c) of the rectangle, then +64 per step
+        uint32_t r = fdiv(lane, p.div_iw);
+        uint32_t c = lane - r * p.iw_n;
+        int32_t a = (int32_t)(((p.oh_lo + r) * g.sh - g.pt) * g.in_w + (p.ow_lo + c) * g.sw - g.pl);
+        uint32_t oo = (p.oh_lo + r) * g.out_w + p.ow_lo + c;
+        for (uint32_t i = lane; i < p.n_int; i += 64) {
+            yp[oo] = window_inside<KIND, KW>(t + a, g.in_w, inv_full);
+            c += p.dc;
+            a += p.step_a;
+            oo += p.step_o;
+            if (c >= p.iw_n) {
+                c -= p.iw_n;
+                a += p.wrap_a;
+                oo += p.wrap_o;
             }
         }
-        float inv = inv_full;
-        if constexpr (KIND == K_AVG) {
-            if (!g.cip) inv = q88::inv_denom(vh * (uint32_t)valid_taps(iw0, (int32_t)g.pw, (int32_t)g.dw,
-                                                                       (int32_t)g.in_w));
+        // ring: outputs above the interior, beside its rows, below it
+        for (uint32_t k = lane; k < p.n_ring; k += 64) {
+            uint32_t oh, ow;
+            if (k < p.top_n) {
+                oh = fdiv(k, p.div_ow);
+                ow = k - oh * g.out_w;
+            } else if (k < p.top_n + p.mid_n) {
+                const uint32_t j = k - p.top_n, rr = fdiv(j, p.div_side), cc = j - rr * p.side;
+                oh = p.oh_lo + rr;
+                ow = cc < p.ow_lo ? cc : cc + p.iw_n;
+            } else {
+                const uint32_t j = k - p.top_n - p.mid_n, rr = fdiv(j, p.div_ow);
+                oh = p.oh_hi + rr;
+                ow = j - rr * g.out_w;
+            }
+            yp[oh * g.out_w + ow] = window_checked<KIND, KW>(t, g, oh, ow, inv_full);
         }
-        yp[o] = a.finish(inv);
+    } else {
+        const uint32_t ohw = g.out_h * g.out_w;
+        for (uint32_t o = lane; o < ohw; o += 64) {
+            const uint32_t oh = fdiv(o, p.div_ow), ow = o - oh * g.out_w;
+            yp[o] = window_checked<KIND, 0>(t, g, oh, ow, inv_full);
+        }
     }
+}
+
+// Interior rectangle and ring of a plane for a KW x KW window (dilation 1);
+// kw == 0: no interior (every output takes the checked path).
+PlaneGeom plane_geom(const PoolGeom& g, uint32_t kw) {
+    PlaneGeom p{};
+    auto range = [&](uint32_t in, uint32_t out, uint32_t s, uint32_t pad, uint32_t& lo, uint32_t& hi) {
+        // o is inside iff o * s >= pad and o * s - pad + kw <= in
+        lo = (pad + s - 1) / s;
+        const uint64_t top = (uint64_t)in + pad;
+        hi = top >= kw ? (uint32_t)std::min<uint64_t>(out, (top - kw) / s + 1) : 0u;
+        if (hi < lo) hi = lo;
+    };
+    uint32_t ow_hi = 0;
+    if (kw > 0) {
+        range(g.in_h, g.out_h, g.sh, g.pt, p.oh_lo, p.oh_hi);
+        range(g.in_w, g.out_w, g.sw, g.pl, p.ow_lo, ow_hi);
+    }
+    if (kw == 0 || p.oh_hi <= p.oh_lo || ow_hi <= p.ow_lo) {
+        p.oh_lo = p.oh_hi = g.out_h;   // empty interior: the "top" part of the ring is everything
+        p.ow_lo = ow_hi = 0;
+    }
+    p.iw_n = ow_hi - p.ow_lo;
+    const uint32_t ih_n = p.oh_hi - p.oh_lo;
+    p.n_int = ih_n * p.iw_n;
+    p.n_ring = g.out_h * g.out_w - p.n_int;
+    p.top_n = p.oh_lo * g.out_w;
+    p.side = g.out_w - p.iw_n;
+    p.mid_n = ih_n * p.side;
+    if (p.iw_n > 0) {
+        const uint32_t dr = 64 / p.iw_n;
+        p.dc = 64 % p.iw_n;
+        p.step_a = (int32_t)(dr * g.sh * g.in_w + p.dc * g.sw);
+        p.wrap_a = (int32_t)(g.sh * g.in_w) - (int32_t)(p.iw_n * g.sw);
+        p.step_o = dr * g.out_w + p.dc;
+        p.wrap_o = g.out_w - p.iw_n;
+    }
+    p.div_iw = make_fastdiv(p.iw_n);
+    p.div_ow = make_fastdiv(g.out_w);
+    p.div_side = make_fastdiv(p.side);
+    return p;
 }
 
 // ---------------------------------------------------------------- direct --
@@ -797,16 +950,16 @@ int pool_launch(const int16_t* x, int16_t* y, uint64_t planes, const PoolGeom& g
         if (blocks <= 0x7FFFFFFFull) {
             const uint32_t vec = ((uint64_t)g.in_h * g.in_w) % 8 == 0 && (((uintptr_t)x & 15u) == 0);
             const uint32_t kwp = g.dh == 1 && g.dw == 1 && g.ph == g.pw && (g.ph == 2 || g.ph == 3) ? g.ph : 0;
-            const FastDiv dow = make_fastdiv(g.out_w);
+            const PlaneGeom pg = plane_geom(g, kwp);
             if (kwp == 3)
                 hipLaunchKernelGGL((pool_plane<KIND, 3>), dim3((uint32_t)blocks), dim3(kThreads), 0, s, x, y,
-                                   g, planes, vec, inv_full, dow);
+                                   g, pg, planes, vec, inv_full);
             else if (kwp == 2)
                 hipLaunchKernelGGL((pool_plane<KIND, 2>), dim3((uint32_t)blocks), dim3(kThreads), 0, s, x, y,
-                                   g, planes, vec, inv_full, dow);
+                                   g, pg, planes, vec, inv_full);
             else
                 hipLaunchKernelGGL((pool_plane<KIND, 0>), dim3((uint32_t)blocks), dim3(kThreads), 0, s, x, y,
-                                   g, planes, vec, inv_full, dow);
+                                   g, pg, planes, vec, inv_full);
             return cm_check_launch("pool_plane");
         }
     }

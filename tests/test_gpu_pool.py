@@ -109,3 +109,30 @@ def test_strip_path_random(seed):
     x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
     got, want = pool_both(x, N, C, H, W, OH, OW, k, k, sh, sw, pt, pl, 1, 1, ptype, lp, cip)
     np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_plane_path_random(seed):
+    """Random shapes on the wave-per-plane path (planes of at most 2048 elements):
+    2x2 / 3x3 windows (interior rectangle + border ring) and other windows,
+    independent row / column strides and pads (some windows wholly in padding),
+    plane sizes that are and are not multiples of 8, plane counts not a multiple
+    of 4, every pool type, full-range values."""
+    g = wl.rng(812, seed)
+    k = int(g.choice([2, 3, 3, 4]))
+    kw = k if g.integers(0, 4) else int(g.choice([1, 2, 3]))
+    sh, sw = int(g.integers(1, 4)), int(g.integers(1, 4))
+    pt, pl = int(g.integers(0, k + 1)), int(g.integers(0, kw + 1))
+    H = int(g.integers(1, 45))
+    W = int(g.integers(1, max(2, min(64, 2048 // H))))
+    H, W = max(H, k - 2 * pt, 1), max(W, kw - 2 * pl, 1)
+    N, C = int(g.integers(1, 4)), int(g.integers(1, 23))
+    ptype, lp = [(0, 0), (1, 0), (2, 1), (2, 2)][int(g.integers(0, 4))]
+    cip = int(g.integers(0, 2)) if ptype == 1 else 0
+    OH = (H + 2 * pt - k) // sh + 1
+    OW = (W + 2 * pl - kw) // sw + 1
+    say(f"pool plane random seed {seed}: {(N, C, H, W, k, kw, sh, sw, pt, pl, ptype, lp, cip)}")
+    assert H * W <= 2048 and OH >= 1 and OW >= 1
+    x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
+    got, want = pool_both(x, N, C, H, W, OH, OW, k, kw, sh, sw, pt, pl, 1, 1, ptype, lp, cip)
+    np.testing.assert_array_equal(got, want)
