@@ -41,6 +41,7 @@ inline EpiArgs cm_epi_args(const cm_epilogue_t* e) {
     return e ? EpiArgs{e->add, e->add_mode, e->act} : EpiArgs{nullptr, 0u, 0u};
 }
 int cm_check_launch(const char* what);
+uint32_t cm_cu_count();   // compute units of the current device (cached per device)
 
 // Division of any n < 2^31 by a fixed d >= 1 as a multiply and shift
 // (Granlund-Montgomery, the round-up variant): l = ceil(log2 d), p = 31 + l,

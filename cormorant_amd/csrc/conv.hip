@@ -18,6 +18,8 @@
 #include "cm_internal.h"
 #include "q88.h"
 
+#include <algorithm>
+
 int cm_conv_gemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
                         uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
                         uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
@@ -36,11 +38,264 @@ namespace {
 
 constexpr int kThreads = 256;
 
+// ---------------------------------------------------------------- depthwise --
+// Output channel m of image n reads input channel m of image n through its own
+// kh x kw filter (ConvKernel.cpp:251-319).  Work item = (image, channel, band of
+// `band_h` output rows); one block per item.  The block stages the band's
+// input rows in LDS with their zero padding -- tile row i holds input row
+// ih_lo + i, tile column j holds input column j - cofs, out-of-range
+// positions hold 0 -- so every tap reads LDS without a bounds check (a zero
+// tap adds nothing to the wrapping sum, exactly like the reference's skipped
+// tap).  Global reads are range-checked buffer loads (16-byte vectors when
+// input rows are whole vectors), issued in batches before any is written to
+// LDS.  A thread then owns one output column and a segment of the band's rows;
+// for a 3x3 filter with row stride 1 it slides a 3-row window down the
+// column, reading one new tile row per output.  The filter is block-uniform:
+// its taps are scalar loads.  Products of two int16 values accumulate in
+// uint32, wrapping mod 2^32 like AccData_t.
+constexpr uint32_t kDwLdsBytes = 48u << 10;   // tile budget per block
+constexpr int kDwBatch = 2;                   // staging loads in flight per thread and pass
+
+struct DwBand {
+    const int16_t* x;
+    const int16_t* w;
+    const int16_t* bias;
+    int16_t* y;
+    EpiArgs epi;
+    uint32_t C, M, H, W, OH, OW, kh, kw, sh, sw, dh, dw, pt, pl;
+    uint32_t band_h, n_bands;
+    uint32_t pp, n_groups;        // channels (planes) per item, channel groups per image
+    uint32_t pitch, cofs, rows;   // one plane's tile: rows x pitch elements, input column 0 at
+                                  // cofs; a block stacks pp of them
+    uint32_t vec;                 // 16-byte staging (W % 8 == 0, cofs and pitch % 8 == 0, x aligned)
+    uint32_t units, gdr, gdj;     // staging units per tile row (pitch / 8 or pitch); a thread's
+                                  // next unit is gdr rows and gdj units on (kThreads = gdr * units + gdj)
+    uint32_t segs;                // row segments per column when pp * OW < kThreads, else 0
+    FastDiv div_bands, div_groups, div_ow, div_units, div_cols, div_rows;   // div_cols: pp * OW
+};
+
+// Stage the input rows [ih_lo, ih_lo + rows) of planes 0..np-1 (consecutive
+// channels, plane j at element j * plane of the resource): stacked tile row
+// j * rows + r, unit u covers tile columns [u * E, u * E + E) (E = 8 for
+// 16-byte units, else 1).
+template <int E>
+__device__ __forceinline__ void dw_stage(const DwBand& g, int16_t* tile, const __amdgpu_buffer_rsrc_t rs,
+                                         int32_t ih_lo, uint32_t rows, const FastDiv& div_rows,
+                                         uint32_t np) {
+    typedef short v8s __attribute__((ext_vector_type(8)));
+    const uint32_t n = np * rows * g.units, plane = g.H * g.W;
+    uint32_t rr = fdiv(threadIdx.x, g.div_units);   // stacked row j * rows + r
+    uint32_t u = threadIdx.x - rr * g.units;
+    for (uint32_t base = 0; base < n; base += kThreads * kDwBatch) {
+        uint32_t off[kDwBatch], dst[kDwBatch];
+#pragma unroll
+        for (int k = 0; k < kDwBatch; ++k) {
+            const uint32_t j = fdiv(rr, div_rows), r = rr - j * rows;   // plane, row within it
+            const int32_t ih = ih_lo + (int32_t)r, iw = (int32_t)(u * E) - (int32_t)g.cofs;
+            const bool in = j < np;
+            const bool ok = in && (uint32_t)ih < g.H && (uint32_t)iw < g.W;
+            off[k] = ok ? (j * plane + (uint32_t)ih * g.W + (uint32_t)iw) * 2u : kOob;
+            dst[k] = in ? rr * g.units + u : 0xFFFFFFFFu;
+            rr += g.gdr;
+            u += g.gdj;
+            if (u >= g.units) {
+                u -= g.units;
+                ++rr;
+            }
+        }
+        if constexpr (E == 8) {
+            v8s d[kDwBatch];
+#pragma unroll
+            for (int k = 0; k < kDwBatch; ++k)
+                d[k] = __builtin_bit_cast(v8s, __builtin_amdgcn_raw_buffer_load_b128(rs, off[k], 0, 0));
+#pragma unroll
+            for (int k = 0; k < kDwBatch; ++k)
+                if (dst[k] != 0xFFFFFFFFu) *reinterpret_cast<v8s*>(tile + dst[k] * 8) = d[k];
+        } else {
+            int16_t d[kDwBatch];
+#pragma unroll
+            for (int k = 0; k < kDwBatch; ++k) d[k] = (int16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off[k], 0, 0);
+#pragma unroll
+            for (int k = 0; k < kDwBatch; ++k)
+                if (dst[k] != 0xFFFFFFFFu) tile[dst[k]] = d[k];
+        }
+    }
+}
+
+template <int K, bool HAS_BIAS>   // K > 0: a K x K filter with dilation 1
+__global__ __launch_bounds__(kThreads) void conv_dw_band(DwBand g) {
+    extern __shared__ __align__(16) int16_t tile[];
+    // volatile: element reads, never paired into unaligned 4-byte reads
+    typedef __attribute__((address_space(3))) const volatile int16_t lds_i16;
+    const uint32_t item = blockIdx.x;
+    const uint32_t ng = fdiv(item, g.div_bands);        // n * n_groups + channel group
+    const uint32_t band = item - ng * g.n_bands;
+    const uint32_t n = fdiv(ng, g.div_groups);
+    const uint32_t m0 = (ng - n * g.n_groups) * g.pp;
+    const uint32_t np = min(g.pp, g.M - m0);
+    const uint32_t oh0 = band * g.band_h;
+    const uint32_t bh = min(g.band_h, g.OH - oh0);
+    const int32_t ih_lo = (int32_t)(oh0 * g.sh) - (int32_t)g.pt;
+    const uint32_t plane = g.H * g.W;
+    const int16_t* xc = g.x + ((uint64_t)n * g.C + m0) * plane;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(xc, np * plane * 2u);
+    // A thread owns one column of one plane and a segment of the band's rows
+    // (or, when the block has >= kThreads columns, every kThreads-th column
+    // over all rows).  Column q of the block is column q % OW of plane q / OW.
+    const uint32_t ncols = g.pp * g.OW;
+    uint32_t q0 = threadIdx.x, qstep = kThreads, ra = 0, rb = bh;
+    if (g.segs > 0) {
+        const uint32_t sgi = fdiv(threadIdx.x, g.div_cols);
+        q0 = threadIdx.x - sgi * ncols;
+        qstep = ncols;   // one column
+        const uint32_t rps = (bh + g.segs - 1) / g.segs;
+        ra = min(bh, sgi * rps);
+        rb = sgi < g.segs ? min(bh, ra + rps) : ra;
+    }
+    // the first column's filter and bias load while the tile stages
+    int32_t wk[K > 0 ? K * K : 1];
+    uint32_t acc0 = 0, jl = 0xFFFFFFFFu;
+    auto load_filter = [&](uint32_t j) {
+        if constexpr (K > 0) {
+            const int16_t* wm = g.w + (uint64_t)(m0 + j) * (K * K);
+#pragma unroll
+            for (int t = 0; t < K * K; ++t) wk[t] = wm[t];
+        }
+        acc0 = HAS_BIAS ? q88::data_to_acc(g.bias[m0 + j]) : 0u;
+        jl = j;
+    };
+    if (g.pp == 1) {
+        load_filter(0u);   // block-uniform: scalar loads
+    } else if (q0 < ncols) {
+        const uint32_t j = fdiv(q0, g.div_ow);
+        if (j < np) load_filter(j);
+    }
+    // every band stages g.rows rows per plane (the last band's extra rows are
+    // never read), so the stacked layout is the same for all items
+    if (g.vec) dw_stage<8>(g, tile, rs, ih_lo, g.rows, g.div_rows, np);
+    else dw_stage<1>(g, tile, rs, ih_lo, g.rows, g.div_rows, np);
+    __syncthreads();
+    const int32_t lo = q88::act_lo(g.epi.act), hi = q88::act_hi(g.epi.act);
+    const uint32_t pitch = g.pitch, rstep = g.sh * pitch;
+    for (uint32_t q = q0; q < ncols; q += qstep) {
+        const uint32_t j = fdiv(q, g.div_ow), c = q - j * g.OW;
+        if (j >= np) break;   // q only grows
+        if (j != jl) load_filter(j);
+        const uint32_t m = m0 + j;
+        const int16_t* wm = g.w + (uint64_t)m * g.kh * g.kw;
+        const uint64_t ybase = (((uint64_t)n * g.M + m) * g.OH + oh0) * g.OW;
+        int16_t* yb = g.y + ybase;
+        const int16_t* addb = g.epi.add_mode == 1u ? g.epi.add + ybase : nullptr;
+        const int16_t* tp = tile + j * g.rows * pitch + c * g.sw + (g.cofs - g.pl);
+        if constexpr (K > 0) {
+            if (g.sh == 1) {
+                // sliding window down the column: each output row reads one new tile row
+                int32_t v[K][K];
+                lds_i16* t = (lds_i16*)(tp + ra * pitch);
+#pragma unroll
+                for (int khi = 0; khi < K - 1; ++khi)
+#pragma unroll
+                    for (int kwi = 0; kwi < K; ++kwi) v[khi + 1][kwi] = t[khi * pitch + kwi];
+                t += (K - 1) * pitch;
+                for (uint32_t r = ra; r < rb; ++r) {
+#pragma unroll
+                    for (int khi = 0; khi < K - 1; ++khi)
+#pragma unroll
+                        for (int kwi = 0; kwi < K; ++kwi) v[khi][kwi] = v[khi + 1][kwi];
+#pragma unroll
+                    for (int kwi = 0; kwi < K; ++kwi) v[K - 1][kwi] = t[kwi];
+                    t += pitch;
+                    uint32_t acc = acc0;
+#pragma unroll
+                    for (int khi = 0; khi < K; ++khi)
+#pragma unroll
+                        for (int kwi = 0; kwi < K; ++kwi) acc += (uint32_t)(v[khi][kwi] * wk[khi * K + kwi]);
+                    int32_t o = q88::acc_to_data(acc);
+                    if (addb) o = q88::add(o, addb[r * g.OW + c]);
+                    yb[r * g.OW + c] = (int16_t)q88::clamp(o, lo, hi);
+                }
+                continue;
+            }
+        }
+        for (uint32_t r = ra; r < rb; ++r) {
+            lds_i16* t = (lds_i16*)(tp + r * rstep);
+            uint32_t acc = acc0;
+            if constexpr (K > 0) {
+#pragma unroll
+                for (int khi = 0; khi < K; ++khi)
+#pragma unroll
+                    for (int kwi = 0; kwi < K; ++kwi)
+                        acc += (uint32_t)((int32_t)t[khi * pitch + kwi] * wk[khi * K + kwi]);
+            } else {
+                for (uint32_t khi = 0; khi < g.kh; ++khi) {
+                    lds_i16* tr = t + khi * g.dh * pitch;
+                    const int16_t* wr = wm + khi * g.kw;
+                    for (uint32_t kwi = 0; kwi < g.kw; ++kwi)
+                        acc += (uint32_t)((int32_t)tr[kwi * g.dw] * (int32_t)wr[kwi]);
+                }
+            }
+            int32_t o = q88::acc_to_data(acc);
+            if (addb) o = q88::add(o, addb[r * g.OW + c]);
+            yb[r * g.OW + c] = (int16_t)q88::clamp(o, lo, hi);
+        }
+    }
+}
+
+// Band geometry of a depthwise convolution; false when one output row's input
+// rows do not fit the LDS budget or indices leave 32-bit range (the per-output
+// kernel below takes those shapes).
+bool dw_band_geom(DwBand& g, uint64_t batch, uintptr_t xaddr) {
+    const uint64_t iw_max = (uint64_t)(g.OW - 1) * g.sw + (uint64_t)(g.kw - 1) * g.dw;   // + pl offset
+    const uint64_t planes = batch * g.M;
+    if ((uint64_t)g.H * g.W >= (1u << 26) || g.OW >= (1u << 24) || g.OH >= (1u << 24) || g.pl >= (1u << 20) ||
+        iw_max >= (1u << 24) || planes >= (1u << 30) ||
+        (uint64_t)g.OH * g.sh + g.pt + (uint64_t)g.kh * g.dh >= (1u << 30))
+        return false;
+    g.cofs = (g.pl + 7) & ~7u;
+    const uint64_t need_cols = std::max<uint64_t>(g.W, iw_max + 1 > g.pl ? iw_max + 1 - g.pl : 0);
+    const uint64_t pitch = (g.cofs + need_cols + 7) & ~7ull;
+    auto rows_of = [&](uint64_t bh) { return (bh - 1) * g.sh + (uint64_t)(g.kh - 1) * g.dh + 1; };
+    if (rows_of(1) * pitch * 2 > kDwLdsBytes) return false;
+    g.pitch = (uint32_t)pitch;
+    // About four outputs per thread, as long as the grid keeps four blocks per
+    // CU: bands of one plane's rows, or, when a whole plane is fewer outputs
+    // than that, several consecutive channels' planes per block.
+    const uint64_t want = 4ull * cm_cu_count(), per_block = 4ull * kThreads;
+    uint64_t bh = std::min<uint64_t>(g.OH, (per_block + g.OW - 1) / g.OW);
+    while (bh > 1 && planes * ((g.OH + bh - 1) / bh) < want) bh = (bh + 1) / 2;
+    while (bh > 1 && rows_of(bh) * pitch * 2 > kDwLdsBytes) --bh;
+    g.band_h = (uint32_t)std::max<uint64_t>(bh, 1);
+    g.n_bands = (g.OH + g.band_h - 1) / g.band_h;
+    g.rows = (uint32_t)rows_of(g.band_h);
+    uint64_t pp = 1;
+    if (g.n_bands == 1) {
+        const uint64_t outs = (uint64_t)g.OH * g.OW, tile_bytes = (uint64_t)g.rows * pitch * 2;
+        pp = std::max<uint64_t>(1, std::min<uint64_t>({per_block / outs, (uint64_t)g.M, kDwLdsBytes / tile_bytes}));
+        while (pp > 1 && batch * ((g.M + pp - 1) / pp) < want) pp = (pp + 1) / 2;
+    }
+    g.pp = (uint32_t)pp;
+    g.n_groups = (uint32_t)((g.M + pp - 1) / pp);
+    if (batch * g.n_groups * g.n_bands > 0x7FFFFFFFull || pp * g.H * g.W >= (1u << 30)) return false;
+    g.vec = g.W % 8 == 0 && (xaddr & 15u) == 0;
+    g.units = g.vec ? g.pitch / 8 : g.pitch;
+    g.gdr = kThreads / g.units;
+    g.gdj = kThreads % g.units;
+    const uint64_t ncols = pp * g.OW;
+    g.segs = ncols < kThreads ? (uint32_t)(kThreads / ncols) : 0u;
+    g.div_bands = make_fastdiv(g.n_bands);
+    g.div_groups = make_fastdiv(g.n_groups);
+    g.div_ow = make_fastdiv(g.OW);
+    g.div_units = make_fastdiv(g.units);
+    g.div_rows = make_fastdiv(g.rows);
+    g.div_cols = make_fastdiv((uint32_t)std::min<uint64_t>(ncols, 0x7FFFFFFF));
+    return true;
+}
+
 struct DwGeom {
     uint32_t in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, sh, sw, dh, dw, pt, pl;
 };
 
-// Depthwise: output channel m reads input channel m of the same image.
+// Per-output fallback for rows too wide for the band tile: one thread per output.
 template <bool HAS_BIAS>
 __global__ __launch_bounds__(kThreads) void conv_depthwise(const int16_t* __restrict__ x,
                                                            const int16_t* __restrict__ w,
@@ -312,6 +567,20 @@ int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int1
     if (is_dw) {
         const uint64_t total = (uint64_t)batch * out_ch * out_h * out_w;
         if (total == 0 || lc.need) return CM_OK;
+        DwBand bg{};
+        bg.x = x; bg.w = w; bg.bias = b; bg.y = y; bg.epi = ea;
+        bg.C = in_ch; bg.M = out_ch; bg.H = in_h; bg.W = in_w; bg.OH = out_h; bg.OW = out_w;
+        bg.kh = kh; bg.kw = kw; bg.sh = sh; bg.sw = sw; bg.dh = dh; bg.dw = dw; bg.pt = pad_top; bg.pl = pad_left;
+        if (dw_band_geom(bg, batch, (uintptr_t)x)) {
+            const dim3 grid((uint32_t)((uint64_t)batch * bg.n_groups * bg.n_bands));
+            const size_t lds = (size_t)bg.pp * bg.rows * bg.pitch * 2;
+            const bool k3 = kh == 3 && kw == 3 && dh == 1 && dw == 1;
+            if (k3 && b) hipLaunchKernelGGL((conv_dw_band<3, true>), grid, dim3(kThreads), lds, s, bg);
+            else if (k3) hipLaunchKernelGGL((conv_dw_band<3, false>), grid, dim3(kThreads), lds, s, bg);
+            else if (b) hipLaunchKernelGGL((conv_dw_band<0, true>), grid, dim3(kThreads), lds, s, bg);
+            else hipLaunchKernelGGL((conv_dw_band<0, false>), grid, dim3(kThreads), lds, s, bg);
+            return cm_check_launch("conv_dw_band");
+        }
         DwGeom g{in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, sh, sw, dh, dw, pad_top, pad_left};
         const dim3 grid((uint32_t)cm_grid_blocks(total, kThreads));
         if (b) hipLaunchKernelGGL(conv_depthwise<true>, grid, dim3(kThreads), 0, s, x, w, b, y, g, total, ea);

@@ -717,6 +717,8 @@ constexpr uint64_t kPgLdsMax = 78u * 1024u;   // dynamic LDS per block: two bloc
 
 }  // namespace
 
+uint32_t cm_cu_count() { return cu_count(); }
+
 namespace {
 
 enum PgMode { kPackAndRun, kPackOnly, kRunPacked };

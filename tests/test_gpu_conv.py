@@ -312,3 +312,83 @@ def test_conv_packed_rejects_other_paths():
     assert K.conv_packed_size(*ok) > 64
     with pytest.raises(_native.CmError):
         K.conv_pack(w, buf, *ok)   # 64 bytes is too small
+
+
+DW_CASES = [
+    # N, C, H, W, M, kh, kw, sh, sw, dh, dw, pt, pl, bias
+    (1, 32, 28, 28, 32, 3, 3, 1, 1, 1, 1, 1, 1, 0),      # perf case dw-3x3-32ch-28x28
+    (1, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1, 1, 0),      # perf case dw-3x3-64ch-56x56
+    (16, 32, 112, 112, 32, 3, 3, 1, 1, 1, 1, 1, 1, 1),   # MobileNetV2's first depthwise layer
+    (4, 96, 56, 56, 96, 3, 3, 2, 2, 1, 1, 1, 1, 1),      # stride 2 (16-byte staging)
+    (2, 40, 15, 17, 40, 3, 3, 2, 2, 1, 1, 0, 1, 1),      # element staging, asymmetric pads
+    (2, 24, 9, 40, 20, 5, 5, 1, 2, 2, 1, 3, 2, 1),       # general taps, dilation, out_ch < in_ch
+    (1, 3, 4, 9000, 3, 3, 3, 1, 1, 1, 1, 1, 1, 1),       # rows too wide for the tile: per-output kernel
+    (3, 5, 7, 7, 5, 7, 7, 1, 1, 1, 1, 3, 3, 0),          # a window as large as the plane
+    # several channels' planes per block (small planes, many of them)
+    (8, 255, 14, 14, 255, 3, 3, 1, 1, 1, 1, 1, 1, 1),    # 2 per block, a partial last group
+    (16, 192, 8, 8, 192, 3, 3, 1, 1, 1, 1, 1, 1, 0),     # 16-byte staging
+    (16, 400, 7, 7, 399, 3, 3, 2, 2, 1, 1, 1, 1, 1),     # stride 2, out_ch < in_ch, partial group
+]
+
+
+def dw_run(geom, seed, add_act=None):
+    N, C, H, W, M, kh, kw, sh, sw, dh, dw, pt, pl, bias = geom
+    OH = (H + 2 * pt - dh * (kh - 1) - 1) // sh + 1
+    OW = (W + 2 * pl - dw * (kw - 1) - 1) // sw + 1
+    g = wl.rng(835, seed, *geom)
+    x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
+    w = g.integers(-32768, 32768, M * kh * kw, dtype=np.int16)
+    b = g.integers(-32768, 32768, M, dtype=np.int16)
+    args = (N, C, H, W, M, OH, OW, kh, kw, sh, sw, dh, dw, pt, pl, bias, 1)
+    want = np.zeros(N * M * OH * OW, np.int16)
+    oracle.set_threads(oracle_threads())
+    oracle.conv(x, w, b, want, *args, threads=True)
+    y = empty_dev(want.size)
+    if add_act is None:
+        K.ConvKernel(dev(x), dev(w), dev(b), y, *args)
+        return host(y), want
+    add = g.integers(-32768, 32768, want.size, dtype=np.int16)
+    K.ConvKernel(dev(x), dev(w), dev(b), y, *args, add=dev(add), act=add_act)
+    exp = np.clip(want.astype(np.int32) + add, -32768, 32767)
+    if add_act != K.ACT_NONE:
+        exp = np.clip(exp, 0, 32767 if add_act == K.ACT_RELU else 1536)
+    return host(y).astype(np.int32), exp
+
+
+@pytest.mark.parametrize("geom", DW_CASES, ids=[str(g) for g in DW_CASES])
+def test_depthwise_cases(geom):
+    """Depthwise on the band kernel (3x3 taps unrolled, general taps, 16-byte and
+    element staging) and the per-output kernel, full-range values that wrap."""
+    say(f"depthwise {geom}")
+    got, want = dw_run(geom, 0)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("act", [0, 1, 2])
+def test_depthwise_fused_epilogue(act):
+    """y = act(sat16(conv + add)) on the band kernel."""
+    say(f"depthwise epilogue act={act}")
+    got, want = dw_run((2, 32, 28, 28, 32, 3, 3, 1, 1, 1, 1, 1, 1, 1), 1, add_act=act)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_depthwise_random(seed):
+    """Random depthwise shapes: square and non-square filters, strides, dilations,
+    pads up to and past the window, widths with and without whole 16-byte rows."""
+    g = wl.rng(836, seed)
+    kh, kw = int(g.integers(1, 6)), int(g.integers(1, 6))
+    if g.integers(0, 2):
+        kw = kh = 3
+    sh, sw = int(g.integers(1, 4)), int(g.integers(1, 4))
+    dh, dw = (1, 1) if g.integers(0, 2) else (int(g.integers(1, 3)), int(g.integers(1, 3)))
+    pt, pl = int(g.integers(0, kh + 1)), int(g.integers(0, kw + 1))
+    H = int(g.integers(max(1, dh * (kh - 1) + 1 - 2 * pt), 70))
+    W = 8 * int(g.integers(1, 12)) if g.integers(0, 2) else int(g.integers(max(1, dw * (kw - 1) + 1 - 2 * pl), 90))
+    C = int(g.integers(1, 40))
+    M = int(g.integers(1, C + 1))
+    N = int(g.integers(1, 4))
+    geom = (N, C, H, W, M, kh, kw, sh, sw, dh, dw, pt, pl, int(g.integers(0, 2)))
+    say(f"depthwise random seed {seed}: {geom}")
+    got, want = dw_run(geom, seed)
+    np.testing.assert_array_equal(got, want)
