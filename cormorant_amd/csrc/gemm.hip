@@ -22,9 +22,8 @@
 // wave tile 64 x 32 = 4 x 2 MFMA 16x16x64 tiles with 3 accumulator sets (hh,
 // mid, ll): 96 accumulator registers, so two waves share each SIMD and one
 // wave's MFMAs run while the other waits on memory or does its limb split.
-// Tiles are split into limbs while being stored to LDS (rows of 64 int8 k
-// values, padded to 80 B so the 16 lanes of a fragment read hit distinct
-// banks).  The next tile's loads are issued before the MFMA phase; loads are
+// Tiles are split into limbs while being stored to LDS (see Planes for the
+// layouts and their bank conflicts).  The next tile's loads are issued before the MFMA phase; loads are
 // unconditional (out-of-range elements are zeroed by the buffer range check
 // or by a select), so all of a tile's loads are in flight at once.
 #include <type_traits>
@@ -41,7 +40,8 @@ typedef unsigned int v2u __attribute__((ext_vector_type(2)));
 
 constexpr int BM = 128, BN = 128, BK = 64;
 constexpr int kThreads = 512;
-constexpr int kStride = 80;          // LDS bytes per row of 64 int8 (k) values
+constexpr int kChunk = BM * 16;      // A planes: LDS bytes of one 16-byte k chunk of all 128 rows
+constexpr int kStride = 80;          // B planes: LDS bytes per column of 64 int8 (k) values
 constexpr int kFoldIters = 512;      // fold MFMA partials every 512*64 = 32768 k
 constexpr int TI = 4, TJ = 2;        // MFMA tiles per wave: 4 row tiles x 2 column tiles
 constexpr uint32_t kTabMax = 2048;   // largest K of the table-driven convolution gather
@@ -93,12 +93,32 @@ __device__ __forceinline__ uint32_t pack(uint32_t lo, uint32_t hi) {
 
 // One k step's limb planes.  Two of them alternate: the MFMA phase reads one
 // while the next tile is split into the other.
+// Limb planes of 128 rows (A) / columns (B) x 64 int8 k values.
+// A is chunk-major: k chunk q (16 bytes) of row r at q * kChunk + (r ^ 2q) * 16.
+// An MFMA fragment read (16 lanes: rows r0..r0+15 of one chunk) covers one
+// contiguous 256-byte block, and the staging stores (thread t: row t / 4,
+// chunk t % 4, so that a load quad reads one row) land in distinct banks: the
+// XOR moves the four chunks of a row pair to eight different 16-byte slots.  B keeps one 80-byte row per column: its staging
+// is 4-byte stores of 2 columns x 16 k words (paired into ds_write2, no
+// conflict); its fragment reads conflict.  Measured on single-pattern LDS
+// kernels with the bank-conflict counter: an 80-byte pitch costs 4 conflict
+// cycles per fragment read and 8 per 16-byte store of 4 chunks x 4 rows; the
+// chunk-major reads and stores cost none.  A chunk-major B (with an XOR of the
+// column by the chunk against the stores' conflicts) removed the rest of the
+// conflicts but ran 10 % slower: its addresses no longer pair into ds_write2
+// or fold into immediate offsets.
 struct Planes {
-    uint8_t a_hi[BM * kStride];
-    uint8_t a_lo[BM * kStride];
+    uint8_t a_hi[4 * kChunk];
+    uint8_t a_lo[4 * kChunk];
     uint8_t b_hi[BN * kStride];
     uint8_t b_lo[BN * kStride];
 };
+__device__ __forceinline__ uint32_t a_off(uint32_t r, uint32_t q) { return q * kChunk + ((r ^ (q << 1)) << 4); }
+
+// A staging: thread t owns row a_row(t) and k chunk a_chunk(t); the four threads
+// of a row are adjacent lanes, so each load quad reads one row's 128 bytes.
+__device__ __forceinline__ uint32_t a_row(uint32_t t) { return t >> 2; }
+__device__ __forceinline__ uint32_t a_chunk(uint32_t t) { return t & 3u; }
 
 // Epilogue tile: the block's 128 x 128 raw sums, rows padded to 132 words so
 // the four row groups of an MFMA result write fall into different bank halves.
@@ -133,7 +153,7 @@ __device__ __forceinline__ void store16(uint8_t* hi_plane, uint8_t* lo_plane, ui
 }
 
 // ---------------------------------------------------------------- A tile --
-// Thread t owns row t/4 and k values [16*(t&3), +16) of the 64-k slice.  The
+// Thread t owns row a_row(t) and k values [16 * a_chunk(t), +16) of the 64-k slice.  The
 // loads only fill registers (8 words for 16-byte loads, 16 raw values
 // otherwise); packing and the limb split happen in store(), after the MFMA
 // phase, so every load of a tile is in flight at once.
@@ -145,8 +165,8 @@ struct ATile {
     // the same row and are zeroed afterwards.
     __device__ __forceinline__ void load(const GemmArgs& g, const int16_t* abase, uint32_t row0,
                                          uint32_t k0) {
-        const uint32_t r = row0 + (threadIdx.x >> 2);
-        const uint32_t ks = k0 + (threadIdx.x & 3) * 16;
+        const uint32_t r = row0 + a_row(threadIdx.x);
+        const uint32_t ks = k0 + a_chunk(threadIdx.x) * 16;
         const bool rok = r < g.rows;
         const int16_t* p = abase + (uint64_t)(rok ? r : 0u) * g.lda;
         if (g.a_vec) {
@@ -172,8 +192,8 @@ struct ATile {
     template <bool VEC>
     __device__ __forceinline__ void load_buf(const GemmArgs& g, __amdgpu_buffer_rsrc_t ra,
                                              uint32_t row0, uint32_t k0) {
-        const uint32_t rel = threadIdx.x >> 2;
-        const uint32_t ks = k0 + (threadIdx.x & 3) * 16;
+        const uint32_t rel = a_row(threadIdx.x);
+        const uint32_t ks = k0 + a_chunk(threadIdx.x) * 16;
         const bool rok = row0 + rel < g.rows;
         const uint32_t rbyte = rel * (uint32_t)g.lda * 2u;
         if constexpr (VEC) {
@@ -212,7 +232,7 @@ struct ATile {
 #pragma unroll
             for (int j = 0; j < 8; ++j) w[j] = pack(raw[2 * j], raw[2 * j + 1]);
         }
-        store16(s.a_hi, s.a_lo, (threadIdx.x >> 2) * kStride + (threadIdx.x & 3) * 16, w, hs, ls);
+        store16(s.a_hi, s.a_lo, a_off(a_row(threadIdx.x), a_chunk(threadIdx.x)), w, hs, ls);
     }
 };
 
@@ -560,11 +580,11 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     // vector buffer paths: per-thread load offsets, the same for every k step
     uint32_t a_base[2], a_kc[2], b_off[4];
     {
-        const uint32_t rel = threadIdx.x >> 2;
+        const uint32_t rel = a_row(threadIdx.x);
         const bool rok = row0 + rel < g.rows;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
-            a_kc[q] = (threadIdx.x & 3) * 16 + q * 8;
+            a_kc[q] = a_chunk(threadIdx.x) * 16 + q * 8;
             a_base[q] = rok ? (rel * (uint32_t)g.lda + a_kc[q]) * 2u : kOob;
         }
         const uint32_t cr = (threadIdx.x >> 4) * 4, kr = (threadIdx.x & 15) * 4;
@@ -599,7 +619,7 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     // split can interleave with the MFMA phase.
     // convolution: weight rows past the last output channel are never stored,
     // so their limbs need not be staged (uniform per wave when M % 16 == 0)
-    const bool a_row_live = !CONV || row0 + (threadIdx.x >> 2) < g.rows;
+    const bool a_row_live = !CONV || row0 + a_row(threadIdx.x) < g.rows;
     auto stage_tile = [&](ATile& a, BTile& b, Planes& p, bool real) {
         int32_t h = 0, l = 0;
         if (a_row_live) a.store(AV == 0 ? g.a_vec != 0 : AV == 1, p, h, l);
@@ -636,17 +656,18 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     // the MFMAs of the wave's first NI row tiles (the others are left untouched)
     auto mfma_rows = [&](auto ni, const Planes& p, uint32_t it) {
         constexpr int NI = decltype(ni)::value;
-        const uint32_t koff = (lane >> 4) * 16;
+        const uint32_t kq = lane >> 4;
+        const uint32_t abase = a_off(wrow + (lane & 15), kq);   // wrow % 16 == 0: + i * 16 rows = + i * 256
         v4i ah[TI], al[TI];
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            const uint32_t r = (wrow + i * 16 + (lane & 15)) * kStride + koff;
+            const uint32_t r = abase + i * 256;
             ah[i] = *reinterpret_cast<const v4i*>(p.a_hi + r);
             al[i] = *reinterpret_cast<const v4i*>(p.a_lo + r);
         }
 #pragma unroll
         for (int j = 0; j < TJ; ++j) {
-            const uint32_t cidx = (wcol + j * 16 + (lane & 15)) * kStride + koff;
+            const uint32_t cidx = (wcol + j * 16 + (lane & 15)) * kStride + kq * 16;
             const v4i bh = *reinterpret_cast<const v4i*>(p.b_hi + cidx);
             const v4i bl = *reinterpret_cast<const v4i*>(p.b_lo + cidx);
 #pragma unroll
@@ -736,7 +757,7 @@ __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
     uint32_t row_sum = 256u * (uint32_t)row_hs + (uint32_t)row_ls + 128u * 16u * nk;
     row_sum += (uint32_t)__shfl_xor((int)row_sum, 1, 64);
     row_sum += (uint32_t)__shfl_xor((int)row_sum, 2, 64);
-    if ((threadIdx.x & 3) == 0) s.row_sum[threadIdx.x >> 2] = row_sum;
+    if (a_chunk(threadIdx.x) == 0) s.row_sum[a_row(threadIdx.x)] = row_sum;
     if constexpr (CONV)
         atomicAdd(&s.col_sum[threadIdx.x & 127], 256u * (uint32_t)chs + (uint32_t)cls + 128u * 16u * nk);
     else
