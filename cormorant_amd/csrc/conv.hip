@@ -7,12 +7,16 @@
 //     LDS, weights pre-split into limb planes; conv_pgemm.hip);
 //   * 3x3, <= 64 channels in and out, stride 1 or 2: conv_patch (input patch and
 //     all weights in LDS);
+//   * 1x1 / stride 1 / no padding, small layers (<= 2^21 outputs, in_ch <= 512):
+//     one wave per 32x32 output tile, fragments loaded straight into registers,
+//     no LDS (conv_pw.hip);
 //   * 1x1 / stride 1 / no padding, planes that fill 128-column tiles: batched
 //     GEMM Y[n] = W[out_ch][in_ch] x X[n][in_ch][h*w] on the int8-limb MFMA core;
 //   * any other: implicit GEMM on the same core, im2col gathered straight from
 //     NCHW x while the B tile is built (no im2col buffer);
-//   * depthwise (is_depthwise = 1, weights [out_ch][1][kh][kw]): direct kernel,
-//     one thread per output, uint32 wrapping accumulator (ConvKernel.cpp:251-319).
+//   * depthwise (is_depthwise = 1, weights [out_ch][1][kh][kw]): LDS band kernel
+//     (rows too wide for it: one thread per output), uint32 wrapping accumulator
+//     (ConvKernel.cpp:251-319).
 // All paths: acc = wrap32((has_bias ? bias << 8 : 0) + sum x*w), y = sat16(acc >> 8),
 // then the optional fused epilogue (Add of a same-shaped tensor, Relu / Relu6).
 #include "cm_internal.h"
@@ -28,6 +32,9 @@ int cm_conv_gemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias,
 int cm_conv_pointwise_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
                              uint32_t batch, uint32_t in_ch, uint32_t out_ch, uint32_t hw,
                              const cm_epilogue_t* epi, const LaunchCtx& lc);
+int cm_conv_pw_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
+                      uint32_t batch, uint32_t in_ch, uint32_t out_ch, uint32_t hw,
+                      const cm_epilogue_t* epi, const LaunchCtx& lc);
 int cm_conv_pgemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
                          uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
                          uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
@@ -637,13 +644,19 @@ int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int1
         const int rc = try_patch();
         if (rc != 1) return rc;
     }
-    // 1x1 / stride 1 / no padding as one GEMM per image, when an image's
-    // pixels fill its 128-column tiles to at least 80 %; small planes (e.g.
-    // 7x7, 14x14) go through the gather path, whose columns run across images
+    // 1x1 / stride 1 / no padding: small layers on the register-only MFMA kernel
+    // (conv_pw.hip); else one GEMM per image, when an image's pixels fill its
+    // 128-column tiles to at least 80 %; small planes (e.g. 7x7, 14x14) go
+    // through the gather path, whose columns run across images
     const uint64_t hw = (uint64_t)in_h * in_w;
     const uint64_t tiles = (hw + 127) / 128;
-    if (kh == 1 && kw == 1 && sh == 1 && sw == 1 && pad_top == 0 && pad_left == 0 &&
-        out_h == in_h && out_w == in_w && hw <= 0x7FFFFFFFull && (tiles * 128 - hw) * 5 <= tiles * 128)
+    const bool pointwise = kh == 1 && kw == 1 && sh == 1 && sw == 1 && pad_top == 0 && pad_left == 0 &&
+                           out_h == in_h && out_w == in_w && hw <= 0x7FFFFFFFull;
+    if (pointwise) {
+        const int rc = cm_conv_pw_launch(x, w, b, y, batch, in_ch, out_ch, (uint32_t)hw, epi, lc);
+        if (rc != 1) return rc;
+    }
+    if (pointwise && (tiles * 128 - hw) * 5 <= tiles * 128)
         return cm_conv_pointwise_launch(x, w, b, y, batch, in_ch, out_ch, (uint32_t)hw, epi, lc);
     return cm_conv_gemm_launch(x, w, b, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw,
                                sh, sw, dh, dw, pad_top, pad_left, epi, lc);

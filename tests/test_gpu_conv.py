@@ -392,3 +392,56 @@ def test_depthwise_random(seed):
     say(f"depthwise random seed {seed}: {geom}")
     got, want = dw_run(geom, seed)
     np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_pointwise_small_random(seed):
+    """Small 1x1 convolutions (<= 2^21 outputs, in_ch <= 512) on the register-only
+    MFMA kernel: channel counts that are and are not multiples of 8 / 32 / 64,
+    planes of 1..900 pixels, several images per 32-column tile, bias, fused Add
+    and activation, full-range values whose sums wrap."""
+    g = wl.rng(837, seed)
+    C = int(g.choice([1, 3, 8, 16, 24, 40, 64, 96, 100, 160, 320, 512]))
+    M = int(g.choice([1, 5, 16, 24, 32, 33, 64, 96, 160, 320]))
+    hw = int(g.choice([1, 3, 7, 14, 28, 30]))
+    N = int(g.integers(1, 17))
+    while M * N * hw * hw > (1 << 21):
+        N = max(1, N // 2)
+        if N == 1 and M * hw * hw > (1 << 21):
+            hw //= 2
+    bias, act = int(g.integers(0, 2)), int(g.integers(0, 3))
+    args = (N, C, hw, hw, M, hw, hw, 1, 1, 1, 1, 1, 1, 0, 0, bias, 0)
+    assert K.conv_workspace_size(*args) == 0
+    say(f"pointwise small seed {seed}: N={N} C={C} M={M} hw={hw} bias={bias} act={act}")
+    x = g.integers(-32768, 32768, N * C * hw * hw, dtype=np.int16)
+    w = g.integers(-32768, 32768, M * C, dtype=np.int16)
+    b = g.integers(-32768, 32768, M, dtype=np.int16)
+    add = g.integers(-32768, 32768, N * M * hw * hw, dtype=np.int16)
+    want = np.zeros(N * M * hw * hw, np.int16)
+    oracle.set_threads(oracle_threads())
+    oracle.conv(x, w, b, want, *args, threads=True)
+    y = empty_dev(want.size)
+    K.ConvKernel(dev(x), dev(w), dev(b), y, *args)
+    np.testing.assert_array_equal(host(y), want)
+    y2 = empty_dev(want.size)
+    K.ConvKernel(dev(x), dev(w), dev(b), y2, *args, add=dev(add), act=act)
+    exp = np.clip(want.astype(np.int32) + add, -32768, 32767)
+    if act:
+        exp = np.clip(exp, 0, 32767 if act == K.ACT_RELU else 1536)
+    np.testing.assert_array_equal(host(y2).astype(np.int32), exp)
+
+
+def test_pointwise_small_unaligned_weights():
+    """Weights at an odd element offset (no 16-byte loads) with in_ch % 8 == 0."""
+    g = wl.rng(838)
+    N, C, hw, M = 4, 64, 14, 48
+    args = (N, C, hw, hw, M, hw, hw, 1, 1, 1, 1, 1, 1, 0, 0, 1, 0)
+    x = g.integers(-32768, 32768, N * C * hw * hw, dtype=np.int16)
+    w = g.integers(-32768, 32768, M * C + 1, dtype=np.int16)
+    b = g.integers(-32768, 32768, M, dtype=np.int16)
+    want = np.zeros(N * M * hw * hw, np.int16)
+    oracle.conv(x, w[1:].copy(), b, want, *args)
+    dw_ = dev(w)[1:]
+    y = empty_dev(want.size)
+    K.ConvKernel(dev(x), dw_, dev(b), y, *args)
+    np.testing.assert_array_equal(host(y), want)
