@@ -125,10 +125,19 @@ __global__ __launch_bounds__(kThreads) void conv_pw(PwArgs g) {
         bcol[j] = col < g.NP ? (n * g.C * g.P + p) * 2u : kOob;
         yoff[j] = col < g.NP ? n * g.M * g.P + p : 0xFFFFFFFFu;
     }
-    // the fused Add's operand of every output this lane stores, loaded now so
-    // that its latency hides behind the k loop (loaded inside the store loop,
-    // each waited for the previous store)
-    uint32_t addv[2][4][2];
+    // the bias and the fused Add's operand of every output this lane stores,
+    // loaded now so that their latency hides behind the k loop (loaded in the
+    // epilogue they added a memory round trip to every launch: ~1.6 us)
+    uint32_t addv[2][4][2], biasv[2][4];
+    if constexpr (HAS_BIAS) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t m = rt * 32u + i * 16u + kg * 4u + (uint32_t)e;
+                biasv[i][e] = q88::data_to_acc(g.bias[m < g.M ? m : 0u]);
+            }
+    }
     if (g.epi.add_mode == 1u) {
         const __amdgpu_buffer_rsrc_t ar = make_rsrc(g.epi.add, g.y_bytes);
 #pragma unroll
@@ -217,7 +226,7 @@ __global__ __launch_bounds__(kThreads) void conv_pw(PwArgs g) {
             const uint32_t rs = (uint32_t)__shfl((int)rsum[i], (int)rr, 64);
             const uint32_t m = rt * 32u + i * 16u + rr;
             if (m >= g.M) continue;
-            const uint32_t b8 = HAS_BIAS ? q88::data_to_acc(g.bias[m]) : 0u;
+            const uint32_t b8 = HAS_BIAS ? biasv[i][e] : 0u;
 #pragma unroll
             for (int j = 0; j < 2; ++j) {
                 if (yoff[j] == 0xFFFFFFFFu) continue;

@@ -27,6 +27,7 @@ namespace {
 typedef short v8s __attribute__((ext_vector_type(8)));
 
 constexpr int kThreads = 256;
+constexpr int kNonTemporal = 2;   // buffer access cache policy: nt
 constexpr uint64_t kPoolBlocks = 2048;   // fallback: 256 CUs x 8 resident blocks of 256 threads
 
 struct PoolGeom {
@@ -85,20 +86,25 @@ __global__ __launch_bounds__(kThreads) void pool_global(const int16_t* __restric
     Acc<KIND> a;
     uint32_t done = 0;
     if (vec_ok) {
-        const v8s* xv = reinterpret_cast<const v8s*>(xp);
+        // range-checked buffer loads: past the plane they read 0 and touch no
+        // memory, so none needs a branch and all kBatch are in flight together
+        // (a guarded load became a branch with a wait for every earlier load);
+        // 0 adds nothing to a sum, and MAX masks those elements to -32768
         const uint32_t nv = hw / 8;
+        const __amdgpu_buffer_rsrc_t rs = make_rsrc(xp, nv * 16u);
         for (uint32_t base = 0; base < nv; base += 64 * kBatch) {
             v8s t[kBatch];
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                const uint32_t v = base + u * 64 + lane;
-                if (v < nv) t[u] = __builtin_nontemporal_load(xv + v);
-            }
+            for (int u = 0; u < kBatch; ++u)
+                t[u] = __builtin_bit_cast(v8s, __builtin_amdgcn_raw_buffer_load_b128(
+                                                   rs, (base + u * 64 + lane) * 16u, 0, kNonTemporal));
 #pragma unroll
             for (int u = 0; u < kBatch; ++u) {
-                if (base + u * 64 + lane < nv) {
+                const int32_t m = -(int32_t)(base + u * 64 + lane < nv);
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) a.add(t[u][j]);
+                for (int j = 0; j < 8; ++j) {
+                    const int32_t x = t[u][j];
+                    a.add(KIND == K_MAX ? (x & m) | (-32768 & ~m) : x);
                 }
             }
         }
@@ -143,7 +149,6 @@ constexpr uint32_t kBandTarget = CM_POOL_BAND_TARGET < kBandBytes ? CM_POOL_BAND
 #define CM_POOL_PERSIST_PER_CU 6
 #endif
 constexpr int kPersistPerCu = CM_POOL_PERSIST_PER_CU;
-constexpr int kNonTemporal = 2;   // buffer access cache policy: nt
 constexpr uint32_t kInvTab = 64;   // AVG: 1/d for every denominator d <= 63, per block
 
 struct BandGeom {
