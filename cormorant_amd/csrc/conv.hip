@@ -2,6 +2,9 @@
 //
 // Dispatch (standard convolutions, first match):
 //   * few output channels, K <= 32, many pixels: direct vector-ALU kernel;
+//   * strided windows of 2..32 taps, small layers (<= 2^19 outputs, K <= 2048): one
+//     block of four waves per 32x32 output tile, the reduction split over the
+//     waves, fragments loaded straight into registers (conv_rk.hip);
 //   * windows of >= 2 taps, the same stride and dilation on both axes, when the
 //     caller's workspace holds the packed weights: conv_pgemm (input patch in
 //     LDS, weights pre-split into limb planes; conv_pgemm.hip);
@@ -35,6 +38,14 @@ int cm_conv_pointwise_launch(const int16_t* x, const int16_t* w, const int16_t* 
 int cm_conv_pw_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
                       uint32_t batch, uint32_t in_ch, uint32_t out_ch, uint32_t hw,
                       const cm_epilogue_t* epi, const LaunchCtx& lc);
+bool cm_conv_rk_takes(uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch,
+                      uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t sh, uint32_t sw,
+                      uint32_t dh, uint32_t dw, uint32_t pad_top, uint32_t pad_left);
+int cm_conv_rk_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y, uint32_t batch,
+                      uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch, uint32_t out_h,
+                      uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t sh, uint32_t sw, uint32_t dh,
+                      uint32_t dw, uint32_t pad_top, uint32_t pad_left, const cm_epilogue_t* epi,
+                      const LaunchCtx& lc);
 int cm_conv_pgemm_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
                          uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
                          uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
@@ -549,6 +560,9 @@ size_t cm_conv_packed_bytes(uint32_t batch, uint32_t in_ch, uint32_t in_h, uint3
     if (direct_channels(K, out_ch, kh * kw, (uint64_t)batch * out_h * out_w,
                         2ull * in_ch * in_h * in_w * batch))
         return 0;
+    if (cm_conv_rk_takes(batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, sh, sw, dh, dw, pad_top,
+                         pad_left))
+        return 0;
     alignas(16) static const int16_t probe[8] = {};   // an aligned stand-in, never read
     if (!pgemm_row_loads(probe, in_w, sh, dh)) {
         size_t need = 0;
@@ -621,6 +635,14 @@ int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int1
             case 24: return launch_direct<24>(g, s);
             default: return launch_direct<32>(g, s);
         }
+    }
+    // Small layers: the register-only kernel with the reduction split over a
+    // block's waves (conv_rk.hip)
+    if (cm_conv_rk_takes(batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw, sh, sw, dh, dw, pad_top,
+                         pad_left)) {
+        const int rc = cm_conv_rk_launch(x, w, b, y, batch, in_ch, in_h, in_w, out_ch, out_h, out_w, kh, kw,
+                                         sh, sw, dh, dw, pad_top, pad_left, epi, lc);
+        if (rc != 1) return rc;
     }
     // The patch GEMM (it needs the caller's workspace for the packed weights)
     // stages input rows 16 bytes at a time when they allow it; where they do

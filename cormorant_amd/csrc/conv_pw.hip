@@ -23,6 +23,7 @@
 // 0 and -128, contributes 0 to both sides).  Every term is taken modulo 2^32,
 // the accumulator's own wrap.  |S_mid| stays below 2^31 for K <= 2^15.
 #include "cm_internal.h"
+#include "limbs.h"
 #include "q88.h"
 
 namespace {
@@ -47,18 +48,10 @@ struct PwArgs {
     FastDiv div_p, div_rt;
 };
 
-__device__ __forceinline__ uint32_t hi4(uint32_t w0, uint32_t w1) {
-    return __builtin_amdgcn_perm(w1, w0, 0x07050301u);   // high bytes of 4 int16, k order kept
-}
-__device__ __forceinline__ uint32_t lo4(uint32_t w0, uint32_t w1) {
-    return __builtin_amdgcn_perm(w1, w0, 0x06040200u) ^ 0x80808080u;   // low bytes - 128
-}
-__device__ __forceinline__ int32_t bsum(uint32_t w, int32_t acc) {
-    return __builtin_amdgcn_sdot4((int)w, 0x01010101, acc, false);
-}
-__device__ __forceinline__ uint32_t pack2(uint32_t lo, uint32_t hi) {
-    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
-}
+using limbs::hi4;
+using limbs::lo4;
+using limbs::bsum;
+using limbs::pack2;
 
 // One k step's raw operands of a lane: 16 k values of its two weight rows (as
 // 8 packed words each) and of its two columns (one int16 per register).

@@ -102,15 +102,19 @@ def test_workspace_size_queries():
     # batches whose outputs overlap run one launch each, each of which may split
     assert lib.cm_matmul_workspace_size(100, 5000, 60, 3, 500000, 300000, 10) == 16 * 100 * 64 * 4
     assert lib.cm_matmul_workspace_size(0, 5000, 60, 1, 0, 0, 0) == 0
-    # convolution: a 7x7x160 3x3 layer at batch 16 with column stride 2 (the gather
-    # path over 16 * 7 * 4 = 448 columns, split over k)
-    conv = lib.cm_conv_workspace_size(16, 160, 7, 7, 160, 7, 4, 3, 3, 1, 2, 1, 1, 1, 1, 1, 0)
+    # convolution: a 7x7 3x3 layer 256 -> 160 at batch 16 with column stride 2 (K =
+    # 2304 is past the register-only kernel: the gather path over 16 * 7 * 4 = 448
+    # columns, split over k)
+    conv = lib.cm_conv_workspace_size(16, 256, 7, 7, 160, 7, 4, 3, 3, 1, 2, 1, 1, 1, 1, 1, 0)
     assert conv > 0 and conv % (160 * 448 * 4) == 0
     # the same layer with stride 1 takes the patch-GEMM path: two row tiles of 128
-    # channels, 23 k steps (two chunks of 64 channels x 9 taps, then 32 channels x
-    # 9 taps in 5 steps), 3 planes of 128 x 64 bytes per tile and step
-    assert lib.cm_conv_workspace_size(16, 160, 7, 7, 160, 7, 7, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0) == \
-        2 * 23 * 3 * 128 * 64 + 8 * 256
+    # channels, 36 k steps (four chunks of 64 channels x 9 taps), 3 planes of
+    # 128 x 64 bytes per tile and step
+    assert lib.cm_conv_workspace_size(16, 256, 7, 7, 160, 7, 7, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0) == \
+        2 * 36 * 3 * 128 * 64 + 8 * 256
+    # a small strided layer (16 x 160 x 14 x 14 -> 7 x 7, K = 1440) on the
+    # register-only kernel: none
+    assert lib.cm_conv_workspace_size(16, 160, 14, 14, 160, 7, 7, 3, 3, 2, 2, 1, 1, 1, 1, 1, 0) == 0
     # conv A of the benchmark block: the patch-GEMM path, whose workspace holds the
     # weights as two int8 limb planes and one int8 plane (9 k steps x 128 rows x 64 k
     # x 3), 128 row sums and 128 int8 flags; depthwise never uses a workspace

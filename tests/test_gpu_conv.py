@@ -92,6 +92,9 @@ GEOMS = [
     (16, 40, 16, 16, 48, 3, 3, 1, 1, 1, 1, 2, 2, 1, 0),   # 48-byte positions, padding 2
     (64, 56, 9, 12, 33, 3, 3, 2, 2, 1, 1, 2, 1, 1, 0),    # 80-byte positions, pads 2 / 1
     (2, 32, 37, 45, 32, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0),    # the same layer under 64 tiles: gather
+    # the 3x3 patch path at sizes the register-only kernel leaves to it (> 2^21 outputs)
+    (512, 32, 9, 17, 32, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0),   # odd output width
+    (320, 16, 30, 60, 16, 3, 3, 2, 2, 1, 1, 1, 1, 0, 0),  # stride 2, no bias
 ]
 
 
@@ -150,14 +153,15 @@ def pgemm_need(C, M, kh, kw):
 
 
 PGEMM = [
-    # N, C, H, W, M, kh, kw, s, d, p: every shape fills >= 200 blocks
+    # N, C, H, W, M, kh, kw, s, d, p: every shape fills >= 200 blocks and has more
+    # than 2^21 outputs (smaller layers take the register-only kernel)
     (32, 64, 56, 56, 128, 3, 3, 1, 1, 1),      # conv A
     (32, 64, 56, 56, 128, 3, 3, 2, 2, 2),      # conv B
     (24, 70, 40, 36, 130, 3, 3, 1, 1, 1),      # two channel chunks, two row tiles
-    (64, 24, 30, 40, 8, 3, 3, 2, 2, 2),        # stride = dilation 2, 24 channels
-    (60, 16, 33, 40, 5, 5, 5, 2, 1, 2),        # 5x5, stride 2, dilation 1
-    (160, 130, 11, 11, 40, 3, 3, 1, 2, 2),     # three chunks (64, 64, 2 channels), dilation 2
-    (48, 8, 26, 22, 3, 3, 1, 1, 3, 1),         # 3x1 window, dilation 3
+    (64, 24, 30, 40, 120, 3, 3, 2, 2, 2),      # stride = dilation 2, 24 channels
+    (60, 16, 33, 40, 110, 5, 5, 2, 1, 2),      # 5x5, stride 2, dilation 1
+    (160, 130, 11, 11, 120, 3, 3, 1, 2, 2),    # three chunks (64, 64, 2 channels), dilation 2
+    (48, 8, 26, 22, 96, 3, 1, 1, 3, 1),        # 3x1 window, dilation 3
 ]
 
 
@@ -256,11 +260,12 @@ def test_patch_path_random(seed):
 
 
 PACKED = [
-    # N, C, H, W, M, kh, kw, s, d, p
-    (8, 32, 28, 32, 32, 3, 3, 1, 1, 1),        # 32-channel row tile
-    (4, 48, 20, 24, 40, 3, 3, 2, 1, 1),        # 64-channel row tile, stride 2
-    (2, 130, 9, 9, 150, 3, 3, 1, 2, 2),        # three channel chunks, two row tiles
-    (16, 64, 14, 14, 64, 3, 3, 1, 1, 1),       # MobileNet-like 14x14 layer
+    # N, C, H, W, M, kh, kw, s, d, p (shapes the patch-GEMM path takes: more than
+    # 2^21 outputs or K > 2048)
+    (80, 32, 28, 32, 32, 3, 3, 1, 1, 1),       # 32-channel row tile
+    (200, 48, 20, 24, 110, 3, 3, 2, 1, 1),     # stride 2
+    (2, 240, 9, 9, 150, 3, 3, 1, 2, 2),        # four channel chunks, two row tiles, K = 2160
+    (192, 64, 14, 14, 96, 3, 3, 1, 1, 1),      # 14-wide rows (element staging), batch 192
 ]
 
 
@@ -308,7 +313,9 @@ def test_conv_packed_rejects_other_paths():
     w = torch.zeros(32 * 32 * 9, dtype=torch.int16, device="cuda")
     with pytest.raises(_native.CmError):
         K.conv_pack(w, buf, *aniso)
-    ok = (4, 32, 14, 14, 32, 14, 14, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0)
+    small = (4, 32, 14, 14, 32, 7, 7, 3, 3, 2, 2, 1, 1, 1, 1, 1, 0)     # the register-only kernel
+    assert K.conv_packed_size(*small) == 0
+    ok = (64, 32, 28, 40, 32, 28, 40, 3, 3, 1, 1, 1, 1, 1, 1, 1, 0)
     assert K.conv_packed_size(*ok) > 64
     with pytest.raises(_native.CmError):
         K.conv_pack(w, buf, *ok)   # 64 bytes is too small
@@ -444,4 +451,75 @@ def test_pointwise_small_unaligned_weights():
     dw_ = dev(w)[1:]
     y = empty_dev(want.size)
     K.ConvKernel(dev(x), dw_, dev(b), y, *args)
+    np.testing.assert_array_equal(host(y), want)
+
+
+RK_SHAPES = [
+    # N, C, H, W, M, kh, kw, s, d, p: the MobileNetV2-like strided small-map layers
+    (16, 24, 56, 56, 24, 3, 3, 2, 1, 1),
+    (16, 32, 28, 28, 32, 3, 3, 2, 1, 1),
+    (16, 96, 14, 14, 96, 3, 3, 2, 1, 1),
+    (16, 160, 14, 14, 160, 3, 3, 2, 1, 1),
+    (4, 227, 14, 14, 61, 3, 3, 2, 1, 1),    # K = 2043 (32 steps), K % 8 != 0
+]
+
+
+@pytest.mark.parametrize("geom", RK_SHAPES, ids=[str(g) for g in RK_SHAPES])
+def test_register_conv_shapes(geom):
+    """Small convolutions on the register-only kernel (the reduction split over a
+    block's four waves), full-range values, bias, fused Add and Relu6."""
+    N, C, H, W, M, kh, kw, s, d, p = geom
+    OH, OW = (H + 2 * p - d * (kh - 1) - 1) // s + 1, (W + 2 * p - d * (kw - 1) - 1) // s + 1
+    args = (N, C, H, W, M, OH, OW, kh, kw, s, s, d, d, p, p, 1, 0)
+    assert K.conv_workspace_size(*args) == 0 and K.conv_packed_size(*args) == 0
+    say(f"register conv {geom}")
+    g = wl.rng(839, *geom)
+    x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
+    w = g.integers(-32768, 32768, M * C * kh * kw, dtype=np.int16)
+    b = g.integers(-32768, 32768, M, dtype=np.int16)
+    add = g.integers(-32768, 32768, N * M * OH * OW, dtype=np.int16)
+    want = np.zeros(N * M * OH * OW, np.int16)
+    oracle.set_threads(oracle_threads())
+    oracle.conv(x, w, b, want, *args, threads=True)
+    y = empty_dev(want.size)
+    K.ConvKernel(dev(x), dev(w), dev(b), y, *args)
+    np.testing.assert_array_equal(host(y), want)
+    y2 = empty_dev(want.size)
+    K.ConvKernel(dev(x), dev(w), dev(b), y2, *args, add=dev(add), act=K.ACT_RELU6)
+    exp = np.clip(np.clip(want.astype(np.int32) + add, -32768, 32767), 0, 1536)
+    np.testing.assert_array_equal(host(y2).astype(np.int32), exp)
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_register_conv_random(seed):
+    """Random small strided convolutions: windows of 2..25 taps (1 x k and k x 1
+    too), strides (at least one above 1) and dilations 1..3 per axis, pads up to and
+    past the window, channel counts with K % 8 == 0 and not, with and without bias."""
+    g = wl.rng(840, seed)
+    kh, kw = int(g.integers(1, 6)), int(g.integers(1, 6))
+    if kh * kw < 2:
+        kw = 2
+    sh, sw = int(g.integers(1, 4)), int(g.integers(1, 4))
+    if sh * sw < 2:
+        sw = 2   # the register-only kernel takes strided windows
+    dh, dw = int(g.integers(1, 4)), int(g.integers(1, 4))
+    pt, pl = int(g.integers(0, kh + 2)), int(g.integers(0, kw + 2))
+    H = int(g.integers(max(1, dh * (kh - 1) + 1 - 2 * pt), 30))
+    W = int(g.integers(max(1, dw * (kw - 1) + 1 - 2 * pl), 30))
+    C = int(g.integers(1, max(2, min(120, 2000 // (kh * kw)))))
+    M = int(g.integers(1, 70))
+    N = int(g.integers(1, 5))
+    OH = (H + 2 * pt - dh * (kh - 1) - 1) // sh + 1
+    OW = (W + 2 * pl - dw * (kw - 1) - 1) // sw + 1
+    bias = int(g.integers(0, 2))
+    args = (N, C, H, W, M, OH, OW, kh, kw, sh, sw, dh, dw, pt, pl, bias, 0)
+    say(f"register conv random seed {seed}: {args}")
+    x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
+    w = g.integers(-32768, 32768, M * C * kh * kw, dtype=np.int16)
+    b = g.integers(-32768, 32768, M, dtype=np.int16)
+    want = np.zeros(N * M * OH * OW, np.int16)
+    oracle.set_threads(oracle_threads())
+    oracle.conv(x, w, b, want, *args, threads=True)
+    y = empty_dev(want.size)
+    K.ConvKernel(dev(x), dev(w), dev(b), y, *args)
     np.testing.assert_array_equal(host(y), want)
