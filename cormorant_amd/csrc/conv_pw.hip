@@ -69,9 +69,11 @@ __device__ __forceinline__ void pw_load(const PwArgs& g, __amdgpu_buffer_rsrc_t 
         if constexpr (AV) {
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
-                // C % 8 == 0: a group of 8 k values is wholly inside or outside the row
-                const bool ok = arow[i] != kOob && kb + q * 8 < g.C;
-                const v4u v = __builtin_amdgcn_raw_buffer_load_b128(wr, ok ? arow[i] + (kb + q * 8) * 2u : kOob, 0, 0);
+                // C % 8 == 0: a group of 8 k values is wholly inside or outside the
+                // row; an invalid row's arow is kOob, a k past the end sets bit 31
+                // (validity in the offset: a select on it became a branch per load)
+                const uint32_t hole = (uint32_t)(kb + q * 8 >= g.C) << 31;
+                const v4u v = __builtin_amdgcn_raw_buffer_load_b128(wr, (arow[i] + (kb + q * 8) * 2u) | hole, 0, 0);
                 st.a[i][4 * q + 0] = v[0]; st.a[i][4 * q + 1] = v[1];
                 st.a[i][4 * q + 2] = v[2]; st.a[i][4 * q + 3] = v[3];
             }
@@ -79,8 +81,8 @@ __device__ __forceinline__ void pw_load(const PwArgs& g, __amdgpu_buffer_rsrc_t 
             uint32_t r[16];
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const bool ok = arow[i] != kOob && kb + e < g.C;
-                r[e] = __builtin_amdgcn_raw_buffer_load_b16(wr, ok ? arow[i] + (kb + e) * 2u : kOob, 0, 0);
+                const uint32_t hole = (uint32_t)(kb + e >= g.C) << 31;
+                r[e] = __builtin_amdgcn_raw_buffer_load_b16(wr, (arow[i] + (kb + e) * 2u) | hole, 0, 0);
             }
 #pragma unroll
             for (int e = 0; e < 8; ++e) st.a[i][e] = pack2(r[2 * e], r[2 * e + 1]);
@@ -91,8 +93,9 @@ __device__ __forceinline__ void pw_load(const PwArgs& g, __amdgpu_buffer_rsrc_t 
     for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
-            const bool ok = bcol[j] != kOob && kb + e < g.C;
-            st.b[j][e] = __builtin_amdgcn_raw_buffer_load_b16(xr, ok ? bcol[j] + (kb + e) * cst : kOob, 0, 0);
+            // an invalid column's bcol is kOob (the sum stays below 2^32)
+            const uint32_t hole = (uint32_t)(kb + e >= g.C) << 31;
+            st.b[j][e] = __builtin_amdgcn_raw_buffer_load_b16(xr, (bcol[j] + (kb + e) * cst) | hole, 0, 0);
         }
 }
 
