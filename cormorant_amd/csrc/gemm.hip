@@ -1047,6 +1047,9 @@ int launch_gemm(GemmArgs& g0, uint32_t zdim, const LaunchCtx& lc, const char* na
 
 }  // namespace
 
+int cm_matmul_rk_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k, uint32_t m,
+                        const cm_epilogue_t* epi, const LaunchCtx& lc);
+
 int cm_matmul_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
                      uint32_t m, uint32_t batch, uint32_t a_bs, uint32_t b_bs, uint32_t c_bs,
                      const cm_epilogue_t* epi, const LaunchCtx& lc) {
@@ -1066,6 +1069,12 @@ int cm_matmul_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n,
         g.a_vec = aligned(g.a, 16) && k % 8 == 0;
         g.b_vec = aligned(g.b, 8) && m % 4 == 0;
         batch = 1;
+    }
+    // one small product: the register-only kernel, the reduction split over a
+    // block's waves (matmul_rk.hip)
+    if (batch == 1) {
+        const int rc = cm_matmul_rk_launch(g.a, g.b, g.c, n, k, m, epi, lc);
+        if (rc != 1) return rc;
     }
     // Batches whose outputs overlap (0 < c_stride < n*m) run one launch each, in
     // batch order: the reference's sequential batch loop (MatmulKernel.cpp:108-111)

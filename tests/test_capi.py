@@ -95,8 +95,10 @@ def test_workspace_size_queries():
     assert lib.cm_matmul_workspace_size(1024, 1024, 1024, 32, 1 << 20, 1 << 20, 1 << 20) == 0
     # one tile, 79 k steps: 16 splits of 100 x 64 (60 rounded up) words
     assert lib.cm_matmul_workspace_size(100, 5000, 60, 1, 0, 0, 0) == 16 * 100 * 64 * 4
-    # 16 x 1280 x 1000: 8 tiles, 20 k steps -> 20 splits wanted, at most 16, evened to 10
-    assert lib.cm_matmul_workspace_size(16, 1280, 1000, 1, 0, 0, 0) == 10 * 16 * 1000 * 4
+    # 16 x 1280 x 1000 (16,000 outputs, 20 k steps) takes the register-only kernel: none
+    assert lib.cm_matmul_workspace_size(16, 1280, 1000, 1, 0, 0, 0) == 0
+    # 16 x 1280 x 20000: 157 tiles, 20 k steps -> 2 splits of 16 x 20000 words
+    assert lib.cm_matmul_workspace_size(16, 1280, 20000, 1, 0, 0, 0) == 2 * 16 * 20000 * 4
     # batched without overlap: one launch over every batch, no split
     assert lib.cm_matmul_workspace_size(100, 5000, 60, 4, 500000, 300000, 6000) == 0
     # batches whose outputs overlap run one launch each, each of which may split

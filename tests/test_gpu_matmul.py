@@ -175,3 +175,39 @@ def test_config3b_full():
     n, k, m = case.n, case.k, case.m
     got, want = mm_both(a.reshape(n, k), b.reshape(k, m), n, k, m)
     np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_small_products_register_kernel(seed):
+    """Small single products (<= 2^18 outputs, K <= 4096) on the register-only
+    kernel (the reduction split over a block's waves): row / column counts around
+    the 32-wide tile, K with and without whole 16-byte rows, full-range values that
+    wrap, unaligned A, and the fused epilogue (same-shaped Add, column Add, Relu6)."""
+    g = wl.rng(823, seed)
+    n = int(g.choice([1, 7, 16, 31, 32, 33, 64, 100, 200]))
+    m = int(g.choice([1, 10, 31, 33, 96, 256, 1000]))
+    k = int(g.choice([1, 5, 8, 64, 65, 256, 784, 1280, 2047, 4096]))
+    if n * m > (1 << 18):
+        m = (1 << 18) // n
+    say(f"matmul register kernel seed {seed}: {n} x {k} x {m}")
+    assert K.matmul_workspace_size(n, k, m) == 0
+    a = g.integers(-32768, 32768, n * k + 1, dtype=np.int16)
+    b = g.integers(-32768, 32768, k * m, dtype=np.int16)
+    off = int(seed % 2)   # odd seeds: A one element past a 16-byte boundary
+    want = np.zeros(n * m, np.int16)
+    oracle.set_threads(oracle_threads())
+    oracle.matmul(np.ascontiguousarray(a[off:off + n * k]), b, want, n, k, m, threads=True)
+    da = dev(a)[off:off + n * k]
+    c = empty_dev(n * m)
+    K.MatmulKernel(da, dev(b), c, n, k, m)
+    np.testing.assert_array_equal(host(c), want)
+    same = g.integers(-32768, 32768, n * m, dtype=np.int16)
+    col = g.integers(-32768, 32768, m, dtype=np.int16)
+    for add, column, act in ((same, False, K.ACT_NONE), (col, True, K.ACT_RELU6)):
+        c2 = empty_dev(n * m)
+        K.MatmulKernel(da, dev(b), c2, n, k, m, add=dev(add), add_column=column, act=act)
+        addv = np.tile(col, n) if column else same
+        exp = np.clip(want.astype(np.int32) + addv, -32768, 32767)
+        if act == K.ACT_RELU6:
+            exp = np.clip(exp, 0, 1536)
+        np.testing.assert_array_equal(host(c2).astype(np.int32), exp)

@@ -29,10 +29,10 @@ def workspace(nbytes: int):
 MM = [
     # name, n, k, m, operand range (None = full int16 range)
     ("one_tile_k5000", 100, 5000, 60, 2.0),
-    ("fc_16x1280x1000", 16, 1280, 1000, 1.0),
-    ("odd_steps_k449", 130, 449, 70, 4.0),
-    ("wrap_full_range", 64, 4096, 96, None),
-    ("k256_two_tiles", 200, 256, 100, 8.0),
+    ("fc_16x1280x20000", 16, 1280, 20000, 1.0),   # 16 x 1280 x 1000 takes the register-only kernel
+    ("odd_steps_k449", 130, 449, 2100, 4.0),
+    ("wrap_full_range", 64, 4160, 96, None),
+    ("k256_two_tiles", 200, 256, 1400, 8.0),
     ("tiles64_k640", 1024, 640, 1024, 1.0),    # 64 tiles: split with two k steps per split
 ]
 

@@ -30,9 +30,9 @@ def _noalloc(a, b, c, n, k, m, batch=1, a_bs=0, b_bs=0, c_bs=0, epi=None):
 def test_noalloc_matches_workspace_entry_point():
     import torch
     g = wl.rng(990)
-    # first call: 16 x 1280 x 1000 with a fused column Add and Relu6 (splits 10 ways);
-    # second, smaller: 64 x 4096 x 96 full-range operands whose sums wrap (16 splits)
-    cases = [(16, 1280, 1000, 1.0, True), (64, 4096, 96, None, False)]
+    # first call: 16 x 1280 x 20000 with a fused column Add and Relu6 (splits 2 ways);
+    # second, smaller: 64 x 4160 x 96 full-range operands whose sums wrap (16 splits)
+    cases = [(16, 1280, 20000, 1.0, True), (64, 4160, 96, None, False)]
     for n, k, m, r, fused in cases:
         need = K.matmul_workspace_size(n, k, m)
         assert 0 < need <= SCRATCH_BYTES, need
