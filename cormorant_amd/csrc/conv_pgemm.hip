@@ -11,8 +11,9 @@
 //   conv_pgemm  one block per (128 output channels, range of L consecutive
 //               output pixels of one image; L is chosen so the blocks spread
 //               evenly over the CUs).  The input rows the range's windows touch
-//               are loaded once per chunk of 64 channels and stored in LDS
-//               channel-minor as limb planes, so the 16 k values one MFMA lane
+//               are loaded once (every channel, when they fit in LDS; else in
+//               chunks of 64 channels) and stored in LDS channel-minor as limb
+//               planes, so the 16 k values one MFMA lane
 //               supplies (16 channels of one tap at one pixel) are one 16-byte
 //               LDS read: the B operand needs no per-step staging and no gather.
 //               Each wave's A fragments are 16-byte loads from the packed planes
@@ -70,8 +71,10 @@ struct PgArgs {
     uint32_t lhc, wr, nh;        // padding columns: left [0, lhc), right [wr, wr + nh - lhc)
     uint32_t stage_g;            // 16-byte staging: (row, column group) pair groups per block
     uint32_t cpt_last;           // 16-channel groups of the last chunk
+    uint32_t cpt_all;            // without MULTI: 16-channel groups the patch holds (every chunk)
+    uint32_t nfull;              // without MULTI: full 64-channel chunks before the last one
     uint32_t L, rpi, rpi_n;      // output pixels per block; ranges per image; ranges per row tile
-    FastDiv div_npr, div_nbm, div_rpi, div_ow, div_npos, div_pw, div_nv, div_prows, div_nh, div_kw, div_cpt4, div_cpt_last;
+    FastDiv div_npr, div_nbm, div_rpi, div_ow, div_npos, div_pw, div_nv, div_prows, div_nh, div_kw, div_cpt4, div_cpt_last, div_t4;
     uint32_t vw;                 // output / Add access width in elements (8 or 1)
     uint32_t x_img_bytes, pk_bytes;   // pk_bytes: both packed layouts (limb planes, then int8)
     uint32_t pk8_off;            // byte offset of the int8 plane
@@ -161,9 +164,9 @@ __global__ __launch_bounds__(256) void conv_wpack(PackArgs a) {
 // (2 x 4 MFMA 16x16x64 tiles, three accumulator sets).  Waves of one row read
 // their own weight rows; waves of one column read their own 64 pixels of the
 // patch.  (WR = 4 for more than 64 output channels, 2 for 33-64, 1 for <= 32.)
-// With one channel chunk the input rows of the range are staged into the LDS
-// patch once and every sub-tile reads them; with more chunks each sub-tile
-// restages every chunk.  After staging, each patch position's channel sum is
+// When the LDS patch holds every channel, the input rows of the range are
+// staged once and every sub-tile reads them; otherwise (MULTI) each sub-tile
+// restages 64-channel chunks in turn.  After staging, each patch position's channel sum is
 // kept in LDS, so a pixel's window sum (the limb identity's column sum) is a
 // sum over taps, read outside the k loop.  A fragments come straight from the
 // packed planes (a row tile of one limb is 16 rows x 64 bytes, 1 KB
@@ -183,14 +186,15 @@ __device__ __forceinline__ void wave_sync() {
 }
 
 // VEC: patch rows loaded 16 bytes at a time with g = VEC; 0 = per element.
-// MULTI: more than one channel chunk (restaged inside the k loop, with fewer
-// loads in flight while the accumulators are live).
-// NS: A fragment sets in flight (3: two steps of prefetch, for one chunk whose
-// step count is a multiple of 3; else 2: one step).
+// MULTI: 64-channel chunks restaged in turn inside the k loop (more channels
+// than one patch holds), with fewer loads in flight while the accumulators are
+// live.
+// NS: A fragment sets in flight (3: two steps of prefetch, without MULTI and
+// with a step count that is a multiple of 3; else 2: one step).
 // WR: wave rows (row tile of 32 * WR output channels).
 template <int VEC, bool MULTI, int NS, int WR>
 __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
-    static_assert(NS == 2 || (NS == 3 && !MULTI), "three A sets need one chunk");
+    static_assert(NS == 2 || (NS == 3 && !MULTI), "three A sets need one patch of every channel");
     constexpr uint32_t TB = 32u * WR;             // output channels per row tile
     constexpr uint32_t WC = 4u / WR;              // wave columns
     constexpr uint32_t SPX = 64u * WC;            // pixels per sub-tile
@@ -394,12 +398,39 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
         }
     };
 
-    // After a chunk is staged: each position's sum over the chunk's channel
-    // slots (x = 256 * high + low + 128 per slot; a zero slot adds 0), and the
-    // chunk's q table: q = tap * cpt + cg -> byte offset of (tap, group) from a
-    // pixel's window origin, -1 past the chunk's last sub-chunk.
-    auto chunk_tables = [&](uint32_t cpt, const FastDiv& div_cpt, bool sums) {
-        const uint32_t np = sums ? prows_b * g.PW : 0u;
+    // The q table of the staged patch (it depends on no loaded data, so it is
+    // written before the patch loads land): sub-chunk q -> byte offset of its
+    // (tap, 16-channel group) from a pixel's window origin, -1 past the last
+    // sub-chunk.  The first nfull * taps * 4 entries walk full 64-channel chunks
+    // (q = 4 * (chunk * taps + tap) + group), the rest the last chunk's cpt
+    // groups (q = tap * cpt + group); with every chunk in one patch the groups
+    // of chunk ch sit at slot 4 * ch + group of a position.
+    auto build_qtab = [&](uint32_t cpt, const FastDiv& div_cpt, uint32_t nfull) {
+        const uint32_t qfull = nfull * g.taps * 4u;
+        for (uint32_t q = tid; q < (uint32_t)kMaxQ + 4u; q += kPgThreads) {
+            uint32_t tap, cg;
+            if (q < qfull) {
+                const uint32_t ch = fdiv(q, g.div_t4), r = q - ch * g.taps * 4u;
+                tap = r >> 2;
+                cg = ch * 4u + (r & 3u);
+            } else {
+                const uint32_t r = q - qfull;
+                tap = fdiv(r, div_cpt);
+                cg = nfull * 4u + (r - tap * cpt);
+            }
+            const uint32_t khi = fdiv(tap, g.div_kw), kwi = tap - khi * g.KW;
+            const uint32_t tp = (khi * g.PW + kwi) * g.Dg;
+            qtab[q] = tap < g.taps ? (int32_t)(tp * g.ppitch + cg * 16u) : -1;
+            if (q < (uint32_t)kMaxTaps) {
+                const uint32_t kh2 = fdiv(q, g.div_kw), kw2 = q - kh2 * g.KW;
+                tpos[q] = q < g.taps ? (kh2 * g.PW + kw2) * g.Dg : 0u;
+            }
+        }
+    };
+    // After a patch is staged: each position's sum over its cpt channel slots
+    // (x = 256 * high + low + 128 per slot; a zero slot adds 0).
+    auto pos_sums = [&](uint32_t cpt) {
+        const uint32_t np = prows_b * g.PW;
         const uint32_t base = 128u * 16u * cpt;
         for (uint32_t pos = tid; pos < np; pos += kPgThreads) {
             int32_t sh = 0, sl = 0;
@@ -408,13 +439,6 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
                 sl = bsum16(*reinterpret_cast<const v4i*>(p_lo + pos * g.ppitch + c * 16u), sl);
             }
             spos[pos] = 256u * (uint32_t)sh + (uint32_t)sl + base;
-        }
-        for (uint32_t q = tid; q < (uint32_t)kMaxQ + 4u; q += kPgThreads) {
-            const uint32_t tap = fdiv(q, div_cpt), cg = q - tap * cpt;
-            const uint32_t khi = fdiv(tap, g.div_kw), kwi = tap - khi * g.KW;
-            const uint32_t tp = (khi * g.PW + kwi) * g.Dg;
-            qtab[q] = tap < g.taps ? (int32_t)(tp * g.ppitch + cg * 16u) : -1;
-            if (cg == 0 && tap < (uint32_t)kMaxTaps) tpos[tap] = tap < g.taps ? tp : 0u;
         }
     };
 
@@ -436,32 +460,37 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
         return k >= g.steps ? k - g.steps : k;
     };
 
+    // The first steps' A fragments load before the patch, so their latency
+    // overlaps the staging: the int8 form, which weights that fit int8 use
+    // (known only once the block's flags are in; other weights reload the
+    // limb planes then).
+    a_load8(0, fa_h[0]);
+    if constexpr (NS == 3) a_load8(ks_plus(0, 1), fa_h[1]);
+
     for (uint32_t sub = 0; sub < nsub; ++sub) {
         const uint32_t p0 = pb + sub * SPX + wc * 64u;      // this wave's first pixel of the sub-tile
         const uint32_t pn = p0 < pe ? min(64u, pe - p0) : 0u;   // the wave's pixels of this sub-tile
         const uint32_t nj = (pn + 15u) / 16u;              // 16-pixel column tiles in use (0 - 4)
-        // the first chunk's patch (with one chunk: staged once for every sub-tile),
-        // before the accumulators and A fragments of this sub-tile are live
+        // the first chunk's patch (without MULTI: every chunk, staged once for
+        // every sub-tile), before the accumulators of this sub-tile are live
         if (sub == 0 || MULTI) {
-            if (sub) __syncthreads();   // every wave is done with the previous patch
-            stage_patch(0u, MULTI ? 4u : g.cpt_last);
+            if (sub) __syncthreads();   // every wave is done with the previous patch and q table
+            stage_patch(0u, MULTI ? 4u : g.cpt_all);
+            build_qtab(MULTI ? 4u : g.cpt_last, MULTI ? g.div_cpt4 : g.div_cpt_last, MULTI ? 0u : g.nfull);
             if (sub == 0) {
                 const bool real = row0 + tid < g.M;
                 if (tid < TB) rowterm_s[tid] = real ? 128u * ld_wsum + (uint32_t)ld_bias * 256u : 0u;
                 fast = __syncthreads_and(tid >= TB || !real || ld_fit != 0u) != 0;
+                if (!fast) {
+                    a_load(0, fa_h[0], fa_l[0]);
+                    if constexpr (NS == 3) a_load(ks_plus(0, 1), fa_h[1], fa_l[1]);
+                }
             } else {
                 __syncthreads();
             }
-            chunk_tables(MULTI ? 4u : g.cpt_last, MULTI ? g.div_cpt4 : g.div_cpt_last, !fast);
-            __syncthreads();
-        }
-        if (sub == 0) {
-            if (fast) {
-                a_load8(0, fa_h[0]);
-                if constexpr (NS == 3) a_load8(ks_plus(0, 1), fa_h[1]);
-            } else {
-                a_load(0, fa_h[0], fa_l[0]);
-                if constexpr (NS == 3) a_load(ks_plus(0, 1), fa_h[1], fa_l[1]);
+            if (!fast) {   // the column term's position sums
+                pos_sums(MULTI ? 4u : g.cpt_all);
+                __syncthreads();
             }
         }
         // patch position of the window origin of this lane's pixel in each column
@@ -572,13 +601,17 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
                 const uint32_t c0 = ch * 64u;
                 const bool last = ch + 1 == g.nchunks;
                 const uint32_t cpt = last ? g.cpt_last : 4u;
-                const uint32_t nst = (g.taps * cpt + 3u) / 4u;
+                // without MULTI the one patch holds every chunk: all steps
+                const uint32_t nst = MULTI ? (g.taps * cpt + 3u) / 4u : g.steps;
                 if (MULTI && ch) {   // later chunks: restaged here
-                    __syncthreads();   // every wave is done with the previous chunk's patch
+                    __syncthreads();   // every wave is done with the previous chunk's patch and q table
                     stage_patch(c0, cpt);
+                    build_qtab(cpt, last ? g.div_cpt_last : g.div_cpt4, 0u);
                     __syncthreads();
-                    chunk_tables(cpt, last ? g.div_cpt_last : g.div_cpt4, !FAST);
-                    __syncthreads();
+                    if constexpr (!FAST) {
+                        pos_sums(cpt);
+                        __syncthreads();
+                    }
                 }
                 if constexpr (!FAST) window_sums();
                 int32_t qo = qtab[lane >> 4];
@@ -761,14 +794,16 @@ int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* 
     const uint32_t PW = vec && wr > PWr ? wr : PWr;
     const uint32_t lhc = lh < PWr ? lh : PWr;
     const uint32_t nh = lhc + (PWr > wr ? PWr - wr : 0u);
-    const uint32_t cpt_max = nchunks > 1 ? 4u : (in_ch + 15) / 16;
-    const uint32_t ppitch = cpt_max % 2 ? cpt_max * 16 : cpt_max * 16 + 16;   // odd multiple of 16
     const uint32_t khspan = (kh - 1) * Dg + 1;
     const uint32_t last_cpt = (in_ch - (nchunks - 1) * 64 + 15) / 16;
+    const uint32_t cpt_all = (in_ch + 15) / 16;
     const uint32_t steps = (nchunks - 1) * taps + (taps * last_cpt + 3) / 4;
     auto a16 = [](uint64_t v) { return (v + 15) & ~15ull; };
-    auto layout = [&](uint64_t prows, uint64_t& spos_off, uint64_t& epi_off) {
-        const uint64_t p_plane = prows * PW * ppitch + 16;
+    // LDS bytes per patch position and plane: an odd multiple of 16 (the 16
+    // pixels of a fragment read then fall on distinct bank groups)
+    auto pitch_of = [](uint32_t cpt) { return cpt % 2 ? cpt * 16 : cpt * 16 + 16; };
+    auto layout = [&](uint64_t prows, uint32_t pitch, uint64_t& spos_off, uint64_t& epi_off) {
+        const uint64_t p_plane = prows * PW * pitch + 16;
         spos_off = a16(2 * p_plane);
         epi_off = spos_off + a16(prows * PW * 4);
         return epi_off + 4ull * kEpiBytes;
@@ -779,34 +814,50 @@ int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* 
     // busiest wave (sub-tiles of 64 pixels per wave column); staging a patch
     // row costs about one cycle per 16 bytes loaded, once per block pair (the
     // second block's staging overlaps the first one's MFMAs) and once per
-    // sub-tile and chunk with several chunks; a lone block per CU keeps one
-    // wave per SIMD and runs at about 70%.
+    // sub-tile and chunk when chunks are restaged; a lone block per CU keeps
+    // one wave per SIMD and runs at about 70%.  Returns 0 when no L fits.
     const uint64_t cus = cu_count();
     const uint64_t c_tile = 128ull * steps;
-    const uint64_t c_row = (uint64_t)PW * cpt_max * 2;
-    uint32_t L = 0;
-    uint64_t best = ~0ull, prows = 0;
-    const uint64_t lcap = nchunks > 1 ? 128u : 512u;
-    for (uint64_t l = 16; l <= lcap; l += 16) {
-        const uint64_t rows = std::min<uint64_t>(out_h, (l - 1 + out_w - 1) / out_w + 1);
-        const uint64_t pr = (rows - 1) * Sg + khspan;
-        uint64_t so, eo;
-        if (layout(pr, so, eo) > kPgLdsMax) break;   // grows with l
-        const uint64_t rpi = (P + l - 1) / l;
-        const uint64_t blocks = rpi * batch * mtiles;
-        if (blocks > 0x7FFFFFFFull) continue;
-        const uint64_t k = (blocks + cus - 1) / cus;
-        const uint64_t rem = l % SPX;
-        const uint64_t u = (l / SPX) * 4 + (std::min<uint64_t>(rem, 64) + 15) / 16;
-        const uint64_t stage = pr * c_row * (nchunks > 1 ? nchunks * ((l + SPX - 1) / SPX) : 1u);
-        uint64_t t = k * u * c_tile + ((k + 1) / 2) * stage;
-        if (k == 1) t = t * 10 / 7;
-        if (t < best) { best = t; L = (uint32_t)l; prows = pr; }
-        if (l >= P) break;
+    auto pick_l = [&](bool multi, uint32_t pitch, uint64_t& prows_out) -> uint32_t {
+        const uint32_t cpt_row = multi ? 4u : cpt_all;
+        const uint64_t c_row = (uint64_t)PW * cpt_row * 2;
+        uint32_t l_best = 0;
+        uint64_t best = ~0ull;
+        const uint64_t lcap = multi ? 128u : 512u;
+        for (uint64_t l = 16; l <= lcap; l += 16) {
+            const uint64_t rows = std::min<uint64_t>(out_h, (l - 1 + out_w - 1) / out_w + 1);
+            const uint64_t pr = (rows - 1) * Sg + khspan;
+            uint64_t so, eo;
+            if (layout(pr, pitch, so, eo) > kPgLdsMax) break;   // grows with l
+            const uint64_t rpi = (P + l - 1) / l;
+            const uint64_t blocks = rpi * batch * mtiles;
+            if (blocks > 0x7FFFFFFFull) continue;
+            const uint64_t k = (blocks + cus - 1) / cus;
+            const uint64_t rem = l % SPX;
+            const uint64_t u = (l / SPX) * 4 + (std::min<uint64_t>(rem, 64) + 15) / 16;
+            const uint64_t stage = pr * c_row * (multi ? nchunks * ((l + SPX - 1) / SPX) : 1u);
+            uint64_t t = k * u * c_tile + ((k + 1) / 2) * stage;
+            if (k == 1) t = t * 10 / 7;
+            if (t < best) { best = t; l_best = (uint32_t)l; prows_out = pr; }
+            if (l >= P) break;
+        }
+        return l_best;
+    };
+    // Every channel chunk staged once into one patch when the patch fits and the
+    // q table holds every step; otherwise (MULTI) 64-channel chunks restaged in
+    // turn.  Both consume the same packed weights (the k order is the chunk's).
+    uint64_t prows = 0;
+    uint32_t ppitch = pitch_of(cpt_all);
+    bool multi = false;
+    uint32_t L = steps * 4u <= (uint32_t)kMaxQ ? pick_l(false, ppitch, prows) : 0u;
+    if (L == 0 && nchunks > 1) {
+        multi = true;
+        ppitch = pitch_of(4u);
+        L = pick_l(true, ppitch, prows);
     }
     if (L == 0) return 1;
     uint64_t spos_off = 0, epi_off = 0;
-    const uint64_t lds = layout(prows, spos_off, epi_off);
+    const uint64_t lds = layout(prows, ppitch, spos_off, epi_off);
     const uint32_t rpi = (uint32_t)((P + L - 1) / L);
     const uint64_t zslot = prows * PW * ppitch;
     const uint64_t p_plane = zslot + 16;
@@ -852,6 +903,8 @@ int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* 
     g.spos_off = (uint32_t)spos_off; g.epi_off = (uint32_t)epi_off;
     g.lhc = lhc; g.wr = wr; g.nh = nh;
     g.cpt_last = last_cpt;
+    g.cpt_all = cpt_all;
+    g.nfull = nchunks - 1;
     g.L = L; g.rpi = rpi; g.rpi_n = rpi * batch;
     g.div_nbm = make_fastdiv(rpi * batch);
     g.prows = (uint32_t)prows;
@@ -871,6 +924,7 @@ int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* 
     g.div_kw = make_fastdiv(kw);
     g.div_cpt4 = make_fastdiv(4);
     g.div_cpt_last = make_fastdiv(last_cpt);
+    g.div_t4 = make_fastdiv(taps * 4u);
     g.x_img_bytes = (uint32_t)(2 * x_img);
     g.pk_bytes = (uint32_t)pk_bytes;
     g.pk8_off = (uint32_t)pk_limb;
@@ -885,7 +939,7 @@ int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* 
                               : vec == 2 ? (const void*)conv_pgemm<2, M, NS, W> : (const void*)conv_pgemm<0, M, NS, W>)
 #define CM_PG_PICK_W(M, NS) (wrows == 1 ? CM_PG_PICK(M, NS, 1) : wrows == 2 ? CM_PG_PICK(M, NS, 2) \
                                                                      : CM_PG_PICK(M, NS, 4))
-    if (nchunks > 1) k = CM_PG_PICK(true, 2, 4);
+    if (multi) k = CM_PG_PICK(true, 2, 4);
     else if (steps % 3 == 0) k = CM_PG_PICK_W(false, 3);
     else k = CM_PG_PICK_W(false, 2);
 #undef CM_PG_PICK_W

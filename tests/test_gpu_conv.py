@@ -162,6 +162,8 @@ PGEMM = [
     (60, 16, 33, 40, 110, 5, 5, 2, 1, 2),      # 5x5, stride 2, dilation 1
     (160, 130, 11, 11, 120, 3, 3, 1, 2, 2),    # three chunks (64, 64, 2 channels), dilation 2
     (48, 8, 26, 22, 96, 3, 1, 1, 3, 1),        # 3x1 window, dilation 3
+    (32, 130, 12, 100, 72, 3, 3, 1, 1, 1),     # three chunks too wide for one patch: restaged in turn
+    (112, 150, 20, 24, 40, 5, 5, 1, 1, 2),     # 5x5, three chunks in one patch: 63 k steps
 ]
 
 
