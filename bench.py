@@ -202,6 +202,31 @@ def bench_block(steps: int, warmup: int):
             fnf()
         msf = time_launches([fnf], steps)
         gopsf = 2.0 * case.macs / (msf * 1e-3) / 1e9
+        # weights packed once (cm_conv_pack), then cm_conv_packed_ex per call: what the
+        # inference session runs for constant weights; its output must equal the
+        # per-call path's bit for bit
+        packed_res = None
+        psize = K.conv_packed_size(*args)
+        if psize:
+            packed = torch.empty(-(-psize // 4), dtype=torch.int32, device="cuda")
+            K.conv_pack(dw_, packed, *args)
+            dyp = torch.empty_like(dy)
+            fnp = lambda args=args, dyp=dyp, packed=packed: K.ConvPackedKernel(dx, packed, db, dyp, *args)
+            for _ in range(warmup):
+                fnp()
+            msp = time_launches([fnp], steps)
+            fn()
+            torch.cuda.synchronize()
+            if not torch.equal(dyp, dy):
+                raise RuntimeError(f"{case.name}: packed-weight output differs from the per-call output")
+            gopsp = 2.0 * case.macs / (msp * 1e-3) / 1e9
+            packed_res = dict(ms=round(msp, 5), gops=round(gopsp, 1), limb_products=products,
+                              mfma_frac=round(products * gopsp / 1e3 / INT8_PEAK_TOPS, 4),
+                              frac_of_4product_roofline=round(LIMB_PRODUCTS * gopsp / 1e3 / INT8_PEAK_TOPS, 4),
+                              timing="cm_conv_pack once, then cm_conv_packed_ex per call (constant "
+                                     "weights, as the inference session runs them); output equal to "
+                                     "the per-call path's")
+            del packed, dyp
         out[case.name] = dict(
             shape=f"N={case.batch} C {case.in_ch}->{case.out_ch} {case.hw}x{case.hw} {case.k}x{case.k} "
                   f"s{case.stride} d{case.dil} p{case.pad} bias -> {o}x{o}",
@@ -213,6 +238,7 @@ def bench_block(steps: int, warmup: int):
             full_range_weights=dict(ms=round(msf, 5), gops=round(gopsf, 1), limb_products=LIMB_PRODUCTS,
                                     mfma_frac=round(LIMB_PRODUCTS * gopsf / 1e3 / INT8_PEAK_TOPS, 4)),
             timing="per call, weight pack included",
+            packed_weights=packed_res,
             workspace_bytes=need)
         del dwf, dyf
         out[case.name]["_dev"] = (dx, dw_, db, dy, x, w, b)

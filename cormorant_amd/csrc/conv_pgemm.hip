@@ -825,10 +825,16 @@ int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* 
         uint64_t best = ~0ull;
         const uint64_t lcap = multi ? 128u : 512u;
         for (uint64_t l = 16; l <= lcap; l += 16) {
-            const uint64_t rows = std::min<uint64_t>(out_h, (l - 1 + out_w - 1) / out_w + 1);
+            // output rows a range spans: ranges start at multiples of l, so a
+            // range's offset within its first row is a multiple of gcd(l, out_w),
+            // at most out_w - gcd(l, out_w)
+            const uint64_t off = out_w - gcd((uint32_t)l, out_w);
+            const uint64_t rows = std::min<uint64_t>(out_h, (off + l + out_w - 1) / out_w);
             const uint64_t pr = (rows - 1) * Sg + khspan;
             uint64_t so, eo;
-            if (layout(pr, pitch, so, eo) > kPgLdsMax) break;   // grows with l
+            // (rows do not grow monotonically with l: a longer, row-aligned range
+            // may span fewer rows than a shorter one)
+            if (layout(pr, pitch, so, eo) > kPgLdsMax) continue;
             const uint64_t rpi = (P + l - 1) / l;
             const uint64_t blocks = rpi * batch * mtiles;
             if (blocks > 0x7FFFFFFFull) continue;
