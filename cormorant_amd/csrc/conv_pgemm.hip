@@ -94,12 +94,15 @@ __device__ __forceinline__ uint32_t pack2(uint32_t lo, uint32_t hi) {
 }
 
 // ------------------------------------------------------------ weight pack --
-// One block per output channel row m of a 128-row tile (rows past M are packed
-// as zeros).  Word w of a (row tile, step) plane row covers k bytes 4w..4w+3 of
+// One block per output channel row m of a row tile (rows past M are packed as
+// zeros).  Word w of a (row tile, step) plane row covers k bytes 4w..4w+3 of
 // the step: sub-chunk q = 4*step_in_chunk + w/4, channels 16*(q % cpt) + 4*(w%4)
 // + 0..3 of the chunk, tap q / cpt.  Besides the two limb planes the row is
 // written as int8 values (w8 plane: meaningful when every weight of the row
-// lies in [-128, 127], which wfit records).
+// lies in [-128, 127], which wfit records).  The weight loads are range-checked
+// buffer loads (a padding position reads 0 through bit 31 of its offset: no
+// branch between them), and the row sum and the int8 flag are wave reductions
+// met in LDS after one barrier.
 struct PackArgs {
     const int16_t* w;
     uint8_t* wpk;
@@ -115,7 +118,9 @@ __global__ __launch_bounds__(256) void conv_wpack(PackArgs a) {
     const uint32_t mt = m / a.tb, r = m % a.tb;
     const uint32_t tile = 2u * a.tb * 64u, tile8 = a.tb * 64u;   // bytes per (row tile, step)
     const bool mok = m < a.M;
-    const int16_t* wrow = a.w + (uint64_t)(mok ? m : 0u) * a.C * a.taps;
+    const uint32_t row_elems = a.C * a.taps;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(a.w + (uint64_t)(mok ? m : 0u) * row_elems,
+                                               mok ? row_elems * 2u : 0u);
     uint32_t sum = 0, fit = 1u;
     const uint32_t words = a.steps * 16u;
     for (uint32_t i = threadIdx.x; i < words; i += 256) {
@@ -127,34 +132,46 @@ __global__ __launch_bounds__(256) void conv_wpack(PackArgs a) {
         const uint32_t cpt = (cc + 15u) / 16u;
         const uint32_t q = ls * 4u + (wd >> 2);
         const uint32_t tap = q / cpt, cg = q - tap * cpt;
-        uint32_t hw = 0, lw = 0, bw = 0;
+        const uint32_t live = (uint32_t)(tap < a.taps);
+        uint32_t v[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const uint32_t cl = cg * 16u + (wd & 3u) * 4u + j;
-            const bool ok = mok && tap < a.taps && cl < cc;
-            const int32_t v = ok ? (int32_t)wrow[(uint64_t)(c0 + cl) * a.taps + tap] : 0;
-            sum += (uint32_t)v;
-            fit &= (uint32_t)(v >= -128 && v <= 127);
-            hw |= hi_byte(v) << (8 * j);
-            lw |= lo_byte(v) << (8 * j);
-            bw |= ((uint32_t)v & 0xFFu) << (8 * j);
+            const uint32_t ok = live & (uint32_t)(cl < cc);
+            const uint32_t off = ((((c0 + cl) * a.taps + tap) * 2u) & 0x7FFFFFFFu) | ((ok ^ 1u) << 31);
+            v[j] = (uint32_t)(uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, off, 0, 0);
+        }
+        uint32_t hw = 0, lw = 0, bw = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int32_t x = (int32_t)(int16_t)v[j];
+            sum += (uint32_t)x;
+            fit &= (uint32_t)(x >= -128 && x <= 127);
+            hw |= hi_byte(x) << (8 * j);
+            lw |= lo_byte(x) << (8 * j);
+            bw |= ((uint32_t)x & 0xFFu) << (8 * j);
         }
         uint8_t* dst = a.wpk + (uint64_t)(mt * a.steps + gs) * tile + r * 64u + wd * 4u;
         *reinterpret_cast<uint32_t*>(dst) = hw;
         *reinterpret_cast<uint32_t*>(dst + a.tb * 64u) = lw;
         *reinterpret_cast<uint32_t*>(a.wpk8 + (uint64_t)(mt * a.steps + gs) * tile8 + r * 64u + wd * 4u) = bw;
     }
-    // row sum (every real weight once; padding adds 0)
-    __shared__ uint32_t red[256];
-    red[threadIdx.x] = sum;
-    __syncthreads();
-    for (uint32_t s = 128; s > 0; s >>= 1) {
-        if (threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
-        __syncthreads();
+    // row sum (every real weight once; padding adds 0) and the int8 flag: per
+    // wave, then the four waves' values after one barrier
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) sum += (uint32_t)__shfl_xor((int)sum, o, 64);
+    const uint32_t wave_fit = __ballot(fit == 0u) == 0ull ? 1u : 0u;
+    __shared__ uint32_t red[2][4];
+    const uint32_t w = threadIdx.x >> 6;
+    if ((threadIdx.x & 63u) == 0) {
+        red[0][w] = sum;
+        red[1][w] = wave_fit;
     }
-    if (threadIdx.x == 0 && mok) a.wsum[m] = red[0];
-    const int all_fit = __syncthreads_and((int)fit);
-    if (threadIdx.x == 0) a.wfit[m] = all_fit ? 1u : 0u;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        if (mok) a.wsum[m] = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+        a.wfit[m] = red[1][0] & red[1][1] & red[1][2] & red[1][3];
+    }
 }
 
 // ------------------------------------------------------------- main kernel --
