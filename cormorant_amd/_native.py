@@ -22,6 +22,7 @@ EXPORTS = (
     "cm_selftest_div", "cm_selftest_finalize", "cm_matmul_ex", "cm_conv_ex",
     "cm_matmul_workspace_size", "cm_conv_workspace_size", "cm_set_workspace",
     "cm_matmul_noalloc", "cm_conv_packed_size", "cm_conv_pack", "cm_conv_packed_ex",
+    "cm_conv_pair_packed_size", "cm_conv_pair_pack", "cm_conv_pair_packed_ex",
 )
 
 CM_OK = 0
@@ -112,6 +113,10 @@ _SIGS = {
     "cm_conv_packed_size": (ctypes.c_size_t, [_u32] * 17),
     "cm_conv_pack": (_i, [_vp] + [_u32] * 17 + [_vp, ctypes.c_size_t, _vp]),
     "cm_conv_packed_ex": (_i, [_vp, _vp, _vp, _vp] + [_u32] * 17 + [ctypes.POINTER(CmEpilogue), _vp]),
+    "cm_conv_pair_packed_size": (ctypes.c_size_t, [_u32] * 14),
+    "cm_conv_pair_pack": (_i, [_vp, _vp] + [_u32] * 14 + [_vp, ctypes.c_size_t, _vp]),
+    "cm_conv_pair_packed_ex": (_i, [_vp, _vp, _vp, _vp, _vp] + [_u32] * 15 +
+                               [ctypes.POINTER(CmEpilogue), _vp]),
 }
 
 _lib = None

@@ -237,6 +237,47 @@ int cm_conv_packed_ex(const int16_t* x, const void* packed, const int16_t* bias,
                                     dilation_w, pad_top, pad_left, epi, pick(stream));
 }
 
+size_t cm_conv_pair_packed_size(uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                                uint32_t mid_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
+                                uint32_t stride, uint32_t dilation, uint32_t pad_top, uint32_t pad_left,
+                                uint32_t out_ch) {
+    if ((uint64_t)batch * mid_ch * out_ch * out_h * out_w == 0 || kh * kw < 2) return 0;
+    return cm_conv_pair_pgemm_bytes(batch, in_ch, in_h, in_w, mid_ch, out_h, out_w, kh, kw, stride,
+                                     dilation, pad_top, pad_left, out_ch);
+}
+
+int cm_conv_pair_pack(const int16_t* w1, const int16_t* w2, uint32_t batch, uint32_t in_ch,
+                      uint32_t in_h, uint32_t in_w, uint32_t mid_ch, uint32_t out_h, uint32_t out_w,
+                      uint32_t kh, uint32_t kw, uint32_t stride, uint32_t dilation, uint32_t pad_top,
+                      uint32_t pad_left, uint32_t out_ch, void* packed, size_t packed_bytes,
+                      hipStream_t stream) {
+    if (!w1 || !w2 || !packed) return cm_set_error(CM_ERR_INVALID, "conv pair pack: null weights or packed");
+    if (cm_conv_pair_packed_size(batch, in_ch, in_h, in_w, mid_ch, out_h, out_w, kh, kw, stride, dilation,
+                                 pad_top, pad_left, out_ch) == 0)
+        return cm_set_error(CM_ERR_INVALID, "conv pair pack: the shapes do not take the pair path");
+    return cm_conv_pair_pgemm_pack(w1, w2, batch, in_ch, in_h, in_w, mid_ch, out_h, out_w, kh, kw, stride,
+                             dilation, pad_top, pad_left, out_ch, packed, packed_bytes, pick(stream));
+}
+
+int cm_conv_pair_packed_ex(const int16_t* x, const void* packed, const int16_t* bias1,
+                           const int16_t* bias2, int16_t* y, uint32_t batch, uint32_t in_ch,
+                           uint32_t in_h, uint32_t in_w, uint32_t mid_ch, uint32_t out_h,
+                           uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride,
+                           uint32_t dilation, uint32_t pad_top, uint32_t pad_left, uint32_t out_ch,
+                           uint32_t act1, const cm_epilogue_t* epi2, hipStream_t stream) {
+    if ((uint64_t)batch * out_ch * out_h * out_w == 0) return CM_OK;
+    if (!x || !packed || !y) return cm_set_error(CM_ERR_INVALID, "conv pair: null x, packed or y");
+    if (act1 > 2u) return cm_set_error(CM_ERR_INVALID, "conv pair: act1 %u (0 none, 1 Relu, 2 Clip(0,6))", act1);
+    const int rc = check_epilogue(epi2, false, "conv pair");
+    if (rc) return rc;
+    if (cm_conv_pair_packed_size(batch, in_ch, in_h, in_w, mid_ch, out_h, out_w, kh, kw, stride, dilation,
+                                 pad_top, pad_left, out_ch) == 0)
+        return cm_set_error(CM_ERR_INVALID, "conv pair: the shapes do not take the pair path");
+    return cm_conv_pair_pgemm_run(x, packed, bias1, bias2, y, batch, in_ch, in_h, in_w, mid_ch, out_h,
+                                   out_w, kh, kw, stride, dilation, pad_top, pad_left, out_ch, act1, epi2,
+                                   pick(stream));
+}
+
 int cm_pool(const int16_t* x, int16_t* y, uint32_t batch, uint32_t channels, uint32_t in_h,
             uint32_t in_w, uint32_t out_h, uint32_t out_w, uint32_t pool_h, uint32_t pool_w,
             uint32_t stride_h, uint32_t stride_w, uint32_t pad_top, uint32_t pad_left,

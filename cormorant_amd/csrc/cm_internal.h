@@ -118,6 +118,22 @@ int cm_conv_pgemm_run_packed(const int16_t* x, const void* packed, const int16_t
                              uint32_t out_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
                              uint32_t sh, uint32_t sw, uint32_t dh, uint32_t dw, uint32_t pad_top,
                              uint32_t pad_left, const cm_epilogue_t* epi, hipStream_t s);
+// A patch-GEMM convolution and a 1x1 convolution of its output in one launch
+// (conv_pgemm.hip): packed-weight bytes (0 when the shapes do not take the
+// path), the pack of both weight sets, and the run with them.
+size_t cm_conv_pair_pgemm_bytes(uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                                 uint32_t mid_ch, uint32_t out_h, uint32_t out_w, uint32_t kh,
+                                 uint32_t kw, uint32_t stride, uint32_t dilation, uint32_t pad_top,
+                                 uint32_t pad_left, uint32_t out_ch);
+int cm_conv_pair_pgemm_pack(const int16_t* w1, const int16_t* w2, uint32_t batch, uint32_t in_ch, uint32_t in_h,
+                      uint32_t in_w, uint32_t mid_ch, uint32_t out_h, uint32_t out_w, uint32_t kh,
+                      uint32_t kw, uint32_t stride, uint32_t dilation, uint32_t pad_top, uint32_t pad_left,
+                      uint32_t out_ch, void* dst, size_t bytes, hipStream_t s);
+int cm_conv_pair_pgemm_run(const int16_t* x, const void* packed, const int16_t* bias1, const int16_t* bias2,
+                            int16_t* y, uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                            uint32_t mid_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
+                            uint32_t stride, uint32_t dilation, uint32_t pad_top, uint32_t pad_left,
+                            uint32_t out_ch, uint32_t act1, const cm_epilogue_t* epi2, hipStream_t s);
 // 3x3 convolution through an LDS-staged input patch (conv_patch.hip); returns
 // 1, launching nothing, for shapes it does not take.
 int cm_conv_patch_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,

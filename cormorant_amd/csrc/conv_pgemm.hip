@@ -80,6 +80,17 @@ struct PgArgs {
     uint32_t pk8_off;            // byte offset of the int8 plane
     uint64_t x_img, y_img;
     EpiArgs epi;
+    // PAIR: a 1x1 convolution (M2 output channels) applied to this convolution's
+    // output, which never leaves LDS; y, y_img and epi then describe the 1x1's
+    // output, act1 the activation of the middle tensor
+    const uint8_t* wpk2;         // the 1x1's packed weight planes (32-row tiles)
+    const uint32_t* wsum2;       // [M2] its weight row sums
+    const uint32_t* wfit2;       // [M2] 1 when the row's weights are all int8
+    const int16_t* bias2;
+    uint32_t M2, steps2, HP;     // 1x1 output channels; its k steps; LDS bytes per middle-tile pixel
+    uint32_t hp_off, cs_off, rt2_off;   // LDS: middle-tile planes, pixel column sums, 1x1 row terms
+    uint32_t pk2_bytes, pk2_8off;       // buffer range of the 1x1's planes; offset of its int8 plane
+    uint32_t act1;
 };
 
 __device__ __forceinline__ int32_t bsum16(v4i v, int32_t acc) {
@@ -209,9 +220,16 @@ __device__ __forceinline__ void wave_sync() {
 // NS: A fragment sets in flight (3: two steps of prefetch, without MULTI and
 // with a step count that is a multiple of 3; else 2: one step).
 // WR: wave rows (row tile of 32 * WR output channels).
-template <int VEC, bool MULTI, int NS, int WR>
+// PAIR: the block's outputs (every output channel: one row tile) feed a 1x1
+// convolution in the same launch.  After a sub-tile's k loop the waves write
+// the middle tensor (act1 applied) into LDS as limb planes, pixel-major (byte c
+// of pixel px's row: channel c, the 1x1's k order), and after a barrier each
+// wave computes 32 x 64 tiles of the 1x1 (A from its packed planes, B from the
+// middle tile) and finishes them through the epilogue.
+template <int VEC, bool MULTI, int NS, int WR, bool PAIR>
 __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
     static_assert(NS == 2 || (NS == 3 && !MULTI), "three A sets need one patch of every channel");
+    static_assert(!(PAIR && MULTI), "a pair needs one patch of every channel");
     constexpr uint32_t TB = 32u * WR;             // output channels per row tile
     constexpr uint32_t WC = 4u / WR;              // wave columns
     constexpr uint32_t SPX = 64u * WC;            // pixels per sub-tile
@@ -254,6 +272,7 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
     const int32_t ih_first = (int32_t)(oh_a * g.S) - (int32_t)g.pt;
     const __amdgpu_buffer_rsrc_t xrs = make_rsrc(g.x + (uint64_t)n * g.x_img, g.x_img_bytes);
     const __amdgpu_buffer_rsrc_t wrs = make_rsrc(reinterpret_cast<const int16_t*>(g.wpk), g.pk_bytes);
+    const __amdgpu_buffer_rsrc_t wrs2 = make_rsrc(reinterpret_cast<const int16_t*>(g.wpk2), g.pk2_bytes);
     const uint32_t hw_in = g.H * g.W;
 
     if (tid == 0) {   // the zero slot: 16 bytes of each plane holding the limbs of 0
@@ -288,6 +307,25 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
     const uint32_t rm = min(row0 + (tid & (TB - 1)), g.M - 1u);
     const uint32_t ld_wsum = g.wsum[rm], ld_fit = g.wfit[rm];
     const int32_t ld_bias = g.bias ? (int32_t)g.bias[rm] : 0;
+    // PAIR: the 1x1's row terms and int8 flags (thread t: its row t), written
+    // to LDS with the first conv's after the patch is staged; the middle tile's
+    // bytes start as the limbs of 0 (k positions past the middle channels keep
+    // them: the limb identity's zero operand)
+    uint32_t ld_wsum2 = 0, ld_fit2 = 1u;
+    int32_t ld_bias2 = 0;
+    if constexpr (PAIR) {
+        const uint32_t r2 = min(tid, g.M2 - 1u);
+        ld_wsum2 = g.wsum2[r2];
+        ld_fit2 = g.wfit2[r2];
+        ld_bias2 = g.bias2 ? (int32_t)g.bias2[r2] : 0;
+        const uint32_t nv = (SPX * g.HP + 64u) / 16u;   // a plane and its 64 padding bytes
+        for (uint32_t v = tid; v < nv; v += kPgThreads) {
+            *reinterpret_cast<v4u*>(lds + g.hp_off + v * 16u) = v4u{0u, 0u, 0u, 0u};
+            *reinterpret_cast<v4u*>(lds + g.hp_off + SPX * g.HP + 64u + v * 16u) =
+                v4u{0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
+        }
+    }
+    bool fast2 = true;   // PAIR: every 1x1 weight fits int8 (two limb products)
 
     // Patch staging of one chunk (the range's rows; tasks past prows_b are
     // skipped).  Rows outside the image and channels past C read 0 through the
@@ -462,6 +500,80 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
     const uint32_t kp_term = 16384u * 64u * g.steps;
     const int32_t lo = q88::act_lo(g.epi.act), hi = q88::act_hi(g.epi.act);
     const bool plain = g.epi.add_mode == 0u && g.epi.act == 0u;   // no Add, no activation
+    // Epilogue, per wave, of a 32-row x 64-pixel accumulator tile (output rows
+    // m_base.., rows from m_end on skipped; pixels p0w.. of the range, pnw of them
+    // valid, njw 16-pixel column tiles in use): each 16-row half is finished into
+    // the wave's LDS tile (row 4*(lane/16)+e, pixel column of the lane), then read
+    // back as 8-pixel runs: lane -> (row lane/8 + 8t, pixels 8*(lane%8)..)
+    auto finish_tile = [&](const v4i (&th)[2][4], const v4i (&tm)[2][4], const v4i (&tl)[2][4],
+                           uint32_t m_base, uint32_t m_end, uint32_t p0w, uint32_t pnw, uint32_t njw) {
+        const uint32_t c8 = (lane & 7) * 8;
+        const uint32_t ncol = c8 < pnw ? min(8u, pnw - c8) : 0u;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                if ((uint32_t)j >= njw) continue;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint32_t v = ((uint32_t)th[i][j][e] << 16) + ((uint32_t)tm[i][j][e] << 8) +
+                                       (uint32_t)tl[i][j][e];
+                    et[((lane >> 4) * 4 + e) * kEpiPitch + j * 16 + (lane & 15)] = q88::acc_to_data(v);
+                }
+            }
+            wave_sync();
+            if (ncol) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const uint32_t r = (lane >> 3) + 8 * t;
+                    const uint32_t m = m_base + i * 16 + r;
+                    if (m >= m_end) continue;
+                    const uint64_t o = (uint64_t)n * g.y_img + (uint64_t)m * g.P + p0w + c8;
+                    const v4u tv = *reinterpret_cast<const v4u*>(et + r * kEpiPitch + c8);
+                    int16_t* yp = g.y + o;
+                    const bool vec8 = ncol == 8u && g.vw == 8u;
+                    if (plain && vec8) {
+                        *reinterpret_cast<v4u*>(yp) = tv;
+                        continue;
+                    }
+                    int32_t yv[8];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        yv[2 * q] = (int32_t)(int16_t)(tv[q] & 0xFFFFu);
+                        yv[2 * q + 1] = (int32_t)tv[q] >> 16;
+                    }
+                    if (g.epi.add_mode == 1u) {
+                        const int16_t* ap = g.epi.add + o;
+                        int32_t add[8];
+                        if (vec8) {
+                            const v4u a = *reinterpret_cast<const v4u*>(ap);
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) {
+                                add[2 * q] = (int32_t)(int16_t)(a[q] & 0xFFFFu);
+                                add[2 * q + 1] = (int32_t)a[q] >> 16;
+                            }
+                        } else {
+#pragma unroll
+                            for (int q = 0; q < 8; ++q) add[q] = (uint32_t)q < ncol ? ap[q] : 0;
+                        }
+#pragma unroll
+                        for (int q = 0; q < 8; ++q) yv[q] = q88::add(yv[q], add[q]);
+                    }
+#pragma unroll
+                    for (int q = 0; q < 8; ++q) yv[q] = q88::clamp(yv[q], lo, hi);
+                    if (vec8) {
+                        *reinterpret_cast<v4u*>(yp) = v4u{pack2(yv[0], yv[1]), pack2(yv[2], yv[3]),
+                                                          pack2(yv[4], yv[5]), pack2(yv[6], yv[7])};
+                    } else {
+#pragma unroll
+                        for (int q = 0; q < 8; ++q)
+                            if ((uint32_t)q < ncol) yp[q] = (int16_t)yv[q];
+                    }
+                }
+            }
+            wave_sync();   // the tile's reads are done before the next half overwrites it
+        }
+    };
     const uint32_t nsub = (pe - pb + SPX - 1) / SPX;
     // A fragment sets: the set of global step gs is gs % NS, and the next NS - 1
     // steps' sets are in flight while a step's MFMAs run
@@ -497,6 +609,12 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
             if (sub == 0) {
                 const bool real = row0 + tid < g.M;
                 if (tid < TB) rowterm_s[tid] = real ? 128u * ld_wsum + (uint32_t)ld_bias * 256u : 0u;
+                if constexpr (PAIR) {
+                    if (tid < ((g.M2 + 31u) & ~31u))
+                        reinterpret_cast<uint32_t*>(lds + g.rt2_off)[tid] =
+                            tid < g.M2 ? 128u * ld_wsum2 + (uint32_t)ld_bias2 * 256u : 0u;
+                    fast2 = __syncthreads_and(tid >= g.M2 || ld_fit2 != 0u) != 0;
+                }
                 fast = __syncthreads_and(tid >= TB || !real || ld_fit != 0u) != 0;
                 if (!fast) {
                     a_load(0, fa_h[0], fa_l[0]);
@@ -666,74 +784,113 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
             else k_loop(std::false_type{}, std::false_type{});
         }
 
-        // epilogue, per wave: each 16-channel half of the wave's rows is finished
-        // into its LDS tile (row 4*(lane/16)+e, pixel column of the lane), then
-        // read back as 8-pixel runs: lane -> (row lane/8 + 8t, pixels 8*(lane%8)..)
-        const uint32_t c8 = (lane & 7) * 8;
-        const uint32_t ncol = c8 < pn ? min(8u, pn - c8) : 0u;
+        if constexpr (!PAIR) {
+            finish_tile(hh, mid, ll, wrow, g.M, p0, pn, nj);
+        } else {
+            // the middle tensor of this sub-tile, act1(sat16(acc >> 8)), as limb
+            // planes: pixel px of the sub-tile at px * HP, channel c at byte c
+            // (rows past the middle channels hold 0: their weights are 0)
+            uint8_t* h_hi = lds + g.hp_off;
+            uint8_t* h_lo = h_hi + SPX * g.HP + 64u;
+            const int32_t lo1 = q88::act_lo(g.act1), hi1 = q88::act_hi(g.act1);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+            for (int i = 0; i < 2; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                if ((uint32_t)j >= nj) continue;
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t hw = 0, lw = 0;
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t v = ((uint32_t)hh[i][j][e] << 16) + ((uint32_t)mid[i][j][e] << 8) +
-                                       (uint32_t)ll[i][j][e];
-                    et[((lane >> 4) * 4 + e) * kEpiPitch + j * 16 + (lane & 15)] = q88::acc_to_data(v);
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t v = ((uint32_t)hh[i][j][e] << 16) + ((uint32_t)mid[i][j][e] << 8) +
+                                           (uint32_t)ll[i][j][e];
+                        const int32_t d = q88::clamp((int32_t)q88::acc_to_data(v), lo1, hi1);
+                        hw |= hi_byte(d) << (8 * e);
+                        lw |= lo_byte(d) << (8 * e);
+                    }
+                    const uint32_t a = (wc * 64u + j * 16u + (lane & 15)) * g.HP + wr * 32u + i * 16u +
+                                       (lane >> 4) * 4u;
+                    *reinterpret_cast<uint32_t*>(h_hi + a) = hw;
+                    *reinterpret_cast<uint32_t*>(h_lo + a) = lw;
                 }
+            __syncthreads();
+            // four limb products: each pixel's sum over the 1x1's k positions
+            uint32_t* cs = reinterpret_cast<uint32_t*>(lds + g.cs_off);
+            if (!fast2) {
+                for (uint32_t px = tid; px < SPX; px += kPgThreads) {
+                    int32_t sh = 0, sl = 0;
+                    for (uint32_t c = 0; c < g.steps2 * 4u; ++c) {
+                        sh = bsum16(*reinterpret_cast<const v4i*>(h_hi + px * g.HP + c * 16u), sh);
+                        sl = bsum16(*reinterpret_cast<const v4i*>(h_lo + px * g.HP + c * 16u), sl);
+                    }
+                    cs[px] = 256u * (uint32_t)sh + (uint32_t)sl + 128u * 64u * g.steps2;
+                }
+                __syncthreads();
             }
-            wave_sync();
-            if (ncol) {
+            // the 1x1: 32 x 64 tiles (row tile rt of its outputs, wave column cw's
+            // pixels) dealt over the waves
+            const uint32_t* rt2 = reinterpret_cast<const uint32_t*>(lds + g.rt2_off);
+            const uint32_t nrt2 = (g.M2 + 31u) / 32u;
+            const uint32_t kp2 = fast2 ? 0u : 16384u * 64u * g.steps2;
+            const uint32_t arow = (lane & 15) * 64u + (lane >> 4) * 16u;
+            for (uint32_t t = wave; t < nrt2 * WC; t += 4u) {
+                const uint32_t rt = t / WC, cw = t - rt * WC;
+                const uint32_t p0w = pb + sub * SPX + cw * 64u;
+                const uint32_t pnw = p0w < pe ? min(64u, pe - p0w) : 0u;
+                if (pnw == 0u) continue;
+                const uint32_t njw = (pnw + 15u) / 16u;
+                v4i h2[2][4], m2[2][4], l2[2][4];
 #pragma unroll
-                for (int t = 0; t < 2; ++t) {
-                    const uint32_t r = (lane >> 3) + 8 * t;
-                    const uint32_t m = wrow + i * 16 + r;
-                    if (m >= g.M) continue;
-                    const uint64_t o = (uint64_t)n * g.y_img + (uint64_t)m * g.P + p0 + c8;
-                    const v4u tv = *reinterpret_cast<const v4u*>(et + r * kEpiPitch + c8);
-                    int16_t* yp = g.y + o;
-                    const bool vec8 = ncol == 8u && g.vw == 8u;
-                    if (plain && vec8) {
-                        *reinterpret_cast<v4u*>(yp) = tv;
-                        continue;
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        h2[i][j] = v4i{0, 0, 0, 0};
+                        m2[i][j] = v4i{0, 0, 0, 0};
+                        const uint32_t colt = fast2 ? 0u : 128u * cs[cw * 64u + j * 16u + (lane & 15)];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            l2[i][j][e] = (int32_t)(rt2[rt * 32u + i * 16u + (lane >> 4) * 4u + e] - kp2 + colt);
                     }
-                    int32_t yv[8];
+                for (uint32_t s2 = 0; s2 < g.steps2; ++s2) {
+                    const uint32_t ro = rt * g.steps2 + s2;
+                    v4i ah[2], al[2];
 #pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        yv[2 * q] = (int32_t)(int16_t)(tv[q] & 0xFFFFu);
-                        yv[2 * q + 1] = (int32_t)tv[q] >> 16;
+                    for (int i = 0; i < 2; ++i) {
+                        if (fast2) {
+                            ah[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                wrs2, g.pk2_8off + ro * 2048u + i * 1024u + arow, 0, 0));
+                            al[i] = ah[i];
+                        } else {
+                            ah[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                wrs2, ro * 4096u + i * 1024u + arow, 0, 0));
+                            al[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                wrs2, ro * 4096u + 2048u + i * 1024u + arow, 0, 0));
+                        }
                     }
-                    if (g.epi.add_mode == 1u) {
-                        const int16_t* ap = g.epi.add + o;
-                        int32_t add[8];
-                        if (vec8) {
-                            const v4u a = *reinterpret_cast<const v4u*>(ap);
 #pragma unroll
-                            for (int q = 0; q < 4; ++q) {
-                                add[2 * q] = (int32_t)(int16_t)(a[q] & 0xFFFFu);
-                                add[2 * q + 1] = (int32_t)a[q] >> 16;
+                    for (int j = 0; j < 4; ++j) {
+                        if ((uint32_t)j >= njw) continue;
+                        const uint32_t b = (cw * 64u + j * 16u + (lane & 15)) * g.HP + s2 * 64u + (lane >> 4) * 16u;
+                        const v4i bh = *reinterpret_cast<const v4i*>(h_hi + b);
+                        const v4i bl = *reinterpret_cast<const v4i*>(h_lo + b);
+                        if (fast2) {   // sum w*x = 256 * sum w*x_hi + sum w*x_lo + 128 * sum w
+#pragma unroll
+                            for (int i = 0; i < 2; ++i) {
+                                m2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bh, m2[i][j], 0, 0, 0);
+                                l2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bl, l2[i][j], 0, 0, 0);
                             }
                         } else {
 #pragma unroll
-                            for (int q = 0; q < 8; ++q) add[q] = (uint32_t)q < ncol ? ap[q] : 0;
+                            for (int i = 0; i < 2; ++i) {
+                                h2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bh, h2[i][j], 0, 0, 0);
+                                m2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bl, m2[i][j], 0, 0, 0);
+                                l2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], bl, l2[i][j], 0, 0, 0);
+                                m2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], bh, m2[i][j], 0, 0, 0);
+                            }
                         }
-#pragma unroll
-                        for (int q = 0; q < 8; ++q) yv[q] = q88::add(yv[q], add[q]);
-                    }
-#pragma unroll
-                    for (int q = 0; q < 8; ++q) yv[q] = q88::clamp(yv[q], lo, hi);
-                    if (vec8) {
-                        *reinterpret_cast<v4u*>(yp) = v4u{pack2(yv[0], yv[1]), pack2(yv[2], yv[3]),
-                                                          pack2(yv[4], yv[5]), pack2(yv[6], yv[7])};
-                    } else {
-#pragma unroll
-                        for (int q = 0; q < 8; ++q)
-                            if ((uint32_t)q < ncol) yp[q] = (int16_t)yv[q];
                     }
                 }
+                finish_tile(h2, m2, l2, rt * 32u, g.M2, p0w, pnw, njw);
             }
-            wave_sync();   // the tile's reads are done before the next half overwrites it
+            if (sub + 1 < nsub) __syncthreads();   // the next sub-tile's middle tile overwrites this one
         }
     }
 }
@@ -773,6 +930,17 @@ namespace {
 
 enum PgMode { kPackAndRun, kPackOnly, kRunPacked };
 
+// A 1x1 convolution fused after the patch GEMM (the pair path): its weights
+// [out_ch][mid] (mid = the first convolution's output channels), bias, and the
+// activation applied to the middle tensor.
+struct PairSpec {
+    const int16_t* w2;
+    const int16_t* bias2;
+    uint32_t out_ch;
+    uint32_t act1;
+};
+constexpr uint32_t kPairMaxOut = 256;   // the 1x1's output channels: one per thread for its row terms
+
 // One patch-GEMM call: pack the weights into lc.ws and run (kPackAndRun), only
 // pack them into `dst` (kPackOnly), or run with weights packed earlier
 // (kRunPacked, `packed`).  Returns 1 (launching nothing) when the shape does
@@ -782,7 +950,8 @@ int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* 
               uint32_t in_ch, uint32_t in_h, uint32_t in_w, uint32_t out_ch, uint32_t out_h,
               uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t sh, uint32_t sw, uint32_t dh,
               uint32_t dw, uint32_t pad_top, uint32_t pad_left, const cm_epilogue_t* epi,
-              const LaunchCtx& lc, PgMode mode, const void* packed, void* dst, size_t dst_bytes) {
+              const LaunchCtx& lc, PgMode mode, const void* packed, void* dst, size_t dst_bytes,
+              const PairSpec* pair = nullptr) {
     const EpiArgs ea = cm_epi_args(epi);
     if (in_ch == 0 || out_ch == 0 || kh == 0 || kw == 0 || sh == 0 || dh == 0) return 1;
     // one stride / dilation pair for both axes keeps the patch rows and columns alike
@@ -801,6 +970,22 @@ int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* 
     const uint32_t mtiles = (out_ch + TB - 1) / TB;
     const uint32_t gg = gcd(sh, dh), Sg = sh / gg, Dg = dh / gg;
     if ((uint64_t)out_ch * P * 2 >= 0x80000000ull) return 1;
+    // pair: one row tile holds every middle channel; the 1x1's k steps (64
+    // channels each, at most two) and its LDS: the middle tile's two planes,
+    // pixel column sums and row terms.  HP, the bytes per pixel, is an odd
+    // multiple of 16 with room for the TB channels the waves write: 48 for a
+    // 32-row tile (the 1x1's one k step then reads 16 bytes of the next pixel:
+    // k positions whose weights are 0, read alike by the MFMAs and the column
+    // sums, so the limb identity stays exact), else the k bytes + 16 (80 or
+    // 144).  Each plane ends in 64 bytes of the limbs of 0, which the last
+    // pixel's read reaches.
+    const uint32_t m2 = pair ? pair->out_ch : 0u;
+    const uint32_t steps2 = pair ? (out_ch + 63u) / 64u : 0u;
+    const uint32_t HP = !pair ? 0u : TB == 32u ? 48u : std::max(steps2 * 64u, TB) + 16u;
+    if (pair && (mtiles != 1u || m2 == 0u || m2 > kPairMaxOut || pair->act1 > 2u ||
+                 (uint64_t)m2 * P * 2 >= 0x80000000ull))
+        return 1;
+    const uint64_t pair_lds = pair ? 2ull * (SPX * HP + 64u) + 4ull * SPX + 4ull * kPairMaxOut : 0u;
     // 16-byte patch loads: rows 16-byte aligned, and g = 1 or 2
     const uint32_t vec = (in_w % 8 == 0 && aligned(x, 16) && (gg == 1 || gg == 2)) ? gg : 0u;
     // patch columns a window reaches; with 16-byte loads the rows are widened to
@@ -823,7 +1008,7 @@ int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* 
         const uint64_t p_plane = prows * PW * pitch + 16;
         spos_off = a16(2 * p_plane);
         epi_off = spos_off + a16(prows * PW * 4);
-        return epi_off + 4ull * kEpiBytes;
+        return epi_off + 4ull * kEpiBytes + pair_lds;
     };
     // Pixels per block L (a multiple of 16): the fewest modelled cycles per CU,
     // with blocks dealt over the CUs two at a time.  A wave's 16-pixel column
@@ -873,7 +1058,7 @@ int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* 
     uint32_t ppitch = pitch_of(cpt_all);
     bool multi = false;
     uint32_t L = steps * 4u <= (uint32_t)kMaxQ ? pick_l(false, ppitch, prows) : 0u;
-    if (L == 0 && nchunks > 1) {
+    if (L == 0 && nchunks > 1 && !pair) {
         multi = true;
         ppitch = pitch_of(4u);
         L = pick_l(true, ppitch, prows);
@@ -887,7 +1072,13 @@ int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* 
     // workspace: limb planes, int8 plane, row sums, int8 flags
     const uint64_t pk_limb = (uint64_t)mtiles * steps * (2u * TB * 64u);
     const uint64_t pk_bytes = pk_limb + (uint64_t)mtiles * steps * (TB * 64u);
-    const uint64_t need = pk_bytes + 8ull * mtiles * TB;
+    // pair: the 1x1's packed weights after the first convolution's (32-row
+    // tiles, the same plane layout with one tap), then its row sums and flags
+    const uint32_t mtiles2 = (m2 + 31u) / 32u;
+    const uint64_t off2 = pair ? (pk_bytes + 8ull * mtiles * TB + 255u) & ~255ull : 0u;
+    const uint64_t pk2_limb = (uint64_t)mtiles2 * steps2 * (2u * 32u * 64u);
+    const uint64_t pk2_bytes = pk2_limb + (uint64_t)mtiles2 * steps2 * (32u * 64u);
+    const uint64_t need = pair ? off2 + pk2_bytes + 8ull * mtiles2 * 32u : pk_bytes + 8ull * mtiles * TB;
     if (pk_bytes >= 0x80000000ull) return 1;
     if (lc.need) {
         if (need > *lc.need) *lc.need = need;
@@ -909,7 +1100,15 @@ int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* 
                     reinterpret_cast<uint32_t*>(wbuf + pk_bytes) + mtiles * TB,
                     in_ch, out_ch, taps, nchunks, steps, taps, TB};
         hipLaunchKernelGGL(conv_wpack, dim3(mtiles * TB), dim3(256), 0, lc.s, pa);
-        const int rc = cm_check_launch("conv_wpack");
+        int rc = cm_check_launch("conv_wpack");
+        if (!rc && pair) {
+            uint8_t* w2 = wbuf + off2;
+            PackArgs pb2{pair->w2, w2, w2 + pk2_limb, reinterpret_cast<uint32_t*>(w2 + pk2_bytes),
+                         reinterpret_cast<uint32_t*>(w2 + pk2_bytes) + mtiles2 * 32u,
+                         out_ch, m2, 1u, steps2, steps2, 1u, 32u};
+            hipLaunchKernelGGL(conv_wpack, dim3(mtiles2 * 32u), dim3(256), 0, lc.s, pb2);
+            rc = cm_check_launch("conv_wpack");
+        }
         if (rc || mode == kPackOnly) return rc;
     }
     const uint8_t* wpk = mode == kRunPacked ? static_cast<const uint8_t*>(packed) : wbuf;
@@ -952,19 +1151,35 @@ int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* 
     g.pk_bytes = (uint32_t)pk_bytes;
     g.pk8_off = (uint32_t)pk_limb;
     g.x_img = x_img;
-    g.y_img = (uint64_t)out_ch * P;
+    g.y_img = (uint64_t)(pair ? m2 : out_ch) * P;
     g.epi = ea;
+    if (pair) {
+        const uint8_t* w2 = wpk + off2;
+        g.wpk2 = w2;
+        g.wsum2 = reinterpret_cast<const uint32_t*>(w2 + pk2_bytes);
+        g.wfit2 = g.wsum2 + mtiles2 * 32u;
+        g.bias2 = pair->bias2;
+        g.M2 = m2; g.steps2 = steps2; g.HP = HP;
+        g.hp_off = (uint32_t)(epi_off + 4ull * kEpiBytes);
+        g.cs_off = g.hp_off + 2u * (SPX * HP + 64u);
+        g.rt2_off = g.cs_off + 4u * SPX;
+        g.pk2_bytes = (uint32_t)pk2_bytes;
+        g.pk2_8off = (uint32_t)pk2_limb;
+        g.act1 = pair->act1;
+    }
     // 16-byte output accesses: every run of 8 pixels starts 16-byte aligned
     // (ranges start at multiples of L, sub-tiles at multiples of 64 pixels)
     g.vw = P % 8 == 0 && aligned(y, 16) && (ea.add_mode != 1u || aligned(ea.add, 16)) ? 8u : 1u;
     const void* k = nullptr;
-#define CM_PG_PICK(M, NS, W) (vec == 1 ? (const void*)conv_pgemm<1, M, NS, W> \
-                              : vec == 2 ? (const void*)conv_pgemm<2, M, NS, W> : (const void*)conv_pgemm<0, M, NS, W>)
-#define CM_PG_PICK_W(M, NS) (wrows == 1 ? CM_PG_PICK(M, NS, 1) : wrows == 2 ? CM_PG_PICK(M, NS, 2) \
-                                                                     : CM_PG_PICK(M, NS, 4))
-    if (multi) k = CM_PG_PICK(true, 2, 4);
-    else if (steps % 3 == 0) k = CM_PG_PICK_W(false, 3);
-    else k = CM_PG_PICK_W(false, 2);
+#define CM_PG_PICK(M, NS, W, PR) (vec == 1 ? (const void*)conv_pgemm<1, M, NS, W, PR> \
+                                  : vec == 2 ? (const void*)conv_pgemm<2, M, NS, W, PR> \
+                                             : (const void*)conv_pgemm<0, M, NS, W, PR>)
+#define CM_PG_PICK_W(M, NS, PR) (wrows == 1 ? CM_PG_PICK(M, NS, 1, PR) : wrows == 2 ? CM_PG_PICK(M, NS, 2, PR) \
+                                                                             : CM_PG_PICK(M, NS, 4, PR))
+    if (multi) k = CM_PG_PICK(true, 2, 4, false);
+    else if (pair) k = steps % 3 == 0 ? CM_PG_PICK_W(false, 3, true) : CM_PG_PICK_W(false, 2, true);
+    else if (steps % 3 == 0) k = CM_PG_PICK_W(false, 3, false);
+    else k = CM_PG_PICK_W(false, 2, false);
 #undef CM_PG_PICK_W
 #undef CM_PG_PICK
     if (lds > 65536u &&
@@ -1031,4 +1246,47 @@ int cm_conv_pgemm_run_packed(const int16_t* x, const void* packed, const int16_t
                              sh, sw, dh, dw, pad_top, pad_left, epi, lc, kRunPacked, packed, nullptr, 0);
     return rc == 1 ? cm_set_error(CM_ERR_INVALID, "conv packed: the shape does not take the patch-GEMM path")
                    : rc;
+}
+
+// ------------------------------------------------------------- conv pair --
+// A standard convolution (the patch GEMM, every middle channel in one row tile)
+// with act1 applied, then a 1x1 convolution of its output, in one launch.
+size_t cm_conv_pair_pgemm_bytes(uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                                 uint32_t mid_ch, uint32_t out_h, uint32_t out_w, uint32_t kh,
+                                 uint32_t kw, uint32_t stride, uint32_t dilation, uint32_t pad_top,
+                                 uint32_t pad_left, uint32_t out_ch) {
+    size_t need = 0;
+    const LaunchCtx lc{nullptr, nullptr, 0, &need};
+    const int16_t* p = probe_ptr();
+    const PairSpec ps{p, p, out_ch, 0u};
+    const int rc = pg_launch(p, p, p, const_cast<int16_t*>(p), batch, in_ch, in_h, in_w, mid_ch, out_h,
+                             out_w, kh, kw, stride, stride, dilation, dilation, pad_top, pad_left, nullptr,
+                             lc, kPackOnly, nullptr, nullptr, 0, &ps);
+    return rc == CM_OK ? need : 0u;
+}
+
+int cm_conv_pair_pgemm_pack(const int16_t* w1, const int16_t* w2, uint32_t batch, uint32_t in_ch, uint32_t in_h,
+                      uint32_t in_w, uint32_t mid_ch, uint32_t out_h, uint32_t out_w, uint32_t kh,
+                      uint32_t kw, uint32_t stride, uint32_t dilation, uint32_t pad_top, uint32_t pad_left,
+                      uint32_t out_ch, void* dst, size_t bytes, hipStream_t s) {
+    const LaunchCtx lc{s, nullptr, 0, nullptr};
+    const int16_t* p = probe_ptr();
+    const PairSpec ps{w2, nullptr, out_ch, 0u};
+    const int rc = pg_launch(p, w1, nullptr, const_cast<int16_t*>(p), batch, in_ch, in_h, in_w, mid_ch,
+                             out_h, out_w, kh, kw, stride, stride, dilation, dilation, pad_top, pad_left,
+                             nullptr, lc, kPackOnly, nullptr, dst, bytes, &ps);
+    return rc == 1 ? cm_set_error(CM_ERR_INVALID, "conv pair pack: the shapes do not take the pair path") : rc;
+}
+
+int cm_conv_pair_pgemm_run(const int16_t* x, const void* packed, const int16_t* bias1, const int16_t* bias2,
+                            int16_t* y, uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                            uint32_t mid_ch, uint32_t out_h, uint32_t out_w, uint32_t kh, uint32_t kw,
+                            uint32_t stride, uint32_t dilation, uint32_t pad_top, uint32_t pad_left,
+                            uint32_t out_ch, uint32_t act1, const cm_epilogue_t* epi2, hipStream_t s) {
+    const LaunchCtx lc{s, nullptr, 0, nullptr};
+    const PairSpec ps{nullptr, bias2, out_ch, act1};
+    const int rc = pg_launch(x, nullptr, bias1, y, batch, in_ch, in_h, in_w, mid_ch, out_h, out_w, kh, kw,
+                             stride, stride, dilation, dilation, pad_top, pad_left, epi2, lc, kRunPacked,
+                             packed, nullptr, 0, &ps);
+    return rc == 1 ? cm_set_error(CM_ERR_INVALID, "conv pair: the shapes do not take the pair path") : rc;
 }

@@ -198,6 +198,50 @@ def ConvPackedKernel(x, packed, bias, y, batch, in_ch, in_h, in_w, out_ch, out_h
                  ctypes.byref(epi) if epi is not None else None, _stream(stream))
 
 
+def conv_pair_packed_size(batch, in_ch, in_h, in_w, mid_ch, out_h, out_w, kh, kw, stride,
+                          dilation, pad_top, pad_left, out_ch) -> int:
+    """Bytes of packed weights for ConvPairKernel: a kh x kw convolution in_ch -> mid_ch
+    (stride and dilation the same on both axes) and a 1x1 convolution mid_ch -> out_ch
+    of its output, in one launch (0: the shapes do not take that path)."""
+    args = [batch, in_ch, in_h, in_w, mid_ch, out_h, out_w, kh, kw, stride, dilation, pad_top,
+            pad_left, out_ch]
+    return int(_native.load().cm_conv_pair_packed_size(*(_u32("conv pair arg", v) for v in args)))
+
+
+def conv_pair_pack(w1, w2, packed, batch, in_ch, in_h, in_w, mid_ch, out_h, out_w, kh, kw, stride,
+                   dilation, pad_top, pad_left, out_ch, stream=None) -> None:
+    """Pack both convolutions' weights (ConvKernel layouts: [mid_ch][in_ch][kh][kw] and
+    [out_ch][mid_ch]) into the device tensor `packed` once."""
+    args = [batch, in_ch, in_h, in_w, mid_ch, out_h, out_w, kh, kw, stride, dilation, pad_top,
+            pad_left, out_ch]
+    args = [_u32("conv pair arg", v) for v in args]
+    p1 = _dev_ptr(w1, mid_ch * in_ch * kh * kw, "w1")
+    p2 = _dev_ptr(w2, out_ch * mid_ch, "w2")
+    pp, nbytes = _workspace(packed)
+    _native.call("cm_conv_pair_pack", p1, p2, *args, pp, nbytes, _stream(stream))
+
+
+def ConvPairKernel(x, packed, bias1, bias2, y, batch, in_ch, in_h, in_w, mid_ch, out_h, out_w, kh,
+                   kw, stride, dilation, pad_top, pad_left, out_ch, act1=ACT_NONE, add=None,
+                   act=ACT_NONE, stream=None) -> None:
+    """y = act(Add(Conv1x1(act1(Conv(x, w1, bias1)), w2, bias2), add)), with the weights
+    packed by conv_pair_pack; the middle tensor never leaves the GPU's LDS.  The same
+    result, bit for bit, as the two ConvKernel calls with their fused epilogues."""
+    args = [batch, in_ch, in_h, in_w, mid_ch, out_h, out_w, kh, kw, stride, dilation, pad_top,
+            pad_left, out_ch]
+    args = [_u32("conv pair arg", v) for v in args]
+    if batch * out_ch * out_h * out_w == 0:
+        return
+    px = _dev_ptr(x, batch * in_ch * in_h * in_w, "x")
+    pp, _ = _workspace(packed)
+    pb1 = _dev_ptr(bias1, mid_ch, "bias1") if bias1 is not None else None
+    pb2 = _dev_ptr(bias2, out_ch, "bias2") if bias2 is not None else None
+    py = _dev_ptr(y, batch * out_ch * out_h * out_w, "y")
+    epi = _epilogue(add, False, act, batch * out_ch * out_h * out_w)
+    _native.call("cm_conv_pair_packed_ex", px, pp, pb1, pb2, py, *args, _u32("act1", act1),
+                 ctypes.byref(epi) if epi is not None else None, _stream(stream))
+
+
 def PoolingKernel(x, y, batch, channels, in_h, in_w, out_h, out_w, pool_h, pool_w,
                   stride_h=1, stride_w=1, pad_top=0, pad_left=0, dil_h=1, dil_w=1,
                   pool_type=POOL_MAX, lp_order=2, count_include_pad=0, stream=None) -> None:

@@ -204,6 +204,38 @@ int cm_conv_packed_ex(const int16_t *x, const void *packed, const int16_t *bias,
                       uint32_t has_bias, uint32_t is_depthwise, const cm_epilogue_t *epi,
                       hipStream_t stream);
 
+/* A convolution and a 1x1 convolution of its output in one launch.  No
+ * counterpart in the reference, where they are two run_conv calls (with a
+ * run_op for the activation between them and one for a residual Add after):
+ * the scheduler session uses it for Conv -> Relu/Clip(0,6) -> Conv 1x1 chains
+ * whose middle tensor nothing else reads.  The first convolution: x
+ * [batch][in_ch][in_h][in_w], weights w1 [mid_ch][in_ch][kh][kw], the same
+ * stride and dilation on both axes, padding pad_top / pad_left, optional
+ * bias1, then act1 (0 none, 1 Relu, 2 Clip(0,6)); the second: weights w2
+ * [out_ch][mid_ch], optional bias2, then epi2 (a same-shaped Add and / or an
+ * activation); y [batch][out_ch][out_h][out_w].  The middle tensor stays in
+ * LDS.  cm_conv_pair_packed_size returns the packed-weight bytes (0 when the
+ * shapes do not take the path: mid_ch at most 128 and out_ch at most 256,
+ * and the first convolution's input rows must fit the kernel's LDS patch);
+ * cm_conv_pair_pack writes both weight sets (16-byte aligned device memory);
+ * cm_conv_pair_packed_ex computes, bit for bit, what the two cm_conv_ex calls
+ * with those epilogues compute. */
+size_t cm_conv_pair_packed_size(uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in_w,
+                                uint32_t mid_ch, uint32_t out_h, uint32_t out_w, uint32_t kh,
+                                uint32_t kw, uint32_t stride, uint32_t dilation, uint32_t pad_top,
+                                uint32_t pad_left, uint32_t out_ch);
+int cm_conv_pair_pack(const int16_t *w1, const int16_t *w2, uint32_t batch, uint32_t in_ch,
+                      uint32_t in_h, uint32_t in_w, uint32_t mid_ch, uint32_t out_h, uint32_t out_w,
+                      uint32_t kh, uint32_t kw, uint32_t stride, uint32_t dilation, uint32_t pad_top,
+                      uint32_t pad_left, uint32_t out_ch, void *packed, size_t packed_bytes,
+                      hipStream_t stream);
+int cm_conv_pair_packed_ex(const int16_t *x, const void *packed, const int16_t *bias1,
+                           const int16_t *bias2, int16_t *y, uint32_t batch, uint32_t in_ch,
+                           uint32_t in_h, uint32_t in_w, uint32_t mid_ch, uint32_t out_h,
+                           uint32_t out_w, uint32_t kh, uint32_t kw, uint32_t stride,
+                           uint32_t dilation, uint32_t pad_top, uint32_t pad_left, uint32_t out_ch,
+                           uint32_t act1, const cm_epilogue_t *epi2, hipStream_t stream);
+
 /* cm_matmul_ex for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
  * counterpart in the reference.  Same arguments and result as cm_matmul_ex
