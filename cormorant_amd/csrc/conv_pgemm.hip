@@ -985,7 +985,7 @@ int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* 
     if (pair && (mtiles != 1u || m2 == 0u || m2 > kPairMaxOut || pair->act1 > 2u ||
                  (uint64_t)m2 * P * 2 >= 0x80000000ull))
         return 1;
-    const uint64_t pair_lds = pair ? 2ull * (SPX * HP + 64u) + 4ull * SPX + 4ull * kPairMaxOut : 0u;
+    uint64_t pair_lds = pair ? 2ull * (SPX * HP + 64u) + 4ull * SPX + 4ull * kPairMaxOut : 0u;
     // 16-byte patch loads: rows 16-byte aligned, and g = 1 or 2
     const uint32_t vec = (in_w % 8 == 0 && aligned(x, 16) && (gg == 1 || gg == 2)) ? gg : 0u;
     // patch columns a window reaches; with 16-byte loads the rows are widened to
@@ -1058,6 +1058,17 @@ int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* 
     uint32_t ppitch = pitch_of(cpt_all);
     bool multi = false;
     uint32_t L = steps * 4u <= (uint32_t)kMaxQ ? pick_l(false, ppitch, prows) : 0u;
+    if (pair && L) {
+        // the middle tile's LDS must not cost the pair more than half of the
+        // pixel range the convolution alone would take (shorter ranges re-stage
+        // more halo rows in more blocks than the saved launch is worth)
+        const uint64_t keep = pair_lds;
+        uint64_t pr0 = 0;
+        pair_lds = 0;
+        const uint32_t L0 = pick_l(false, ppitch, pr0);
+        pair_lds = keep;
+        if (2u * L < L0) return 1;
+    }
     if (L == 0 && nchunks > 1 && !pair) {
         multi = true;
         ppitch = pitch_of(4u);

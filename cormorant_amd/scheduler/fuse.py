@@ -21,11 +21,20 @@ output must not share memory with them.  ``live_from`` gives each fused
 output's new first-use node (the MatMul / Conv node) for the pool layout, which
 then never places it in a slot its inputs occupy; ``fusions`` re-checks the
 actual storage of every fused group and drops any group that overlaps.
+
+Convolution pairs: a Conv (with its Relu / Clip(0,6)) whose output nothing but
+a 1x1 Conv (with its Add / activation) reads can run as one launch
+(``cm_conv_pair_packed_ex``) that keeps the middle tensor on chip:
+
+    conv [-> Relu | Clip(0,6)] -> conv 1x1 [-> Add (same-shaped)] [-> Relu | Clip(0,6)]
+
+``launch_list(plan, pair_ok)`` forms them where ``pair_ok`` (the backend's
+shape check) accepts the pair; the result is the same bit for bit.
 """
 from __future__ import annotations
 
 from dataclasses import dataclass
-from typing import Dict, List, Optional, Set, Tuple
+from typing import Callable, Dict, List, Optional, Set, Tuple
 
 from .nodes import OP_ADD, OP_RELU, OP_RELU6, KernelCall
 
@@ -43,6 +52,47 @@ class FusedCall:
     add: Optional[str]               # tensor added in the epilogue
     add_mode: int
     act: int
+
+    def __str__(self) -> str:
+        return " + ".join(str(c) for c in (self.call,) + self.absorbed)
+
+
+def _call_of(item) -> KernelCall:
+    return item.call if isinstance(item, FusedCall) else item
+
+
+def _absorbed(item) -> Tuple[KernelCall, ...]:
+    return item.absorbed if isinstance(item, FusedCall) else ()
+
+
+def _out_of(item) -> str:
+    return item.out if isinstance(item, FusedCall) else _writes(item)
+
+
+@dataclass(frozen=True)
+class PairCall:
+    """A convolution group and the 1x1 convolution group that alone reads its
+    output, as one launch.  ``call`` / ``absorbed`` list the member calls in
+    order (the first convolution, its activation, the 1x1 convolution, its Add
+    and activation), like a fused group's."""
+    first: object    # KernelCall or FusedCall: the convolution (activation only)
+    second: object   # KernelCall or FusedCall: the 1x1 convolution (same-shaped Add, activation)
+
+    @property
+    def call(self) -> KernelCall:
+        return _call_of(self.first)
+
+    @property
+    def absorbed(self) -> Tuple[KernelCall, ...]:
+        return _absorbed(self.first) + (_call_of(self.second),) + _absorbed(self.second)
+
+    @property
+    def out(self) -> str:
+        return _out_of(self.second)
+
+    @property
+    def act1(self) -> int:
+        return self.first.act if isinstance(self.first, FusedCall) else ACT_NONE
 
     def __str__(self) -> str:
         return " + ".join(str(c) for c in (self.call,) + self.absorbed)
@@ -176,10 +226,69 @@ def candidates(plan) -> List[Tuple[int, FusedCall]]:
     return out
 
 
+def _indexed(plan, groups: Dict[int, FusedCall]) -> List[Tuple[int, object]]:
+    """(index in plan.calls of the item's first call, item) with `groups` in place."""
+    seq: List[Tuple[int, object]] = []
+    calls = [c for _, c in plan.calls]
+    k = 0
+    while k < len(calls):
+        if k in groups:
+            seq.append((k, groups[k]))
+            k += 1 + len(groups[k].absorbed)
+        else:
+            seq.append((k, calls[k]))
+            k += 1
+    return seq
+
+
+def _pair_match(g: _Graph, ka: int, a, kb: int, b) -> Optional[PairCall]:
+    """The pair of items a (plan index ka) and b (plan index kb), or None."""
+    ca, cb = _call_of(a), _call_of(b)
+    if ca.kernel != "conv" or cb.kernel != "conv" or any(ca.offsets or ()) or any(cb.offsets or ()):
+        return None
+    n, _c, _h, _w, m, oh, ow, kh, kw, sh, sw, dh, dw, _pt, _pl, _hb, dwise = ca.args
+    if dwise or kh * kw < 2 or sh != sw or dh != dw:
+        return None
+    if isinstance(a, FusedCall) and a.add is not None:
+        return None
+    n2, c2, h2, w2, _m2, oh2, ow2, kh2, kw2, sh2, sw2, dh2, dw2, pt2, pl2, _hb2, dwise2 = cb.args
+    if dwise2 or (kh2, kw2, sh2, sw2, dh2, dw2, pt2, pl2) != (1, 1, 1, 1, 1, 1, 0, 0):
+        return None
+    if (n2, c2, h2, w2, oh2, ow2) != (n, m, oh, ow, oh, ow):
+        return None
+    if isinstance(b, FusedCall) and b.add_mode not in (ADD_NONE, ADD_SAME):
+        return None
+    mid = _out_of(a)
+    if cb.tensors[0] != mid or not g.private(mid, ka + len(_absorbed(a)), kb):
+        return None
+    return PairCall(a, b)
+
+
+def _pairs(plan, seq: List[Tuple[int, object]]) -> List[Tuple[int, PairCall]]:
+    """Every pair the call structure allows in seq (no storage or shape check)."""
+    g = _Graph(plan)
+    out: List[Tuple[int, PairCall]] = []
+    i = 0
+    while i + 1 < len(seq):
+        pc = _pair_match(g, seq[i][0], seq[i][1], seq[i + 1][0], seq[i + 1][1])
+        if pc is not None:
+            out.append((i, pc))
+            i += 2
+        else:
+            i += 1
+    return out
+
+
 def live_from(plan) -> Dict[str, int]:
-    """{fused output tensor: node index of its MatMul / Conv} for the pool layout."""
+    """{fused or paired output tensor: node index of its first MatMul / Conv} for
+    the pool layout."""
     node_of = [idx for idx, _ in plan.calls]
-    return {f.out: node_of[k] for k, f in candidates(plan)}
+    cands = candidates(plan)
+    starts = {f.out: node_of[k] for k, f in cands}
+    seq = _indexed(plan, dict(cands))
+    for i, pc in _pairs(plan, seq):
+        starts[pc.out] = node_of[seq[i][0]]
+    return starts
 
 
 def _span(plan, call: KernelCall, name: str) -> Tuple[str, str, int, int]:
@@ -212,17 +321,37 @@ def fusions(plan) -> List[Tuple[int, FusedCall]]:
     return ok
 
 
-def launch_list(plan) -> List[object]:
-    """plan.calls with every fusable group replaced by its FusedCall."""
-    groups = dict(fusions(plan))
-    seq: List[object] = []
-    k = 0
-    calls = [c for _, c in plan.calls]
-    while k < len(calls):
-        if k in groups:
-            seq.append(groups[k])
-            k += 1 + len(groups[k].absorbed)
+def _pair_storage_ok(plan, pc: PairCall) -> bool:
+    """The pair's output overlaps nothing the launch reads (its Add operand may
+    coincide with it exactly: in place)."""
+    cb = _call_of(pc.second)
+    out = _span(plan, pc.absorbed[-1], pc.out)
+    ins = [_span(plan, pc.call, n) for n in _reads(pc.call)]
+    ins += [_span(plan, cb, n) for n in _reads(cb) if n != cb.tensors[0]]
+    if any(_overlap(out, s) for s in ins):
+        return False
+    b = pc.second
+    if isinstance(b, FusedCall) and b.add is not None:
+        add = _span(plan, b.absorbed[0], b.add)
+        if _overlap(out, add) and add[2] != out[2]:
+            return False
+    return True
+
+
+def launch_list(plan, pair_ok: Optional[Callable[[PairCall], bool]] = None) -> List[object]:
+    """plan.calls with every fusable group replaced by its FusedCall and, when
+    ``pair_ok`` is given, every convolution pair it accepts by a PairCall."""
+    seq = _indexed(plan, dict(fusions(plan)))
+    if pair_ok is None:
+        return [item for _, item in seq]
+    pairs = {i: pc for i, pc in _pairs(plan, seq) if _pair_storage_ok(plan, pc) and pair_ok(pc)}
+    out: List[object] = []
+    i = 0
+    while i < len(seq):
+        if i in pairs:
+            out.append(pairs[i])
+            i += 2
         else:
-            seq.append(calls[k])
-            k += 1
-    return seq
+            out.append(seq[i][1])
+            i += 1
+    return out

@@ -17,7 +17,9 @@ Reshape / Squeeze / Unsqueeze / Dropout outputs are the same device address
 as their source; a graph output at the end of a reshape chain is written
 directly by the producing kernel.  With ``fuse=True`` (default) an Add /
 Relu / Clip(0,6) call that is the sole reader of a MatMul / Conv output runs
-in that call's epilogue (``fuse.py``); results are bit-identical either way.
+in that call's epilogue, and a convolution whose output only a 1x1
+convolution reads runs with it as one launch (``cm_conv_pair_packed_ex``,
+weights packed at init; ``fuse.py``); results are bit-identical either way.
 There is no CPU execution path: without the native library the constructor
 raises.
 """
@@ -45,14 +47,14 @@ class InferenceSession:
     def __init__(self, model, stream: int = 0, fuse: bool = True) -> None:
         self.graph = model if isinstance(model, OnnxGraph) else OnnxGraph(model)
         self.plan = BufferPlan(self.graph)
+        self._lib = _native.load()
         if fuse:
             starts = _fuse.live_from(self.plan)
             if starts:
                 self.plan = BufferPlan(self.graph, starts)
-            self.launch_list = _fuse.launch_list(self.plan)
+            self.launch_list = _fuse.launch_list(self.plan, pair_ok=lambda pc: self._packed_size(pc) > 0)
         else:
             self.launch_list = [c for _, c in self.plan.calls]
-        self._lib = _native.load()
         self.stream = int(stream)
         _native.call("cm_buf_pool_init")
         self._bufs: Dict[Tuple[str, str], object] = {}
@@ -83,9 +85,15 @@ class InferenceSession:
                 if self.workspace_bytes:
                     self._ws_ptr = base + 2 * ws_off
                 for i, (off, ps) in self._packed.items():
-                    call = self._call_of(self.launch_list[i])
+                    item = self.launch_list[i]
+                    call = self._call_of(item)
                     wptr = self.device_ptr(call.tensors[1]) + (2 * call.offsets[1] if call.offsets else 0)
-                    _native.call("cm_conv_pack", wptr, *call.args, base + off, ps, None)
+                    if isinstance(item, _fuse.PairCall):
+                        w2ptr = self.device_ptr(self._call_of(item.second).tensors[1])
+                        _native.call("cm_conv_pair_pack", wptr, w2ptr, *self._pair_args(item), base + off,
+                                     ps, None)
+                    else:
+                        _native.call("cm_conv_pack", wptr, *call.args, base + off, ps, None)
             for t in self.graph.input_tensors:
                 self._alloc(("input", t.onnx_name), self.plan.layouts[t.onnx_name].alloc)
             for t in self.graph.output_tensors:
@@ -132,15 +140,27 @@ class InferenceSession:
 
     @staticmethod
     def _call_of(item) -> KernelCall:
-        return item.call if isinstance(item, _fuse.FusedCall) else item
+        return item.call if isinstance(item, (_fuse.FusedCall, _fuse.PairCall)) else item
+
+    @classmethod
+    def _pair_args(cls, pc) -> Tuple[int, ...]:
+        """cm_conv_pair_* shape arguments: batch, in_ch, in_h, in_w, mid_ch, out_h,
+        out_w, kh, kw, stride, dilation, pad_top, pad_left, out_ch."""
+        a = pc.call.args
+        return (a[0], a[1], a[2], a[3], a[4], a[5], a[6], a[7], a[8], a[9], a[11], a[13], a[14],
+                cls._call_of(pc.second).args[4])
 
     def _packed_size(self, item) -> int:
+        if isinstance(item, _fuse.PairCall):
+            return int(self._lib.cm_conv_pair_packed_size(*self._pair_args(item)))
         call = self._call_of(item)
         if call.kernel != "conv":
             return 0
         return int(self._lib.cm_conv_packed_size(*call.args))
 
     def _workspace_need(self, item) -> int:
+        if isinstance(item, _fuse.PairCall):
+            return 0
         call = item.call if isinstance(item, _fuse.FusedCall) else item
         if call.kernel in ("matmul", "matmul_at"):
             return int(self._lib.cm_matmul_workspace_size(*call.args))
@@ -153,6 +173,22 @@ class InferenceSession:
         packed = self._packed.get(index)
         if packed is not None:   # packed weights in place of the weight tensor, no workspace
             ws = ()
+        if isinstance(item, _fuse.PairCall):
+            ca, cb = item.call, self._call_of(item.second)
+            epi = None
+            if isinstance(item.second, _fuse.FusedCall):
+                epi = _native.CmEpilogue()
+                epi.add = self.device_ptr(item.second.add) if item.second.add is not None else None
+                epi.add_mode = item.second.add_mode
+                epi.act = item.second.act
+            name = "cm_conv_pair_packed_ex"
+            args = (self.device_ptr(ca.tensors[0]),
+                    int(self._bufs[("pool", "")].contents.dev) + packed[0],
+                    self.device_ptr(ca.tensors[2]) if ca.args[15] else None,
+                    self.device_ptr(cb.tensors[2]) if cb.args[15] else None,
+                    self.device_ptr(item.out)) + self._pair_args(item) + (
+                        item.act1, ctypes.byref(epi) if epi is not None else None)
+            return getattr(self._lib, name), name, args, epi
         if isinstance(item, _fuse.FusedCall):
             call = item.call
             name = "cm_conv_ex" if call.kernel == "conv" else "cm_matmul_ex"

@@ -611,6 +611,69 @@ def test_fused_launches_mobilenet_small():
     np.testing.assert_array_equal(got, gs.run_plan(BufferPlan(g), {"X": x})["Y"])
 
 
+def test_conv_pairs_mobilenet():
+    """Each 3x3 convolution (its Clip(0,6) fused) whose output only the next 1x1
+    convolution reads pairs with that convolution's group: the 14 pairs whose
+    middle tensor has at most 128 channels, 38 launches -> 24; the paired launch
+    list, run on the oracle with every middle tensor kept out of the plan's
+    storage, gives the graph's output."""
+    g = graph(wl.mobilenet_model(batch=2, hw=32))
+    plan = BufferPlan(g, fuse.live_from(BufferPlan(g)))
+    seq = fuse.launch_list(plan, pair_ok=lambda pc: pc.call.args[4] <= 128)
+    pairs = [x for x in seq if isinstance(x, fuse.PairCall)]
+    assert len(pairs) == 14 and len(seq) == 24
+    assert all(p.act1 == fuse.ACT_RELU6 for p in pairs)
+    assert sum(isinstance(p.second, fuse.FusedCall) and p.second.add_mode == fuse.ADD_SAME
+               for p in pairs) == 8
+    assert str(pairs[0]).startswith("run_conv(conv0_y_r6, conv1_w, conv1_b, conv1_y,")
+    # every pair's output is live from its first convolution: it never shares a
+    # slot with that convolution's input
+    for p in pairs:
+        out = fuse._span(plan, p.absorbed[-1], p.out)
+        x = fuse._span(plan, p.call, p.call.tensors[0])
+        assert not fuse._overlap(out, x), str(p)
+    x = wl.mobilenet_input(2, 32)
+    oracle.set_threads(min(os.cpu_count() or 1, 8))
+    got = gs.run_plan(plan, {"X": x}, launches=seq)["Y"]
+    np.testing.assert_array_equal(got, gs.run_plan(BufferPlan(g), {"X": x})["Y"])
+
+
+def test_conv_pair_rejections():
+    """No pair when the middle tensor has another reader, when the second
+    convolution is not a plain 1x1 (stride 1, no padding), or when the first
+    one is itself 1x1."""
+    N = ox.make_node
+
+    def model(nodes, out_shape, w2_shape=(8, 4, 1, 1)):
+        inits = [ox.from_array(np.full((4, 3, 3, 3), 0.1, np.float32), "W1"),
+                 ox.from_array(np.full((4, 3, 1, 1), 0.1, np.float32), "W0"),
+                 ox.from_array(np.full(w2_shape, 0.1, np.float32), "W2")]
+        gr = ox.make_graph(nodes, "pairs", [ox.value_info("X", [1, 3, 8, 8])],
+                           [ox.value_info("Y", out_shape)], inits)
+        return graph(ox.make_model(gr))
+
+    def pairs_of(g):
+        plan = BufferPlan(g, fuse.live_from(BufferPlan(g)))
+        return [x for x in fuse.launch_list(plan, pair_ok=lambda pc: True) if isinstance(x, fuse.PairCall)]
+
+    conv3 = N("Conv", ["X", "W1"], ["h"], kernel_shape=[3, 3], pads=[1, 1, 1, 1])
+    # accepted: 3x3 -> 1x1
+    assert len(pairs_of(model([conv3, N("Conv", ["h", "W2"], ["Y"], kernel_shape=[1, 1])],
+                              [1, 8, 8, 8]))) == 1
+    # the middle tensor has a second reader (a residual Add of it)
+    g = model([conv3, N("Conv", ["h", "W2"], ["c"], kernel_shape=[1, 1]),
+               N("Conv", ["h", "W2"], ["d"], kernel_shape=[1, 1]), N("Add", ["c", "d"], ["Y"])],
+              [1, 8, 8, 8])
+    assert not pairs_of(g)
+    # the 1x1 convolution has stride 2
+    g = model([conv3, N("Conv", ["h", "W2"], ["Y"], kernel_shape=[1, 1], strides=[2, 2])], [1, 8, 4, 4])
+    assert not pairs_of(g)
+    # the first convolution is 1x1
+    g = model([N("Conv", ["X", "W0"], ["h"], kernel_shape=[1, 1]),
+               N("Conv", ["h", "W2"], ["Y"], kernel_shape=[1, 1])], [1, 8, 8, 8])
+    assert not pairs_of(g)
+
+
 def test_alias_reader_extends_source_lifetime():
     """A tensor read through a reshape alias after the reshape node stays live
     until that read: a tensor produced in between must not take its slot."""
