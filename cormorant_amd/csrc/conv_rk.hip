@@ -6,7 +6,8 @@
 // then the optional fused Add / Relu / Relu6 epilogue.
 //
 // The layers of a network's small feature maps (up to a few hundred thousand
-// outputs; here strided windows, see cm_conv_rk_takes) are too small for the
+// outputs; here strided windows and wide 1x1 layers, see cm_conv_rk_takes) are
+// too small for the
 // block-tiled kernels to fill the chip, so
 // those kernels' blocks walk the whole reduction serially: 9 to 23 steps of
 // 64 k for a 3x3 window over 64 to 160 channels, each step a chain of loads,
@@ -277,13 +278,22 @@ bool cm_conv_rk_takes(uint32_t batch, uint32_t in_ch, uint32_t in_h, uint32_t in
                       uint32_t dh, uint32_t dw, uint32_t pad_top, uint32_t pad_left) {
     const uint64_t kk = (uint64_t)kh * kw, K = (uint64_t)in_ch * kk;
     const uint64_t np = (uint64_t)batch * out_h * out_w;
-    if (kk < 2 || kk > kRkMaxTaps || in_ch == 0 || out_ch == 0 || np == 0) return false;
-    // strided windows only: measured on MobileNetV2-like layers (batch 16), 3x3
-    // stride 2 at 28x28 / 14x14 / 7x7 outputs took 8.5 / 9.1 / 12.3 us here against
-    // 10.2 / 10.6 / 14.6 on the patch GEMM, while stride-1 layers tied (64 and 160
+    if (kk > kRkMaxTaps || in_ch == 0 || out_ch == 0 || np == 0) return false;
+    // Strided windows, and 1x1 convolutions (stride 1, no padding) over at least
+    // 128 channels.  Measured on MobileNetV2-like layers (batch 16): 3x3 stride 2
+    // at 28x28 / 14x14 / 7x7 outputs took 8.5 / 9.1 / 12.3 us here against 10.2 /
+    // 10.6 / 14.6 on the patch GEMM, while stride-1 3x3 layers tied (64 and 160
     // channels) or lost (96 channels at 14x14: 17.3 against 14.5 us): a wave holds
-    // one k step of loads in flight, and each step waits ~1.5 us for them
-    if (sh * sw < 2) return false;
+    // one k step of loads in flight, and each step waits ~1.5 us for them.  A 1x1
+    // layer gathers nothing twice, and splitting its k steps over four waves
+    // shortens the chain the one-wave-per-tile 1x1 kernel walks: 160 -> 160 / 320
+    // at 7x7 5.4 / 5.6 us against 7.9 / 8.1, 1280 -> 256 12.7 us against 36 on the
+    // gather GEMM (past that kernel's 512 channels); below 128 channels it tied.
+    if (kk == 1) {
+        if (sh != 1 || sw != 1 || pad_top != 0 || pad_left != 0 || in_ch < 128) return false;
+    } else if (sh * sw < 2) {
+        return false;
+    }
     if ((K + 63) / 64 > kRkMaxSteps || (uint64_t)out_ch * np > kRkMaxOut) return false;
     const uint64_t x_bytes = 2ull * batch * in_ch * in_h * in_w;
     if (x_bytes >= 0x80000000ull || 2ull * out_ch * K >= 0x80000000ull) return false;

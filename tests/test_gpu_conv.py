@@ -463,6 +463,11 @@ RK_SHAPES = [
     (16, 96, 14, 14, 96, 3, 3, 2, 1, 1),
     (16, 160, 14, 14, 160, 3, 3, 2, 1, 1),
     (4, 227, 14, 14, 61, 3, 3, 2, 1, 1),    # K = 2043 (32 steps), K % 8 != 0
+    # 1x1 layers over >= 128 channels (stride 1, no padding)
+    (16, 160, 7, 7, 160, 1, 1, 1, 1, 0),
+    (16, 160, 7, 7, 320, 1, 1, 1, 1, 0),
+    (16, 1280, 7, 7, 256, 1, 1, 1, 1, 0),   # 20 k steps, past the 1x1 kernel's 512 channels
+    (3, 130, 9, 11, 40, 1, 1, 1, 1, 0),     # K % 8 != 0, partial tiles
 ]
 
 
