@@ -8,14 +8,15 @@
 // A network's classifier layers (an MLP's 64 x 784 x 256, a 16 x 1280 x 1000
 // head) have a few dozen 128 x 128 tiles at most, so the block-tiled GEMM walks
 // K serially in a handful of blocks or splits it over blocks and adds a reduce
-// launch.  Here a block of four waves owns one 32 x 32 output tile and splits
-// the reduction over its waves (wave w takes k steps w, w + 4, ...); each wave
+// launch.  Here a block of four waves (eight from eight k steps on) owns one
+// 32 x 32 output tile and splits the reduction over its waves (wave w of NW
+// takes k steps w, w + NW, ...); each wave
 // loads its MFMA fragments straight into registers -- A, 16 consecutive k of
 // one row, with 16-byte loads when rows allow; B, 16 k rows of one column,
 // with 2-byte loads -- one k step ahead, splits the limbs in registers, and
 // turns its accumulators into its partial sum of each output (mod 2^32).  The
-// partials meet in LDS after one barrier and each wave finishes a quarter of
-// the tile.  An element outside the matrices gets bit 31 set in its buffer
+// partials meet in LDS after one barrier and each wave finishes 1/NW of the
+// tile.  An element outside the matrices gets bit 31 set in its buffer
 // offset and reads 0 (a select on a validity flag became a branch per load).
 //
 // Limbs and the exact sum are the GEMM kernel's: v = 256*vh + vl + 128 with
@@ -37,7 +38,6 @@ using limbs::pack2;
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
-constexpr int kThreads = 256;             // four waves: one output tile, k split four ways
 constexpr uint32_t kMrMaxSteps = 64;      // k steps of 64 (at most 16 per wave)
 constexpr uint64_t kMrMaxOut = 1u << 18;  // outputs: larger products fill the chip with the GEMM
 
@@ -94,9 +94,12 @@ __device__ __forceinline__ void mr_load(const MrArgs& g, __amdgpu_buffer_rsrc_t 
         }
 }
 
-template <bool AV>
-__global__ __launch_bounds__(kThreads) void matmul_rk(MrArgs g) {
-    __shared__ uint32_t red[kThreads / 64][16][64];   // each wave's partial sums
+// NW waves per block (4, or 8 for 8 or more k steps): the k steps split NW ways.
+template <bool AV, int NW>
+__global__ __launch_bounds__(64 * NW) void matmul_rk(MrArgs g) {
+    static_assert(NW == 4 || NW == 8, "four or eight waves");
+    constexpr uint32_t U = 16u / NW;   // outputs of the lane's 16 each wave finishes
+    __shared__ uint32_t red[NW][16][64];   // each wave's partial sums
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t rt = blockIdx.x % g.rt, ct = blockIdx.x / g.rt;   // scalar: blockIdx is uniform
     const uint32_t r16 = lane & 15, kg = lane >> 4;
@@ -112,23 +115,20 @@ __global__ __launch_bounds__(kThreads) void matmul_rk(MrArgs g) {
         col[j] = ct * 32u + j * 16u + r16;
         bcol[j] = col[j] < g.m ? col[j] * 2u : kOob;
     }
-    // this wave finishes outputs v = 4 * wave + u of the lane's 16: row tile
-    // i = wave >> 1, rows 4 * kg + e with e = 2 * (wave & 1) + (u >> 1), column
-    // j = u & 1; their fused-Add operands load now, behind the k loop
-    const uint32_t fi = wave >> 1;
-    uint32_t fadd[4] = {0u, 0u, 0u, 0u};
+    // this wave finishes outputs v = U * wave + u of the lane's 16 (v = 8 * i +
+    // 2 * e + j: row tile i, row 4 * kg + e, column j); their fused-Add operands
+    // load now, behind the k loop
+    uint32_t fadd[U] = {};
     if (g.epi.add_mode != 0u) {
         const uint32_t ab = g.epi.add_mode == 1u ? g.c_bytes : g.m * 2u;
         const __amdgpu_buffer_rsrc_t xr = make_rsrc(g.epi.add, ab);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t r = rt * 32u + fi * 16u + kg * 4u + 2u * (wave & 1u) + (uint32_t)h;
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const bool ok = r < g.n && col[j] < g.m;
-                const uint32_t el = g.epi.add_mode == 1u ? r * g.m + col[j] : col[j];
-                fadd[2 * h + j] = __builtin_amdgcn_raw_buffer_load_b16(xr, ok ? el * 2u : kOob, 0, 0);
-            }
+        for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t v = U * wave + u, i = v >> 3, e = (v >> 1) & 3u, j = v & 1u;
+            const uint32_t r = rt * 32u + i * 16u + kg * 4u + e;
+            const bool ok = r < g.n && col[j] < g.m;
+            const uint32_t el = g.epi.add_mode == 1u ? r * g.m + col[j] : col[j];
+            fadd[u] = __builtin_amdgcn_raw_buffer_load_b16(xr, ok ? el * 2u : kOob, 0, 0);
         }
     }
 
@@ -169,18 +169,18 @@ __global__ __launch_bounds__(kThreads) void matmul_rk(MrArgs g) {
                 mid[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], bh[j], mid[i][j], 0, 0, 0);
             }
     };
-    // this wave's steps s = wave, wave + 4, ... (two register stages; past the
+    // this wave's steps s = wave, wave + NW, ... (two register stages; past the
     // last step the loads read 0 through the offsets' bit 31 and are never used)
     const uint32_t kl = kg * 16u;
     uint32_t my = 0;
     MrStep s0, s1;
     mr_load<AV>(g, ar, br, arow, bcol, wave * 64u + kl, s0);
-    for (uint32_t s = wave; s < g.nk; s += 8) {
-        mr_load<AV>(g, ar, br, arow, bcol, (s + 4) * 64u + kl, s1);
+    for (uint32_t s = wave; s < g.nk; s += 2 * NW) {
+        mr_load<AV>(g, ar, br, arow, bcol, (s + NW) * 64u + kl, s1);
         compute(s0);
         ++my;
-        if (s + 4 >= g.nk) break;
-        mr_load<AV>(g, ar, br, arow, bcol, (s + 8) * 64u + kl, s0);
+        if (s + NW >= g.nk) break;
+        mr_load<AV>(g, ar, br, arow, bcol, (s + 2 * NW) * 64u + kl, s0);
         compute(s1);
         ++my;
     }
@@ -213,18 +213,16 @@ __global__ __launch_bounds__(kThreads) void matmul_rk(MrArgs g) {
     __syncthreads();
     const int32_t lo = q88::act_lo(g.epi.act), hi = q88::act_hi(g.epi.act);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const uint32_t e = 2u * (wave & 1u) + (uint32_t)h;
-        const uint32_t r = rt * 32u + fi * 16u + kg * 4u + e;
+    for (uint32_t u = 0; u < U; ++u) {
+        const uint32_t v = U * wave + u, i = v >> 3, e = (v >> 1) & 3u, j = v & 1u;
+        const uint32_t r = rt * 32u + i * 16u + kg * 4u + e;
+        uint32_t acc = 0;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t v = fi * 8u + e * 2u + (uint32_t)j;
-            const uint32_t acc = red[0][v][lane] + red[1][v][lane] + red[2][v][lane] + red[3][v][lane];
-            if (r >= g.n || col[j] >= g.m) continue;
-            int32_t o = q88::acc_to_data(acc);
-            if (g.epi.add_mode != 0u) o = q88::add(o, (int16_t)fadd[2 * h + j]);
-            g.c[r * g.m + col[j]] = (int16_t)q88::clamp(o, lo, hi);
-        }
+        for (int w = 0; w < NW; ++w) acc += red[w][v][lane];
+        if (r >= g.n || col[j] >= g.m) continue;
+        int32_t o = q88::acc_to_data(acc);
+        if (g.epi.add_mode != 0u) o = q88::add(o, (int16_t)fadd[u]);
+        g.c[r * g.m + col[j]] = (int16_t)q88::clamp(o, lo, hi);
     }
 }
 
@@ -246,7 +244,14 @@ int cm_matmul_rk_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t
     g.b_bytes = (uint32_t)(2ull * k * m);
     g.c_bytes = (uint32_t)(2ull * out);
     const dim3 grid((uint32_t)((uint64_t)g.rt * ((m + 31) / 32)));
-    if (k % 8 == 0 && ((uintptr_t)a & 15u) == 0) hipLaunchKernelGGL((matmul_rk<true>), grid, dim3(kThreads), 0, lc.s, g);
-    else hipLaunchKernelGGL((matmul_rk<false>), grid, dim3(kThreads), 0, lc.s, g);
+    // eight waves when there are eight or more k steps: each walks half as many
+    const bool av = k % 8 == 0 && ((uintptr_t)a & 15u) == 0;
+    if (g.nk >= 8) {
+        if (av) hipLaunchKernelGGL((matmul_rk<true, 8>), grid, dim3(512), 0, lc.s, g);
+        else hipLaunchKernelGGL((matmul_rk<false, 8>), grid, dim3(512), 0, lc.s, g);
+    } else {
+        if (av) hipLaunchKernelGGL((matmul_rk<true, 4>), grid, dim3(256), 0, lc.s, g);
+        else hipLaunchKernelGGL((matmul_rk<false, 4>), grid, dim3(256), 0, lc.s, g);
+    }
     return cm_check_launch("matmul_rk");
 }
