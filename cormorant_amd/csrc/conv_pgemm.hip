@@ -304,20 +304,26 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
     };
     // Row terms and int8 flags of the block's 128 output channels: loaded here,
     // used after the patch is staged (128 * row sum + bias << 8)
+    // (no bias: a buffer of range 0, whose loads read 0 -- `bias ? bias[r] : 0`
+    // became a branch with a wait for every load issued before it, a memory
+    // round trip ahead of the patch loads)
     const uint32_t rm = min(row0 + (tid & (TB - 1)), g.M - 1u);
     const uint32_t ld_wsum = g.wsum[rm], ld_fit = g.wfit[rm];
-    const int32_t ld_bias = g.bias ? (int32_t)g.bias[rm] : 0;
+    const __amdgpu_buffer_rsrc_t brs = make_rsrc(g.bias ? g.bias : g.x, g.bias ? g.M * 2u : 0u);
+    // (raw 16-bit values, sign-extended where the row terms are written: a
+    // conversion here made the prologue wait for the load)
+    const uint32_t ld_bias = __builtin_amdgcn_raw_buffer_load_b16(brs, rm * 2u, 0, 0);
     // PAIR: the 1x1's row terms and int8 flags (thread t: its row t), written
     // to LDS with the first conv's after the patch is staged; the middle tile's
     // bytes start as the limbs of 0 (k positions past the middle channels keep
     // them: the limb identity's zero operand)
-    uint32_t ld_wsum2 = 0, ld_fit2 = 1u;
-    int32_t ld_bias2 = 0;
+    uint32_t ld_wsum2 = 0, ld_fit2 = 1u, ld_bias2 = 0;
     if constexpr (PAIR) {
         const uint32_t r2 = min(tid, g.M2 - 1u);
         ld_wsum2 = g.wsum2[r2];
         ld_fit2 = g.wfit2[r2];
-        ld_bias2 = g.bias2 ? (int32_t)g.bias2[r2] : 0;
+        const __amdgpu_buffer_rsrc_t b2rs = make_rsrc(g.bias2 ? g.bias2 : g.x, g.bias2 ? g.M2 * 2u : 0u);
+        ld_bias2 = __builtin_amdgcn_raw_buffer_load_b16(b2rs, r2 * 2u, 0, 0);
         const uint32_t nv = (SPX * g.HP + 64u) / 16u;   // a plane and its 64 padding bytes
         for (uint32_t v = tid; v < nv; v += kPgThreads) {
             *reinterpret_cast<v4u*>(lds + g.hp_off + v * 16u) = v4u{0u, 0u, 0u, 0u};
@@ -607,15 +613,21 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
             stage_patch(0u, MULTI ? 4u : g.cpt_all);
             build_qtab(MULTI ? 4u : g.cpt_last, MULTI ? g.div_cpt4 : g.div_cpt_last, MULTI ? 0u : g.nfull);
             if (sub == 0) {
+                // the prologue's loads are used from here on: the empty asm keeps
+                // the compiler from computing with them (and so waiting for them)
+                // ahead of the patch loads
+                uint32_t wsum = ld_wsum, bias = ld_bias, fit = ld_fit;
+                uint32_t wsum2 = ld_wsum2, bias2 = ld_bias2, fit2 = ld_fit2;
+                asm volatile("" : "+v"(wsum), "+v"(bias), "+v"(fit), "+v"(wsum2), "+v"(bias2), "+v"(fit2));
                 const bool real = row0 + tid < g.M;
-                if (tid < TB) rowterm_s[tid] = real ? 128u * ld_wsum + (uint32_t)ld_bias * 256u : 0u;
+                if (tid < TB) rowterm_s[tid] = real ? 128u * wsum + (uint32_t)(int32_t)(int16_t)bias * 256u : 0u;
                 if constexpr (PAIR) {
                     if (tid < ((g.M2 + 31u) & ~31u))
                         reinterpret_cast<uint32_t*>(lds + g.rt2_off)[tid] =
-                            tid < g.M2 ? 128u * ld_wsum2 + (uint32_t)ld_bias2 * 256u : 0u;
-                    fast2 = __syncthreads_and(tid >= g.M2 || ld_fit2 != 0u) != 0;
+                            tid < g.M2 ? 128u * wsum2 + (uint32_t)(int32_t)(int16_t)bias2 * 256u : 0u;
+                    fast2 = __syncthreads_and(tid >= g.M2 || fit2 != 0u) != 0;
                 }
-                fast = __syncthreads_and(tid >= TB || !real || ld_fit != 0u) != 0;
+                fast = __syncthreads_and(tid >= TB || !real || fit != 0u) != 0;
                 if (!fast) {
                     a_load(0, fa_h[0], fa_l[0]);
                     if constexpr (NS == 3) a_load(ks_plus(0, 1), fa_h[1], fa_l[1]);
