@@ -358,9 +358,12 @@ __global__ __launch_bounds__(kThreads) void conv_depthwise(const int16_t* __rest
 // 0), and accumulates w*x for all MT channels with v_dot2 (int16 x int16 pairs
 // into the int32 accumulator, wrapping mod 2^32 like the reference's).
 // Weights of the block's MT channels sit in LDS as [k pair][MT] words (read as
-// a broadcast), next to a per-k table of input byte offsets and tap numbers.
+// a broadcast).  With K <= 32 every gather of a thread and the block's weight
+// loads are issued together at the start: the offsets of the k values depend on
+// the shape alone (a table in the kernel arguments), so one memory round trip
+// covers them all.
 constexpr int kDirThreads = 256;
-constexpr uint32_t kDirChunk = 8;   // k values gathered per load batch
+constexpr uint32_t kDirChunk = 16;   // K is rounded up to a multiple of this (KC = 16 or 32)
 
 struct DirArgs {
     const int16_t* x;
@@ -368,13 +371,15 @@ struct DirArgs {
     const int16_t* bias;
     int16_t* y;
     uint32_t M, H, W, P, OW, kh, kw, sh, sw, dh, dw, pt, pl;
-    uint32_t K, Kc;          // C*kh*kw; K rounded up to 2*kDirChunk
+    uint32_t K, Kc;          // C*kh*kw; K rounded up to kDirChunk
     uint32_t npix;           // batch * P
     uint32_t x_bytes;        // whole input tensor, < 2^31
     uint32_t x_img;          // C*H*W
     uint64_t y_img;          // M*P
     FastDiv div_p, div_ow, div_kk, div_kw;
     EpiArgs epi;
+    int32_t toff[32];        // per k = (c, tap): byte offset from the window origin
+    uint8_t tap[32];         // per k: its tap, 31 past K (always padding)
 };
 
 typedef short v2s __attribute__((ext_vector_type(2)));
@@ -385,21 +390,18 @@ __device__ __forceinline__ uint32_t dot2(uint32_t x, uint32_t w, uint32_t acc) {
                                             (int)acc, false);
 }
 
-template <int MT, bool HAS_BIAS>
+template <int MT, int KC, bool HAS_BIAS>
 __global__ __launch_bounds__(kDirThreads) void conv_direct(DirArgs g) {
     extern __shared__ __align__(16) uint32_t dsm[];
-    uint32_t* wt = dsm;                                          // [Kc / 2][MT]
-    int2* tab = reinterpret_cast<int2*>(dsm + (g.Kc / 2) * MT);   // [Kc + kDirChunk]
+    uint32_t* wt = dsm;                                                  // [KC / 2][MT]
     // bias << 8 of the block's channels, staged with the weights so that the
     // epilogue does not start with a memory round trip
-    uint32_t* bsm = reinterpret_cast<uint32_t*>(tab + g.Kc + kDirChunk);   // [MT]
+    uint32_t* bsm = dsm + (KC / 2) * MT;                                 // [MT]
     const uint32_t m0 = blockIdx.y * MT;
-    // Weight words (k pair, channel): at most 16 x MT (K <= 32), two per thread.
-    // Their loads and the bias load are buffer loads issued before anything is
-    // stored, so one memory round trip covers them and overlaps the k table
-    // below; taps past K and channels past M read 0 (offsets with bit 31 set).
-    constexpr int WPT = (16 * MT + kDirThreads - 1) / kDirThreads;
-    const uint32_t nwords = (g.Kc / 2) * MT;
+    // Weight words (k pair, channel): KC / 2 x MT, WPT per thread.  Buffer loads
+    // with taps past K and channels past M sent out of range (bit 31), read 0.
+    constexpr int WPT = ((KC / 2) * MT + kDirThreads - 1) / kDirThreads;
+    constexpr uint32_t nwords = (KC / 2) * MT;
     uint32_t wlo[WPT], whi[WPT];
     {
         const __amdgpu_buffer_rsrc_t wr = make_rsrc(g.w, g.M * g.K * 2u);
@@ -421,22 +423,8 @@ __global__ __launch_bounds__(kDirThreads) void conv_direct(DirArgs g) {
         const uint32_t m = min(m0 + threadIdx.x, g.M - 1u);
         bias_v = q88::data_to_acc((int32_t)(int16_t)__builtin_amdgcn_raw_buffer_load_b16(br, m * 2u, 0, 0));
     }
-    const uint32_t kk = g.kh * g.kw, hw = g.H * g.W;
-    // k >= K (padding up to Kc, and one chunk past it that the last prefetch
-    // reads) is tap 31, which every thread treats as outside the image
-    for (uint32_t k = threadIdx.x; k < g.Kc + kDirChunk; k += kDirThreads) {
-        const uint32_t c = fdiv(k, g.div_kk), r = k - c * kk;
-        const uint32_t khi = fdiv(r, g.div_kw), kwi = r - khi * g.kw;
-        tab[k] = k < g.K ? int2{(int)(2u * (c * hw + khi * g.dh * g.W + kwi * g.dw)), (int)r}
-                         : int2{0, 31};
-    }
-#pragma unroll
-    for (int u = 0; u < WPT; ++u) {
-        const uint32_t i = u * kDirThreads + threadIdx.x;
-        if (i < nwords) wt[i] = wlo[u] | whi[u] << 16;
-    }
-    if (threadIdx.x < (uint32_t)MT) bsm[threadIdx.x] = bias_v;
 
+    const uint32_t kk = g.kh * g.kw;
     const uint32_t pix = blockIdx.x * kDirThreads + threadIdx.x;
     const bool pok = pix < g.npix;
     const uint32_t n = pok ? fdiv(pix, g.div_p) : 0u;
@@ -456,44 +444,42 @@ __global__ __launch_bounds__(kDirThreads) void conv_direct(DirArgs g) {
     const int32_t pbyte = 2 * ((int32_t)(n * g.x_img) + ih0 * (int32_t)g.W + iw0);
     const __amdgpu_buffer_rsrc_t rsrc =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<int16_t*>(g.x), (short)0, (int)g.x_bytes, 0x00020000);
+    // every k value of the window: k = (c, tap), tap r = (kh, kw); k >= K is
+    // tap 31, which every pixel treats as padding
+    uint32_t xv[KC];
+#pragma unroll
+    for (uint32_t k = 0; k < (uint32_t)KC; ++k) {
+        const uint32_t tap = g.tap[k];
+        const uint32_t off = (((holes >> tap) & 1u) << 31) | ((uint32_t)(pbyte + g.toff[k]) & 0x7FFFFFFFu);
+        xv[k] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < WPT; ++u) {
+        const uint32_t i = u * kDirThreads + threadIdx.x;
+        if (i < nwords) wt[i] = wlo[u] | whi[u] << 16;
+    }
+    if (threadIdx.x < (uint32_t)MT) bsm[threadIdx.x] = bias_v;
     __syncthreads();
 
     uint32_t acc[MT];
 #pragma unroll
     for (int mm = 0; mm < MT; ++mm) acc[mm] = 0u;
-    auto load_chunk = [&](uint32_t k0, uint32_t (&xv)[kDirChunk]) {
 #pragma unroll
-        for (uint32_t q = 0; q < kDirChunk; ++q) {
-            const int2 t = tab[k0 + q];
-            const uint32_t off = (((holes >> t.y) & 1u) << 31) | (uint32_t)(pbyte + t.x);
-            xv[q] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rsrc, off, 0, 0);
+    for (uint32_t q = 0; q < (uint32_t)KC / 2; ++q) {
+        const uint32_t xp = xv[2 * q] | xv[2 * q + 1] << 16;
+        const uint32_t* wr = wt + q * MT;
+#pragma unroll
+        for (int mm = 0; mm < MT; mm += 4) {
+            const v4u wv = *reinterpret_cast<const v4u*>(wr + mm);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[mm + e] = dot2(xp, wv[e], acc[mm + e]);
         }
-    };
-    auto compute_chunk = [&](uint32_t k0, const uint32_t (&xv)[kDirChunk]) {
-#pragma unroll
-        for (uint32_t q = 0; q < kDirChunk / 2; ++q) {
-            const uint32_t xp = xv[2 * q] | xv[2 * q + 1] << 16;
-            const uint32_t* wr = wt + (k0 / 2 + q) * MT;
-#pragma unroll
-            for (int mm = 0; mm < MT; mm += 4) {
-                const v4u wv = *reinterpret_cast<const v4u*>(wr + mm);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) acc[mm + e] = dot2(xp, wv[e], acc[mm + e]);
-            }
-        }
-    };
-    // two gather batches in flight: the next one loads while this one computes
-    // (loads are unconditional; the batch past the end reads only padding)
-    uint32_t xa[kDirChunk], xb[kDirChunk];
-    load_chunk(0, xa);
-    for (uint32_t k0 = 0; k0 < g.Kc; k0 += 2 * kDirChunk) {
-        load_chunk(k0 + kDirChunk, xb);
-        __builtin_amdgcn_sched_barrier(0);   // keep the loads ahead of the compute
-        compute_chunk(k0, xa);
-        load_chunk(k0 + 2 * kDirChunk, xa);
-        __builtin_amdgcn_sched_barrier(0);
-        compute_chunk(k0 + kDirChunk, xb);
     }
+    // the products are done here: without the empty asm the compiler sinks them
+    // into the per-channel stores behind the pixel test below, keeping every
+    // weight read live until then (KC * MT * 2 registers)
+#pragma unroll
+    for (int mm = 0; mm < MT; ++mm) asm volatile("" : "+v"(acc[mm]));
 
     if (!pok) return;
     const int32_t lo = q88::act_lo(g.epi.act), hi = q88::act_hi(g.epi.act);
@@ -530,13 +516,18 @@ uint32_t direct_channels(uint64_t K, uint32_t out_ch, uint32_t kk, uint64_t npix
     return out_ch <= 8 ? 8 : out_ch <= 16 ? 16 : out_ch <= 24 ? 24 : 32;
 }
 
+template <int MT, int KC>
+int launch_direct_kc(const DirArgs& g, hipStream_t s) {
+    const dim3 grid((g.npix + kDirThreads - 1) / kDirThreads, (g.M + MT - 1) / MT);
+    const size_t lds = (size_t)(KC / 2) * MT * 4u + MT * 4u;
+    if (g.bias) hipLaunchKernelGGL((conv_direct<MT, KC, true>), grid, dim3(kDirThreads), lds, s, g);
+    else hipLaunchKernelGGL((conv_direct<MT, KC, false>), grid, dim3(kDirThreads), lds, s, g);
+    return cm_check_launch("conv_direct");
+}
+
 template <int MT>
 int launch_direct(const DirArgs& g, hipStream_t s) {
-    const dim3 grid((g.npix + kDirThreads - 1) / kDirThreads, (g.M + MT - 1) / MT);
-    const size_t lds = (size_t)(g.Kc / 2) * MT * 4u + (size_t)(g.Kc + kDirChunk) * 8u + MT * 4u;
-    if (g.bias) hipLaunchKernelGGL((conv_direct<MT, true>), grid, dim3(kDirThreads), lds, s, g);
-    else hipLaunchKernelGGL((conv_direct<MT, false>), grid, dim3(kDirThreads), lds, s, g);
-    return cm_check_launch("conv_direct");
+    return g.Kc <= 16u ? launch_direct_kc<MT, 16>(g, s) : launch_direct_kc<MT, 32>(g, s);
 }
 
 }  // namespace
@@ -619,7 +610,7 @@ int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int1
         g.M = out_ch; g.H = in_h; g.W = in_w; g.P = out_h * out_w; g.OW = out_w;
         g.kh = kh; g.kw = kw; g.sh = sh; g.sw = sw; g.dh = dh; g.dw = dw; g.pt = pad_top; g.pl = pad_left;
         g.K = (uint32_t)K;
-        g.Kc = (uint32_t)((K + 2 * kDirChunk - 1) / (2 * kDirChunk) * (2 * kDirChunk));
+        g.Kc = (uint32_t)((K + kDirChunk - 1) / kDirChunk * kDirChunk);
         g.npix = (uint32_t)npix;
         g.x_bytes = (uint32_t)x_bytes;
         g.x_img = in_ch * in_h * in_w;
@@ -629,6 +620,11 @@ int cm_conv_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int1
         g.div_kk = make_fastdiv(kh * kw);
         g.div_kw = make_fastdiv(kw);
         g.epi = ea;
+        for (uint32_t k = 0; k < 32; ++k) {
+            const uint32_t c = k / (kh * kw), r = k % (kh * kw), khi = r / kw, kwi = r % kw;
+            g.toff[k] = k < K ? (int32_t)(2u * (c * in_h * in_w + khi * dh * in_w + kwi * dw)) : 0;
+            g.tap[k] = (uint8_t)(k < K ? r : 31u);
+        }
         switch (mt) {
             case 8: return launch_direct<8>(g, s);
             case 16: return launch_direct<16>(g, s);
