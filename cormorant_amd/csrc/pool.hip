@@ -72,6 +72,25 @@ __device__ __forceinline__ int32_t valid_taps(int32_t base, int32_t k, int32_t d
     return n;
 }
 
+// One dword of every 64-byte line a kernel argument spans (offsets 0, 64, ...
+// and its last dword), for a kernel to request all of its argument lines at
+// once: read where first used, behind the branches that use them, each cold
+// line costs a memory round trip of its own.
+template <typename T>
+__device__ __forceinline__ uint32_t arg_lines(const T& a) {
+    constexpr uint32_t nd = sizeof(T) / 4;
+    const uint32_t* d = reinterpret_cast<const uint32_t*>(&a);
+    uint32_t t = d[nd - 1];
+#pragma unroll
+    for (uint32_t i = 0; i * 16 < nd; ++i) t ^= d[i * 16];
+    return t;
+}
+
+// The wave's index in the block as a value the compiler knows is uniform: a
+// buffer descriptor built from threadIdx.x >> 6 otherwise sits in vector
+// registers, and every buffer load through it becomes a read-first-lane loop.
+__device__ __forceinline__ uint32_t wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 // ---------------------------------------------------------------- global --
 constexpr int kBatch = 8;   // 16-byte loads in flight per lane
 
@@ -80,7 +99,7 @@ __global__ __launch_bounds__(kThreads) void pool_global(const int16_t* __restric
                                                         int16_t* __restrict__ y, uint64_t planes,
                                                         uint32_t hw, float inv, uint32_t vec_ok) {
     const uint32_t lane = threadIdx.x & 63;
-    const uint64_t plane = (uint64_t)blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+    const uint64_t plane = (uint64_t)blockIdx.x * (kThreads / 64) + wave_id();
     if (plane >= planes) return;
     const int16_t* xp = x + plane * hw;
     Acc<KIND> a;
@@ -743,7 +762,8 @@ __global__ __launch_bounds__(kThreads) void pool_plane(const int16_t* __restrict
                                                        PlaneGeom p, uint64_t planes, uint32_t vec,
                                                        float inv_full) {
     __shared__ __align__(16) int16_t tile[kThreads / 64][kPlaneMax];
-    const uint32_t lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    asm volatile("" ::"s"(arg_lines(g) ^ arg_lines(p) ^ (uint32_t)planes));
+    const uint32_t lane = threadIdx.x & 63, w = wave_id();
     const uint64_t plane = (uint64_t)blockIdx.x * (kThreads / 64) + w;
     if (plane >= planes) return;   // the whole wave leaves; nothing waits for it
     const uint32_t hw = g.in_h * g.in_w;
