@@ -77,6 +77,34 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const int16_t* base,
                                              kBufferWord3);
 }
 
+// Reads one dword of every 64-byte line that a struct kernel argument spans
+// (offsets 0, 64, ... and its last dword) into one empty asm at a kernel's
+// entry, so that all of the kernel's argument lines are requested at once.
+// Read where first used, behind the branches that use them, each cold line
+// costs a memory round trip of its own (one asm per line, or a chain of XORs,
+// made the compiler wait between batches).  Struct parameters only: they are
+// read in place in the argument segment (arithmetic across two parameters, or
+// a scalar parameter's address, makes the compiler copy them to scratch).
+template <typename A>
+__device__ __forceinline__ void touch_lines(const A& a) {
+    constexpr uint32_t n = sizeof(A) / 4;
+    static_assert(sizeof(A) <= 7 * 64 + 4, "at most 8 argument lines");
+    const uint32_t* d = reinterpret_cast<const uint32_t*>(&a);
+    auto at = [&](uint32_t i) { return d[i * 16u < n ? i * 16u : n - 1u]; };
+    asm volatile("" ::"s"(at(0)), "s"(at(1)), "s"(at(2)), "s"(at(3)), "s"(at(4)), "s"(at(5)),
+                 "s"(at(6)), "s"(d[n - 1u]));
+}
+template <typename A, typename B>
+__device__ __forceinline__ void touch_lines(const A& a, const B& b) {
+    constexpr uint32_t na = sizeof(A) / 4, nb = sizeof(B) / 4;
+    static_assert(sizeof(A) <= 196 && sizeof(B) <= 196, "at most 4 lines per argument");
+    const uint32_t* da = reinterpret_cast<const uint32_t*>(&a);
+    const uint32_t* db = reinterpret_cast<const uint32_t*>(&b);
+    auto at = [](const uint32_t* d, uint32_t n, uint32_t i) { return d[i * 16u < n ? i * 16u : n - 1u]; };
+    asm volatile("" ::"s"(at(da, na, 0)), "s"(at(da, na, 1)), "s"(at(da, na, 2)), "s"(da[na - 1u]),
+                 "s"(at(db, nb, 0)), "s"(at(db, nb, 1)), "s"(at(db, nb, 2)), "s"(db[nb - 1u]));
+}
+
 inline uint64_t cm_grid_blocks(uint64_t work, uint32_t threads, uint64_t cap = 1u << 20) {
     uint64_t b = (work + threads - 1) / threads;
     if (b == 0) b = 1;

@@ -320,6 +320,7 @@ __global__ __launch_bounds__(kThreads) void conv_depthwise(const int16_t* __rest
                                                            const int16_t* __restrict__ bias,
                                                            int16_t* __restrict__ y, DwGeom g,
                                                            uint64_t total, EpiArgs epi) {
+    touch_lines(g, epi);
     const uint64_t stride = (uint64_t)gridDim.x * kThreads;
     const uint64_t ohw = (uint64_t)g.out_h * g.out_w;
     for (uint64_t o = (uint64_t)blockIdx.x * kThreads + threadIdx.x; o < total; o += stride) {
@@ -392,6 +393,7 @@ __device__ __forceinline__ uint32_t dot2(uint32_t x, uint32_t w, uint32_t acc) {
 
 template <int MT, int KC, bool HAS_BIAS>
 __global__ __launch_bounds__(kDirThreads) void conv_direct(DirArgs g) {
+    touch_lines(g);
     extern __shared__ __align__(16) uint32_t dsm[];
     uint32_t* wt = dsm;                                                  // [KC / 2][MT]
     // bias << 8 of the block's channels, staged with the weights so that the

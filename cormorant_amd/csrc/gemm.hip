@@ -511,6 +511,7 @@ enum { B_DENSE = 0, B_CONV_TAB = 1, B_CONV_INC = 2 };
 // copy (and no wait for outstanding loads) is needed where paths would merge.
 template <int MODE, bool HAS_BIAS, bool FOLD, bool BUF, int AV, int BV>
 __global__ __launch_bounds__(kThreads) void q88_gemm(GemmArgs g) {
+    touch_lines(g);
     constexpr bool CONV = MODE != B_DENSE;
     __shared__ __align__(16) Smem s;
     const uint32_t lane = threadIdx.x & 63;
@@ -885,6 +886,7 @@ struct ReduceArgs {
 // flight at once (a run-time trip count would wait for each in turn).
 template <uint32_t SPLITS>
 __global__ __launch_bounds__(kReduceThreads) void split_reduce(ReduceArgs a) {
+    touch_lines(a);
     const uint32_t nq = a.ws_ld / 4u;
     const uint32_t total = a.rows * nq;     // < 2^20: splits need fewer than 160 output tiles
     const uint64_t zs = (uint64_t)a.rows * a.ws_ld;

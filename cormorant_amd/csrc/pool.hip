@@ -72,20 +72,6 @@ __device__ __forceinline__ int32_t valid_taps(int32_t base, int32_t k, int32_t d
     return n;
 }
 
-// One dword of every 64-byte line a kernel argument spans (offsets 0, 64, ...
-// and its last dword), for a kernel to request all of its argument lines at
-// once: read where first used, behind the branches that use them, each cold
-// line costs a memory round trip of its own.
-template <typename T>
-__device__ __forceinline__ uint32_t arg_lines(const T& a) {
-    constexpr uint32_t nd = sizeof(T) / 4;
-    const uint32_t* d = reinterpret_cast<const uint32_t*>(&a);
-    uint32_t t = d[nd - 1];
-#pragma unroll
-    for (uint32_t i = 0; i * 16 < nd; ++i) t ^= d[i * 16];
-    return t;
-}
-
 // The wave's index in the block as a value the compiler knows is uniform: a
 // buffer descriptor built from threadIdx.x >> 6 otherwise sits in vector
 // registers, and every buffer load through it becomes a read-first-lane loop.
@@ -254,6 +240,7 @@ template <int KIND, int KH, int KW, int SH, int PAIR>
 __global__ __launch_bounds__(kThreads) void pool_band(const int16_t* __restrict__ x,
                                                       int16_t* __restrict__ y, PoolGeom g,
                                                       BandGeom b, float inv_full) {
+    touch_lines(g, b);
     extern __shared__ __align__(16) int16_t lds[];
     __shared__ float inv_tab[kInvTab];
     constexpr int16_t kPadV = KIND == K_MAX ? (int16_t)-32768 : (int16_t)0;
@@ -497,6 +484,7 @@ template <int KIND, int KW, int SH, int PAIR>
 __global__ __launch_bounds__(kThreads) void pool_strip(const int16_t* __restrict__ x,
                                                        int16_t* __restrict__ y, PoolGeom g,
                                                        BandGeom b, float inv_full) {
+    touch_lines(g, b);
     extern __shared__ __align__(16) int16_t lds[];
     __shared__ float inv_tab[kInvTab];
     constexpr int KH = KW;
@@ -762,7 +750,7 @@ __global__ __launch_bounds__(kThreads) void pool_plane(const int16_t* __restrict
                                                        PlaneGeom p, uint64_t planes, uint32_t vec,
                                                        float inv_full) {
     __shared__ __align__(16) int16_t tile[kThreads / 64][kPlaneMax];
-    asm volatile("" ::"s"(arg_lines(g) ^ arg_lines(p) ^ (uint32_t)planes));
+    touch_lines(g, p);
     const uint32_t lane = threadIdx.x & 63, w = wave_id();
     const uint64_t plane = (uint64_t)blockIdx.x * (kThreads / 64) + w;
     if (plane >= planes) return;   // the whole wave leaves; nothing waits for it
@@ -879,6 +867,7 @@ template <int KIND>
 __global__ __launch_bounds__(kThreads) void pool_direct(const int16_t* __restrict__ x,
                                                         int16_t* __restrict__ y, PoolGeom g,
                                                         uint64_t total, float inv_full) {
+    touch_lines(g);
     const uint64_t stride = (uint64_t)gridDim.x * kThreads;
     const uint64_t ohw = (uint64_t)g.out_h * g.out_w;
     for (uint64_t o = (uint64_t)blockIdx.x * kThreads + threadIdx.x; o < total; o += stride) {
