@@ -1,4 +1,10 @@
-"""Benchmark of the MI355X Q8.8 kernels (one JSON line on stdout).
+"""Benchmark of the MI355X Q8.8 kernels.
+
+Output: one JSON line per result record ({"record": name, ...}) and per
+reference case ({"record": "perf_case", ...}), as the reference's bench
+programs print one line per case, then the headline line LAST: the contract's
+fields, `roofline`, `cpu_baseline`, `host` and a `summary` of every
+configuration, kept under 4,000 bytes.
 
 Headline workload (the headline metric's vector-op configuration): one step is
 the six-op VectorOP sweep -- Add, Sub, Mul, Div, Relu, Clip(0,6) -- over
@@ -8,17 +14,20 @@ per step, far beyond the 256 MB Infinity Cache).  `value` is the aggregate
 GB/s of the step with the reference formula ports * elements * 2 B / time,
 ports = 3 for binary and 2 for unary ops (bench_src/bench_vectorop.c:93-95).
 
-The same run also reports, under "results":
+The same run also reports, as record lines:
 * the GEMM configurations and the conv + pool block: Q8.8 GOP/s = 2*MAC / t
   (bench_matmul.c:95, bench_conv.c:129-132) with the int8-MFMA utilisation of
   the four limb products; conv A and conv B, then MaxPool / AvgPool / LpPool /
   GlobalAveragePool on each convolution's own output, pool GB/s = (x + y) * 2 B
   / t (bench_pool.c:116-117) with rotating inputs larger than the Infinity
-  Cache, next to a VectorOP copy of the same byte count timed the same way
-  (`frac_of_copy_ceiling`);
+  Cache, next to two copies of the same byte count timed the same way -- VectorOP's
+  copy opcode and a device-to-device hipMemcpyAsync -- the faster of which is the
+  streaming ceiling at that size (`frac_of_copy_ceiling`);
 * the two ONNX graphs run by the scheduler's HIP backend: the MLP's batch-64
   latency and the MobileNetV2-like graph's images/s at batch 16, each with its
-  roofline fraction (sum of per-kernel lower bounds / measured time);
+  roofline fraction: the sum over the launches that run of each launch's bound
+  (bytes it moves at 8 TB/s, or its MACs' four limb products at 5 POP/s) over the
+  measured time, beside the per-op form (every ONNX node's call alone);
 * `perf_cases`: the reference's per-kernel case list (perf_config.json.example
   and the published KV260 report's rows) through cm_bench, the C counterpart
   of bench_src/bench_*.c, one record per case with the reference's fields and
@@ -26,9 +35,9 @@ The same run also reports, under "results":
   oracle.
 CPU figures (the oracle, a C restatement of the reference C-simulation loops, on
 this host): one thread (the faithful C-simulation path, `cpu_baseline.value` and
-each result's `cpu.gops` / `cpu.gbs`; GEMM / conv on a stated slice) and OpenMP
-over the independent outer loop (`*_mt`, the whole product, which also checks
-the GPU output bit for bit); `host` records the CPU model and the thread count.
+each result's `cpu.gops` / `cpu.gbs`, the whole product) and OpenMP over the
+independent outer loop (`*_mt`); both check the GPU output bit for bit; `host`
+records lscpu's CPU model and the thread count.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick]
                        [--workloads vecop,gemm,conv,pool,graphs,cases] [--no-cpu]
@@ -53,9 +62,49 @@ INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA, 5.0 POP/s
 LIMB_PRODUCTS = 4              # int8 MFMA products per exact Q8.8 product
 
 
+HEADLINE_MAX = 4000            # bytes of the last stdout line
+
+
 def log(msg: str) -> None:
     sys.stderr.write(f"[bench] {msg}\n")
     sys.stderr.flush()
+
+
+def emit(record: dict) -> None:
+    """One result record as its own stdout line (ahead of the headline line)."""
+    print(json.dumps(record, separators=(",", ":")), flush=True)
+
+
+def summarize(results: dict, cases: list, cpu_res: dict) -> dict:
+    """The headline line's digest of every configuration: one rate and its roofline
+    fraction each (the full figures are in the record lines printed before it)."""
+    s = {}
+    ops = results.get("vecop", {}).get("ops", {})
+    if ops:
+        s["vecop_hbm_frac"] = {k: v["hbm_frac"] for k, v in ops.items()}
+    for name, e in results.items():
+        if name.startswith("gemm_"):
+            s[name] = dict(gops=e["gops"], mfma_frac=e["mfma_frac"])
+        elif name.startswith("conv_"):
+            s[name] = dict(gops=e["gops"], mfma_frac_issued=e["mfma_frac"],
+                           frac_4product=e["frac_of_4product_roofline"])
+            if e.get("packed_weights"):
+                s[name]["packed_gops"] = e["packed_weights"]["gops"]
+        elif "_on_conv" in name:
+            s[name] = dict(gbs=e["gbs"], hbm_frac=e["hbm_frac"], of_copy=e["frac_of_copy_ceiling"])
+        elif name.startswith("pool_copy_ceiling"):
+            s[name] = dict(gbs=e["gbs"], hbm_frac=e["hbm_frac"])
+        elif name in ("mlp_b64", "mobilenet_like_b16"):
+            s[name] = dict(ms=e["ms_hip_graph"], images_s=e["images_s_hip_graph"],
+                           roofline_frac=e["roofline_frac"], per_op_frac=e["per_op_frac"])
+            if "cpu" in e:
+                s[name]["cpu_images_s"] = e["cpu"]["images_s"]
+        if name in cpu_res and "gops" in cpu_res[name]:
+            s[name]["cpu_gops_1t"] = round(cpu_res[name]["gops"], 2)
+    if cases:
+        s["perf_cases"] = dict(n=len(cases), checked_vs_oracle=all(r.get("checked_vs_oracle")
+                                                                   for r in cases))
+    return s
 
 
 def time_launches(calls, steps: int) -> float:
@@ -262,15 +311,26 @@ def bench_block(steps: int, warmup: int):
         ms = time_graph(calls, max(steps, 4 * rot))
         nbytes = (dy.numel() + ny) * 2
         gbs = nbytes / (ms * 1e-3) / 1e9
-        if o not in ceilings:   # VectorOP copy of the largest pool's byte count, same timing
+        if o not in ceilings:
+            # two copies of the largest pool's byte count, timed the same way: VectorOP's
+            # copy opcode and the runtime's device-to-device hipMemcpyAsync (torch's copy_
+            # of a contiguous same-dtype tensor); the faster one is the streaming ceiling
             ncopy = (dy.numel() + n * c * (o // 2) ** 2) // 2
             src = [t[:ncopy] for t in xs]
             dst = [torch.empty(ncopy, dtype=torch.int16, device="cuda") for _ in range(rot)]
             ccalls = [lambda i=i: K.VectorOPKernel(src[i], None, dst[i], ncopy, 6) for i in range(rot)]
             cms = time_graph(ccalls, max(steps, 4 * rot))
-            ceilings[o] = dict(ms=round(cms, 5), gbs=round(4 * ncopy / (cms * 1e-3) / 1e9, 1),
-                               bytes=4 * ncopy, kernel="vecop_flat<6>", rotating_inputs=rot)
-            ceilings[o]["hbm_frac"] = round(ceilings[o]["gbs"] / HBM_PEAK_GBS, 4)
+            mcalls = [lambda i=i: dst[i].copy_(src[i]) for i in range(rot)]
+            mms = time_graph(mcalls, max(steps, 4 * rot))
+            cgbs, mgbs = 4 * ncopy / (cms * 1e-3) / 1e9, 4 * ncopy / (mms * 1e-3) / 1e9
+            ceilings[o] = dict(bytes=4 * ncopy, rotating_inputs=rot,
+                               vecop_copy=dict(ms=round(cms, 5), gbs=round(cgbs, 1),
+                                               hbm_frac=round(cgbs / HBM_PEAK_GBS, 4),
+                                               kernel="vecop_flat<6>"),
+                               hip_memcpy_d2d=dict(ms=round(mms, 5), gbs=round(mgbs, 1),
+                                                   hbm_frac=round(mgbs / HBM_PEAK_GBS, 4)),
+                               gbs=round(max(cgbs, mgbs), 1),
+                               hbm_frac=round(max(cgbs, mgbs) / HBM_PEAK_GBS, 4))
             del dst
         out[name] = dict(input=f"{cv.name} output [{n},{c},{o},{o}]", ms=round(ms, 5),
                          gbs=round(gbs, 1), hbm_frac=round(gbs / HBM_PEAK_GBS, 4), bytes=nbytes,
@@ -284,21 +344,55 @@ def bench_block(steps: int, warmup: int):
 
 
 # ----------------------------------------------------------------- graphs --
+def call_macs(call) -> int:
+    a = call.args
+    if call.kernel in ("matmul", "matmul_at"):
+        return a[0] * a[1] * a[2] * a[3]
+    if call.kernel == "conv":
+        nb, c, _, _, mo, oh, ow, kh, kw = a[:9]
+        return nb * mo * oh * ow * (1 if a[16] else c) * kh * kw
+    return 0
+
+
+def bound_s(nbytes: int, macs: int) -> float:
+    """max(HBM time of the bytes, int8-MFMA time of the four limb products per MAC)."""
+    return max(nbytes / (HBM_PEAK_GBS * 1e9), LIMB_PRODUCTS * 2 * macs / (INT8_PEAK_TOPS * 1e12))
+
+
 def graph_lower_bound_s(plan) -> float:
-    """Sum over kernel calls of max(HBM time of the algorithmic bytes, int8-MFMA time of
-    the four limb products): the graph's roofline time."""
+    """Per-op bound: the sum over the reference's kernel calls (one per ONNX node, every
+    intermediate through memory) of each call's bound."""
+    return sum(bound_s(2 * sum(c.extents().values()), call_macs(c)) for _, c in plan.calls)
+
+
+def launch_members(item):
+    """The kernel calls one launch of the session runs, in order."""
+    from cormorant_amd.scheduler import fuse
+    if isinstance(item, (fuse.FusedCall, fuse.PairCall)):
+        return (item.call,) + tuple(item.absorbed)
+    return (item,)
+
+
+def launch_lower_bound_s(launch_list) -> float:
+    """Fused bound: the sum over the launches that actually run of max(HBM time of the
+    bytes the launch must move, MFMA time of its MACs).  A launch's bytes are the
+    tensors its member calls read that no member writes, plus the tensor it leaves in
+    memory; intermediates kept on chip (fused epilogues, a convolution pair's middle
+    tensor) count for nothing."""
+    from cormorant_amd.scheduler import fuse
     total = 0.0
-    for _, call in plan.calls:
-        nbytes = 2 * sum(call.extents().values())
-        macs = 0
-        a = call.args
-        if call.kernel in ("matmul", "matmul_at"):
-            macs = a[0] * a[1] * a[2] * a[3]
-        elif call.kernel == "conv":
-            nb, c, _, _, mo, oh, ow, kh, kw = a[:9]
-            macs = nb * mo * oh * ow * (1 if a[16] else c) * kh * kw
-        total += max(nbytes / (HBM_PEAK_GBS * 1e9),
-                     LIMB_PRODUCTS * 2 * macs / (INT8_PEAK_TOPS * 1e12))
+    for item in launch_list:
+        members = launch_members(item)
+        written = {fuse._writes(c) for c in members}
+        out = item.out if isinstance(item, (fuse.FusedCall, fuse.PairCall)) else fuse._writes(item)
+        need = {}
+        for c in members:
+            ext = c.extents()
+            for name in fuse._reads(c):
+                if name not in written:
+                    need[name] = max(need.get(name, 0), ext[name])
+        need[out] = members[-1].extents()[out]
+        total += bound_s(2 * sum(need.values()), sum(call_macs(c) for c in members))
     return total
 
 
@@ -323,20 +417,21 @@ def bench_graphs(steps: int, warmup: int, check: bool):
         torch.cuda.synchronize()
         ms = time_launches([launch], steps)
         ms_graph = time_graph([launch], max(steps, 4))
-        macs = sum(c.args[0] * c.args[1] * c.args[2] * c.args[3]
-                   for _, c in sess.plan.calls if c.kernel.startswith("matmul"))
-        macs += sum(c.args[0] * c.args[4] * c.args[5] * c.args[6] *
-                    (1 if c.args[16] else c.args[1]) * c.args[7] * c.args[8]
-                    for _, c in sess.plan.calls if c.kernel == "conv")
+        macs = sum(call_macs(c) for _, c in sess.plan.calls)
         lb = graph_lower_bound_s(sess.plan)
+        lbf = launch_lower_bound_s(sess.launch_list)
         e = dict(kernel_calls=len(sess.plan.calls), launches=len(sess.launch_list),
                  gmac=round(macs / 1e9, 4),
                  ms=round(ms, 4), ms_hip_graph=round(ms_graph, 4),
                  images_s=round(batch / (ms * 1e-3), 1),
                  images_s_hip_graph=round(batch / (ms_graph * 1e-3), 1),
                  gops=round(2 * macs / (ms_graph * 1e-3) / 1e9, 1),
-                 roofline_lower_bound_ms=round(lb * 1e3, 4),
-                 roofline_frac=round(lb * 1e3 / ms_graph, 4),
+                 roofline_lower_bound_ms=round(lbf * 1e3, 4),
+                 roofline_frac=round(lbf * 1e3 / ms_graph, 4),
+                 roofline_bound="sum over the launches that run of max(bytes each moves / 8 TB/s, "
+                                "4 limb products x 2 x MACs / 5 POP/s)",
+                 per_op_lower_bound_ms=round(lb * 1e3, 4),
+                 per_op_frac=round(lb * 1e3 / ms_graph, 4),
                  pool_bytes=2 * sess.plan.pool_elems)
         y = sess.read_output("Y")
         if check:
@@ -369,16 +464,30 @@ def host_threads() -> int:
 
 
 def host_info() -> dict:
-    model = None
+    """CPU identity: `lscpu`'s model name, with the x86 family / model / stepping
+    numbers (a virtual machine may report only a vendor string as the name)."""
+    import subprocess
+    info = {}
     try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
+        r = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10,
+                           env=dict(os.environ, LC_ALL="C"))
+        for line in r.stdout.splitlines():
+            key, _, val = line.partition(":")
+            info[key.strip()] = val.strip()
+    except (OSError, subprocess.SubprocessError):
         pass
-    return dict(cpu_model=model, logical_cpus=os.cpu_count(), omp_threads=host_threads())
+    if "Model name" not in info:
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    if line.startswith("model name"):
+                        info["Model name"] = line.split(":", 1)[1].strip()
+                        break
+        except OSError:
+            pass
+    return dict(cpu_model=info.get("Model name"), cpu_family=info.get("CPU family"),
+                cpu_model_number=info.get("Model"), stepping=info.get("Stepping"),
+                logical_cpus=os.cpu_count(), omp_threads=host_threads())
 
 
 def cpu_baseline(vec_bufs, extras: dict):
@@ -413,9 +522,9 @@ def cpu_baseline(vec_bufs, extras: dict):
         t_mt += time.perf_counter() - t0
     res["vecop"].update(gbs_mt=bytes_total / t_mt / 1e9, seconds_mt=t_mt, threads_mt=mt)
     oracle.set_threads(1)
-    # GEMM / conv: the whole product with OpenMP (it also checks the GPU output
-    # bit for bit), and a slice on one thread (the faithful C-simulation path;
-    # the whole product would take minutes), scaled by its share of the MACs
+    # GEMM / conv: the whole product on one thread (the faithful C-simulation path,
+    # ~45 s over the four products) and with OpenMP; both check the GPU output bit
+    # for bit
     from cormorant_amd import workloads as wl
 
     def timed(fn, threads):
@@ -437,13 +546,13 @@ def cpu_baseline(vec_bufs, extras: dict):
                                             threads=True), mt)
         if not np.array_equal(dc.cpu().numpy(), want):
             raise SystemExit(f"bench: GPU {case.name} differs from the oracle")
-        rows = n if bt > 1 else 64          # batch 0 of 32, or 64 rows of 4096
-        part = np.empty(rows * m, np.int16)
-        dt_1 = timed(lambda: oracle.matmul(a1, b1, part, rows, k, m), 1)
-        if not np.array_equal(part, want[: rows * m]):
-            raise SystemExit(f"bench: {case.name} one-thread slice differs")
-        res[case.name] = dict(gops=2.0 * rows * k * m / dt_1 / 1e9, seconds=dt_1,
-                              sample=f"{'batch 0 of 32' if bt > 1 else '64 of 4096 rows'}, one thread",
+        log(f"CPU baseline: {case.name} on one thread (whole product)")
+        one = np.empty_like(want)
+        dt_1 = timed(lambda: oracle.matmul(a1, b1, one, n, k, m, bt, n * k, k * m, n * m), 1)
+        if not np.array_equal(one, want):
+            raise SystemExit(f"bench: {case.name} one-thread oracle run differs")
+        res[case.name] = dict(gops=2.0 * case.macs / dt_1 / 1e9, seconds=dt_1,
+                              sample="the whole product, one thread, checked bit for bit",
                               gops_mt=2.0 * case.macs / dt_mt / 1e9, seconds_mt=dt_mt,
                               threads_mt=mt, sample_mt="the whole product, checked bit for bit")
     for case in wl.CONV_CASES:
@@ -458,12 +567,13 @@ def cpu_baseline(vec_bufs, extras: dict):
         dt_mt = timed(lambda: oracle.conv(x1, w1, b, want, case.batch, *args, threads=True), mt)
         if not np.array_equal(dy.cpu().numpy(), want):
             raise SystemExit(f"bench: GPU {case.name} differs from the oracle")
-        part = np.empty(case.out_ch * o * o, np.int16)
-        dt_1 = timed(lambda: oracle.conv(x1, w1, b, part, 1, *args), 1)
-        if not np.array_equal(part, want[: part.size]):
-            raise SystemExit(f"bench: {case.name} one-thread slice differs")
-        res[case.name] = dict(gops=2.0 * case.macs / case.batch / dt_1 / 1e9, seconds=dt_1,
-                              sample="image 0 of 32, one thread",
+        log(f"CPU baseline: {case.name} on one thread (all 32 images)")
+        one = np.empty_like(want)
+        dt_1 = timed(lambda: oracle.conv(x1, w1, b, one, case.batch, *args), 1)
+        if not np.array_equal(one, want):
+            raise SystemExit(f"bench: {case.name} one-thread oracle run differs")
+        res[case.name] = dict(gops=2.0 * case.macs / dt_1 / 1e9, seconds=dt_1,
+                              sample="all 32 images, one thread, checked bit for bit",
                               gops_mt=2.0 * case.macs / dt_mt / 1e9, seconds_mt=dt_mt,
                               threads_mt=mt, sample_mt="all 32 images, checked bit for bit")
     for name, e in list(extras.items()):
@@ -587,10 +697,11 @@ def main() -> int:
                     kernel=dom_kernel, op=dom_name,
                     bytes_per_launch=vecop_bytes(dom_op, wl.VECOP_N))
 
-    results = dict(vecop_ops=per_op, vecop_kernel_ms_per_step=round(kernel_ms, 5),
-                   vecop_copy_ceiling=dict(ms=round(copy_ms, 5), gbs=round(copy_gbs, 1),
-                                           hbm_frac=round(copy_gbs / HBM_PEAK_GBS, 4),
-                                           kernel="vecop_flat<6>", bytes_per_launch=vecop_bytes(6, wl.VECOP_N)))
+    results = dict(vecop=dict(ops=per_op, kernel_ms_per_step=round(kernel_ms, 5),
+                              copy_ceiling=dict(ms=round(copy_ms, 5), gbs=round(copy_gbs, 1),
+                                                hbm_frac=round(copy_gbs / HBM_PEAK_GBS, 4),
+                                                kernel="vecop_flat<6>",
+                                                bytes_per_launch=vecop_bytes(6, wl.VECOP_N))))
     cpu = None
     extras, graphs = {}, {}
     if "gemm" in work:
@@ -633,8 +744,6 @@ def main() -> int:
             row["checked_vs_oracle"] = True
         import shutil
         shutil.rmtree(dump_dir, ignore_errors=True)
-    if cases:
-        results["perf_cases"] = cases
     for name, e in extras.items():
         e.pop("_dev", None)
         if name in cpu_res:
@@ -643,6 +752,12 @@ def main() -> int:
         results[name] = e
     results.update(graphs)
 
+    # one JSON line per result and per reference case first (the reference's bench
+    # programs print one line per case), then the compact headline line last
+    for name, e in results.items():
+        emit(dict(record=name, **e))
+    for row in cases:
+        emit(dict(record="perf_case", **row))
     line = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -666,9 +781,13 @@ def main() -> int:
         "roofline": roofline,
         "cpu_baseline": cpu,
         "host": host_info(),
-        "results": results,
+        "summary": summarize(results, cases, cpu_res),
     }
-    print(json.dumps(line))
+    text = json.dumps(line, separators=(",", ":"))
+    if len(text) > HEADLINE_MAX:     # keep the headline readable by line-tail parsers
+        line["summary"] = {"dropped": f"summary over {HEADLINE_MAX} bytes; see the records above"}
+        text = json.dumps(line, separators=(",", ":"))
+    print(text, flush=True)
     return 0
 
 

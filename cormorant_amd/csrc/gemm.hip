@@ -980,14 +980,19 @@ int launch_gemm(GemmArgs& g0, uint32_t zdim, const LaunchCtx& lc, const char* na
             if (want > *lc.need) *lc.need = want;
             return CM_OK;
         }
+        // the partials are stored and summed as 16-byte vectors: a workspace that
+        // is not 16-byte aligned is used from its first aligned byte on
+        const uintptr_t ws_at = reinterpret_cast<uintptr_t>(lc.ws);
+        const uintptr_t ws_al = (ws_at + 15u) & ~static_cast<uintptr_t>(15u);
+        const size_t ws_avail = lc.ws && lc.ws_bytes > ws_al - ws_at ? lc.ws_bytes - (ws_al - ws_at) : 0u;
         if (splits > 1) {
-            const size_t fit = lc.ws ? lc.ws_bytes / per_split : 0u;
+            const size_t fit = ws_avail / per_split;
             if (fit < splits) splits = fit >= 2 ? even((uint32_t)fit) : 1u;
         }
         if (splits > 1) {
             g.split_steps = (nk_all + splits - 1) / splits;
             g.ws_ld = ws_ld;
-            g.ws = static_cast<uint32_t*>(lc.ws);
+            g.ws = reinterpret_cast<uint32_t*>(ws_al);
             g.a_bs = g.b_bs = g.c_bs = 0;
             grid.z = splits;
         }

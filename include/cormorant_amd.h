@@ -28,7 +28,12 @@
  *     for calls that take none (cm_set_workspace).  The size a call would use
  *     is returned by cm_matmul_workspace_size / cm_conv_workspace_size; a
  *     smaller workspace gives fewer splits, none gives none -- the result is
- *     the same bit for bit, only the speed differs.  Calls that may run at
+ *     the same bit for bit, only the speed differs.  The sizes assume a
+ *     16-byte-aligned workspace (a cm_buf_t's device memory and torch's
+ *     allocations are 256-byte aligned); at another address a MatMul uses it
+ *     from its first 16-byte-aligned byte on, and a Conv runs a path that
+ *     needs none -- again the same result, only slower.
+ *     Calls that may run at
  *     the same time (different streams, a replayed HIP graph beside eager
  *     work) must not share a workspace; calls queued on one stream may.
  *

@@ -136,3 +136,19 @@ def test_plane_path_random(seed):
     x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
     got, want = pool_both(x, N, C, H, W, OH, OW, k, kw, sh, sw, pt, pl, 1, 1, ptype, lp, cip)
     np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("ptype,lp", [(3, 0), (3, 1), (7, 3), (7, 1), (2, 0), (2, 3)])
+@pytest.mark.parametrize("geom", EDGE_CASES, ids=[str(g) for g in EDGE_CASES])
+def test_out_of_range_type_and_order_codes(ptype, lp, geom):
+    """pool_type outside {0, 1} selects LpPool and lp_order other than 1 selects p = 2
+    (PoolingKernel.cpp:214-224, 256-263), on every kernel path (strip, band, plane,
+    global, direct), full-range values."""
+    N, C, H, W, ph, pw, sh, sw, pt, pl, dh, dw = geom
+    OH = (H + 2 * pt - dh * (ph - 1) - 1) // sh + 1
+    OW = (W + 2 * pl - dw * (pw - 1) - 1) // sw + 1
+    say(f"pool geometry {geom} out-of-range codes type={ptype} lp={lp}")
+    g = wl.rng(812, ptype, lp, *geom)
+    x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
+    got, want = pool_both(x, N, C, H, W, OH, OW, ph, pw, sh, sw, pt, pl, dh, dw, ptype, lp, 0)
+    np.testing.assert_array_equal(got, want)

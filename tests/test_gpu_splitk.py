@@ -60,6 +60,28 @@ def test_matmul_split(case):
         np.testing.assert_array_equal(host(c), want, err_msg=f"workspace {ws_bytes}")
 
 
+@pytest.mark.parametrize("extra", [16, 0])
+def test_matmul_split_unaligned_workspace(extra):
+    """A workspace that starts 2 bytes past a 16-byte boundary (an int16 view at an
+    odd element offset): the partials (16-byte vector stores) go to its first aligned
+    byte on, with fewer splits when the rest is too small; the result is the oracle's."""
+    import torch
+    n, k, m = 64, 4160, 96
+    say(f"split-K matmul, workspace at +2 bytes, {extra} spare bytes")
+    g = wl.rng(914, extra)
+    a, b = full_range(g, n * k), full_range(g, k * m)
+    want = np.zeros(n * m, np.int16)
+    oracle.set_threads(oracle_threads())
+    oracle.matmul(a, b, want, n, k, m, threads=True)
+    need = K.matmul_workspace_size(n, k, m)
+    base = workspace(need + extra + 16).view(torch.int16)
+    ws = base[1: 1 + (need + extra) // 2]
+    assert ws.data_ptr() % 16 == 2
+    c = empty_dev(n * m)
+    K.MatmulKernel(dev(a), dev(b), c, n, k, m, workspace=ws)
+    np.testing.assert_array_equal(host(c), want)
+
+
 @pytest.mark.parametrize("act", [K.ACT_NONE, K.ACT_RELU6])
 def test_matmul_split_column_add(act):
     say(f"split-K matmul column add act {act}")

@@ -296,6 +296,86 @@ def test_conv_reference_geometries_vs_numpy_sim(i):
     np.testing.assert_array_equal(y, y2)
 
 
+def _closed_form_conv(x, w, bias, oh_n, ow_n, sh, sw, dh, dw, pt, pl, has_bias, dwise):
+    """sat16(wrap32((has_bias ? bias << 8 : 0) + sum of in-bounds x*w) >> 8) with Python
+    integers, straight from the definition (ConvKernel.cpp:160-169, 235-237, 308-310, 333):
+    ih = oh*sh + i*dh - pt, iw = ow*sw + j*dw - pl; bottom/right padding is what the
+    output size leaves past the input."""
+    N, C, H, W = x.shape
+    M, _, KH, KW = w.shape
+    out = np.zeros((N, M, oh_n, ow_n), np.int64)
+    wrapped = 0
+    for n in range(N):
+        for m in range(M):
+            chans = [m] if dwise else range(C)
+            for oh in range(oh_n):
+                for ow in range(ow_n):
+                    s = (int(bias[m]) << 8) if has_bias else 0
+                    for c in chans:
+                        wc = 0 if dwise else c
+                        for i in range(KH):
+                            ih = oh * sh + i * dh - pt
+                            if not 0 <= ih < H:
+                                continue
+                            for j in range(KW):
+                                iw = ow * sw + j * dw - pl
+                                if 0 <= iw < W:
+                                    s += int(x[n, c, ih, iw]) * int(w[m, wc, i, j])
+                    wrapped += not -2**31 <= s < 2**31
+                    s = (s + 2**31) % 2**32 - 2**31
+                    out[n, m, oh, ow] = max(-32768, min(32767, s >> 8))
+    return out, wrapped
+
+
+# N, C, H, W, M, kh, kw, sh, sw, dh, dw, pad top, left, bottom, right, bias, depthwise
+CONV_WRAP_GEOMS = [
+    (2, 5, 7, 6, 3, 3, 2, 2, 1, 1, 2, 2, 1, 0, 2, 1, 0),     # asymmetric pads, mixed stride/dilation
+    (1, 3, 6, 9, 4, 3, 3, 1, 2, 2, 1, 1, 0, 2, 1, 1, 0),
+    (2, 4, 5, 5, 4, 3, 3, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1),     # depthwise, bias
+    (1, 6, 8, 7, 4, 2, 3, 2, 1, 1, 2, 0, 2, 1, 0, 1, 1),     # depthwise, out_ch < in_ch
+    (1, 9, 4, 4, 2, 1, 1, 1, 1, 1, 1, 0, 0, 0, 0, 1, 0),     # 1x1
+    (1, 2, 3, 3, 2, 5, 5, 1, 1, 1, 1, 2, 2, 2, 2, 0, 0),     # window wider than the input
+]
+
+
+@pytest.mark.parametrize("geom", CONV_WRAP_GEOMS, ids=[str(g) for g in CONV_WRAP_GEOMS])
+def test_conv_closed_form_full_range(geom):
+    """ora_conv (one thread and OpenMP) against Python big integers on tiny full-range
+    shapes: standard and depthwise, bias, asymmetric padding, stride and dilation.  A
+    planted block of -32768 inputs and weights makes sums of k * 2^30 that wrap."""
+    N, C, H, W, M, kh, kw, sh, sw, dh, dw, pt, pl, pb, pr, hb, dwise = geom
+    g = wl.rng(912, *geom)
+    x = g.integers(-32768, 32768, size=(N, C, H, W)).astype(np.int16)
+    w = g.integers(-32768, 32768, size=(M, 1 if dwise else C, kh, kw)).astype(np.int16)
+    b = g.integers(-32768, 32768, size=(M,)).astype(np.int16)
+    x[0, :, : min(H, 3), : min(W, 3)] = -32768
+    w[0] = -32768
+    oh = rc.conv_out_size(H, kh, sh, dh, pt, pb)
+    ow = rc.conv_out_size(W, kw, sw, dw, pl, pr)
+    want, wrapped = _closed_form_conv(x, w, b, oh, ow, sh, sw, dh, dw, pt, pl, hb, dwise)
+    assert wrapped > 0      # some accumulators left the int32 range: the wrap is exercised
+    for threads in (False, True):
+        y = np.full((N, M, oh, ow), 55, np.int16)
+        oracle.conv(x, w, b, y, N, C, H, W, M, oh, ow, kh, kw, sh, sw, dh, dw, pt, pl, hb, dwise,
+                    threads=threads)
+        np.testing.assert_array_equal(y, want)
+
+
+def test_conv_bias_wraps_with_sum():
+    """A bias whose <<8 joins a sum near 2^31 wraps with it: 1 input channel, 1x1,
+    x = w = -32768 gives 2^30 per product; two channels give 2^31, which wraps to
+    -2^31, and bias 0x7FFF << 8 moves it back up (ConvKernel.cpp:160-169, 333)."""
+    x = np.full((1, 2, 1, 1), -32768, np.int16)
+    w = np.full((1, 2, 1, 1), -32768, np.int16)
+    for bias, hb in ((0, 0), (32767, 1), (-32768, 1), (-1, 1)):
+        y = np.zeros((1, 1, 1, 1), np.int16)
+        b = np.array([bias], np.int16)
+        oracle.conv(x, w, b, y, 1, 2, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 0, 0, hb, 0)
+        s = 2 * 2**30 + ((bias << 8) if hb else 0)
+        s = (s + 2**31) % 2**32 - 2**31
+        assert int(y[0, 0, 0, 0]) == max(-32768, min(32767, s >> 8)), bias
+
+
 @pytest.mark.parametrize("case", rc.CONV_SAT, ids=[c[0] for c in rc.CONV_SAT])
 def test_conv_saturation_kats(case):
     _, wv, bv, want = case
@@ -389,3 +469,54 @@ def test_pool_wrap_and_edges():
     s = (300 * 32768 * 256) % 2**32
     s = s - 2**32 if s >= 2**31 else s
     assert y[0] == max(-32768, min(32767, s >> 8))
+
+
+def _closed_form_lp(x, OH, OW, ph, pw, sh, sw, pt, pl, dh, dw, p):
+    """LpPool from the definition with Python integers: p = 1 gives
+    sat16(wrap32(sum |x| << 8) >> 8); p = 2 gives isqrt(sum x^2), exact when the sum
+    of squares stays below 2^24 (PoolingKernel.cpp:222-224, 262-265)."""
+    N, C, H, W = x.shape
+    out = np.zeros((N, C, OH, OW), np.int64)
+    for n in range(N):
+        for c in range(C):
+            for oh in range(OH):
+                for ow in range(OW):
+                    s = 0
+                    for i in range(ph):
+                        ih = oh * sh + i * dh - pt
+                        for j in range(pw):
+                            iw = ow * sw + j * dw - pl
+                            if 0 <= ih < H and 0 <= iw < W:
+                                v = int(x[n, c, ih, iw])
+                                s += (abs(v) << 8) if p == 1 else v * v
+                    if p == 1:
+                        s = (s + 2**31) % 2**32 - 2**31
+                        out[n, c, oh, ow] = max(-32768, min(32767, s >> 8))
+                    else:
+                        assert s < 1 << 24
+                        out[n, c, oh, ow] = math.isqrt(s)
+    return out
+
+
+@pytest.mark.parametrize("pool_type", [2, 3, 7, 255])
+@pytest.mark.parametrize("lp_order", [0, 1, 2, 3, 9])
+def test_pool_out_of_range_codes_closed_form(pool_type, lp_order):
+    """Any pool_type other than 0 (MAX) and 1 (AVG) is LpPool, and any lp_order other
+    than 1 is p = 2 (PoolingKernel.cpp:214-224, 256-263): each code against the
+    definition.  p = 2 on values whose window sums of squares stay below 2^24; p = 1
+    on full-range values whose sums wrap."""
+    N, C, H, W, ph, pw, sh, sw, pt, pl, dh, dw = 2, 3, 9, 8, 3, 2, 2, 1, 1, 0, 1, 2
+    OH = (H + 2 * pt - dh * (ph - 1) - 1) // sh + 1
+    OW = (W + 2 * pl - dw * (pw - 1) - 1) // sw + 1
+    p = 1 if lp_order == 1 else 2
+    g = wl.rng(913, pool_type, lp_order)
+    if p == 1:
+        x = g.integers(-32768, 32768, size=(N, C, H, W)).astype(np.int16)
+    else:
+        x = g.integers(-1365, 1366, size=(N, C, H, W)).astype(np.int16)   # 6 * 1365^2 < 2^24
+    want = _closed_form_lp(x, OH, OW, ph, pw, sh, sw, pt, pl, dh, dw, p)
+    for threads in (False, True):
+        y = np.full(N * C * OH * OW, 99, np.int16)
+        oracle.pool(x.reshape(-1), y, N, C, H, W, OH, OW, ph, pw, sh, sw, pt, pl, dh, dw,
+                    pool_type, lp_order, 0, threads=threads)
+        np.testing.assert_array_equal(y.reshape(N, C, OH, OW), want)

@@ -1,7 +1,8 @@
 """cm_matmul_noalloc (split-K partials in the library's static device array)
-against cm_matmul_ex with a caller workspace, bit for bit, through the C ABI:
-two calls in a row, the second with a smaller input, then a shape whose
-partials exceed the array (rejected, nothing launched)."""
+against cm_matmul_ex with a caller workspace and against the CPU oracle, bit for
+bit, through the C ABI: two calls in a row, the second with a smaller input
+(full-range operands whose sums wrap), then a shape whose partials exceed the
+array (rejected, nothing launched)."""
 from __future__ import annotations
 
 import ctypes
@@ -12,7 +13,8 @@ import pytest
 from cormorant_amd import _native
 from cormorant_amd import kernels as K
 from cormorant_amd import workloads as wl
-from tests.gpu_util import dev, empty_dev, host, say
+import oracle
+from tests.gpu_util import dev, empty_dev, host, oracle_threads, say
 
 pytestmark = pytest.mark.gpu
 
@@ -57,6 +59,16 @@ def test_noalloc_matches_workspace_entry_point():
         rc = _noalloc(da, db, got, n, k, m, epi=epi)
         assert rc == 0, _native.last_error()
         np.testing.assert_array_equal(host(got), host(want))
+        # and against the oracle directly: MatMul, then the Add of the column
+        # vector per row and Clip(0,6) as the separate VectorOP calls compute them
+        ref = np.zeros(n * m, np.int16)
+        oracle.set_threads(oracle_threads())
+        oracle.matmul(a, b, ref, n, k, m, threads=True)
+        if fused:
+            tmp = ref.copy()
+            oracle.vectorop(tmp, host(add), ref, m, 0, n, m, 0)
+            oracle.vectorop(ref.copy(), ref.copy(), ref, n * m, 5)
+        np.testing.assert_array_equal(host(got), ref)
 
 
 def test_noalloc_rejects_partials_beyond_the_array():
