@@ -90,12 +90,34 @@ def build_bench() -> str:
     return BENCH_BIN
 
 
+GEN_DIR = os.path.join(HERE, "..", "tests", "c", "gen")
+
+
+def build_generated_projects() -> list:
+    """Emit the C projects of the two benchmark graphs (the MLP and the
+    MobileNetV2-like network) with scheduler.codegen under tests/c/gen/ and build
+    each with its own Makefile; the GPU tests run their test programs."""
+    from . import workloads as wl
+    from .scheduler import OnnxGraph, codegen, onnx_io as ox
+    built = []
+    for name, model in (("mlp_b64", wl.mlp_model()), ("mobilenet_like_b16", wl.mobilenet_model())):
+        out = os.path.abspath(os.path.join(GEN_DIR, name))
+        codegen.write_project(OnnxGraph(ox.encode_model(model)), out, name)
+        r = subprocess.run(["make", "-s", "-B", "-C", out], capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"generated project {name} failed to build:\n{r.stdout}\n{r.stderr}")
+        built.append(os.path.join(out, "test_inference"))
+    return built
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     args = ap.parse_args()
     print(build(args.jobs))
     print(build_bench())
+    for p in build_generated_projects():
+        print(p)
 
 
 if __name__ == "__main__":
