@@ -194,8 +194,12 @@ def bench_gemm(steps: int, warmup: int):
         a, b = wl.gemm_operands(case, cid)
         da, db = dev(a), dev(b)
         dc = torch.empty(case.batch * case.n * case.m, dtype=torch.int16, device="cuda")
+        # the caller-owned workspace the call uses (the packed B of the direct-to-LDS path)
+        need = K.matmul_workspace_size(case.n, case.k, case.m, case.batch, case.n * case.k,
+                                       case.k * case.m, case.n * case.m)
+        ws = torch.empty(max(need, 4) // 4, dtype=torch.int32, device="cuda")
         fn = lambda: K.MatmulKernel(da, db, dc, case.n, case.k, case.m, case.batch,
-                                    case.n * case.k, case.k * case.m, case.n * case.m)
+                                    case.n * case.k, case.k * case.m, case.n * case.m, workspace=ws)
         for _ in range(warmup):
             fn()
         ms = time_launches([fn], steps)
@@ -205,7 +209,9 @@ def bench_gemm(steps: int, warmup: int):
             ms=round(ms, 5), gops=round(gops, 1),
             mfma_int8_tops=round(LIMB_PRODUCTS * gops / 1e3, 2),
             mfma_frac=round(LIMB_PRODUCTS * gops / 1e3 / INT8_PEAK_TOPS, 4),
-            kernel="q88_gemm (dense)")
+            workspace_bytes=need,
+            kernel="gemm_bpack + gemm_dma (B packed per call, A streamed into LDS)" if need
+            else "q88_gemm (dense)")
         out[case.name]["_dev"] = (da, db, dc, a, b)
     return out
 

@@ -1056,6 +1056,9 @@ int launch_gemm(GemmArgs& g0, uint32_t zdim, const LaunchCtx& lc, const char* na
 
 int cm_matmul_rk_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k, uint32_t m,
                         const cm_epilogue_t* epi, const LaunchCtx& lc);
+int cm_gemm_dma_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
+                       uint32_t m, uint32_t batch, uint32_t a_bs, uint32_t b_bs, uint32_t c_bs,
+                       const cm_epilogue_t* epi, const LaunchCtx& lc);
 
 int cm_matmul_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
                      uint32_t m, uint32_t batch, uint32_t a_bs, uint32_t b_bs, uint32_t c_bs,
@@ -1081,6 +1084,12 @@ int cm_matmul_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n,
     // block's waves (matmul_rk.hip)
     if (batch == 1) {
         const int rc = cm_matmul_rk_launch(g.a, g.b, g.c, n, k, m, epi, lc);
+        if (rc != 1) return rc;
+    }
+    // large products with a workspace for the packed B: operands streamed into
+    // LDS by direct-to-LDS loads (gemm_dma.hip)
+    {
+        const int rc = cm_gemm_dma_launch(g.a, g.b, g.c, n, k, m, batch, a_bs, b_bs, c_bs, epi, lc);
         if (rc != 1) return rc;
     }
     // Batches whose outputs overlap (0 < c_stride < n*m) run one launch each, in

@@ -23,8 +23,10 @@
  *     memory (cm_buf_alloc is the allocator, as inference_buf_alloc is in the
  *     reference).  A MatMul / Conv call whose output tiles are too few to
  *     fill the GPU can split its k range over extra blocks and add the
- *     partial sums in a second pass; the partials go to a WORKSPACE the
- *     caller provides: per call (cm_matmul_ex / cm_conv_ex) or as the default
+ *     partial sums in a second pass, and a large MatMul (at least 256 output
+ *     tiles of 128 x 128, K <= 32768, K and M multiples of 8, 16-byte aligned
+ *     operands) packs its B operand into MFMA-ready limb fragments once per
+ *     call; the partials and the packed B go to a WORKSPACE the caller provides: per call (cm_matmul_ex / cm_conv_ex) or as the default
  *     for calls that take none (cm_set_workspace).  The size a call would use
  *     is returned by cm_matmul_workspace_size / cm_conv_workspace_size; a
  *     smaller workspace gives fewer splits, none gives none -- the result is
