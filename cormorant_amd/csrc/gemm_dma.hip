@@ -52,6 +52,7 @@ constexpr uint32_t kStage = kStageA + kStageB;
 constexpr uint32_t kTilePitch = 132;               // epilogue tile row pitch (words)
 constexpr uint32_t kMaxK = 32768;
 constexpr uint32_t kGroupRows = 8;                 // row tiles per group of the tile order
+constexpr uint64_t kPackBlocks = 1024;             // pack grid target (four per CU of an MI355X)
 
 struct DmaArgs {
     const int16_t* a;
@@ -435,9 +436,10 @@ int cm_gemm_dma_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t 
     const uint32_t nct8 = (m + 127u) / 128u * 8u;
     const uint32_t nbb = b_bs == 0 ? 1u : batch;   // B broadcast over the batch: packed once
     if (nbb > 65535u) return 1;                     // the pack grid's y extent
-    // pack grid: column groups x packed batches x k chunks, about four blocks per CU
+    // pack grid: column groups x packed batches x k chunks, about kPackBlocks
+    // blocks (a fixed target, so that the workspace size depends on the shape only)
     const uint64_t pack_blocks = (uint64_t)(nct8 / 8u) * nbb;
-    const uint64_t want_kc = (4ull * cm_cu_count() + pack_blocks - 1) / pack_blocks;
+    const uint64_t want_kc = (kPackBlocks + pack_blocks - 1) / pack_blocks;
     const uint32_t spc = (uint32_t)((nk + (want_kc < nk ? want_kc : nk) - 1) / (want_kc < nk ? want_kc : nk));
     const uint32_t nkc = (nk + spc - 1) / spc;
     const uint64_t bp_bs = (uint64_t)nk * nct8 * 2048u;

@@ -86,13 +86,24 @@ def test_missing_library_fails_loudly(tmp_path):
 
 
 def test_workspace_size_queries():
-    """cm_*_workspace_size: a dry run of the launch decision (no GPU work).  Shapes
-    whose 128 x 128 output tiles fill the GPU never split; few tiles over a long k
-    range split into at most 16 parts of uint32 partials, rows x cols rounded up
-    to 8 columns."""
+    """cm_*_workspace_size: a dry run of the launch decision (no GPU work).  Large
+    MatMuls (>= 256 output tiles of 128 x 128) pack B into limb fragments: 2 KB per
+    16 columns and 64 k, plus uint32 column sums per k chunk of the pack grid
+    (about 1024 blocks); other shapes whose tiles fill the GPU never split; few
+    tiles over a long k range split into at most 16 parts of uint32 partials,
+    rows x cols rounded up to 8 columns."""
     lib = _native.load()
-    assert lib.cm_matmul_workspace_size(4096, 4096, 4096, 1, 0, 0, 0) == 0
-    assert lib.cm_matmul_workspace_size(1024, 1024, 1024, 32, 1 << 20, 1 << 20, 1 << 20) == 0
+    # 4096^3: 64 k steps x 256 column tiles x 2 KB; 32 column groups -> 32 k chunks of 2 steps
+    assert lib.cm_matmul_workspace_size(4096, 4096, 4096, 1, 0, 0, 0) == \
+        64 * 256 * 2048 + 32 * 256 * 16 * 4
+    # batch 32 of 1024^3: 32 x (16 x 64 x 2 KB) and 8 groups x 32 batches -> 4 k chunks
+    assert lib.cm_matmul_workspace_size(1024, 1024, 1024, 32, 1 << 20, 1 << 20, 1 << 20) == \
+        32 * (16 * 64 * 2048 + 4 * 64 * 16 * 4)
+    # a broadcast B is packed once: 8 groups -> 16 k chunks of one step
+    assert lib.cm_matmul_workspace_size(1024, 1024, 1024, 32, 1 << 20, 0, 1 << 20) == \
+        16 * 64 * 2048 + 16 * 64 * 16 * 4
+    # m not a multiple of 8: the general path, no split
+    assert lib.cm_matmul_workspace_size(4096, 4096, 4092, 1, 0, 0, 0) == 0
     # one tile, 79 k steps: 16 splits of 100 x 64 (60 rounded up) words
     assert lib.cm_matmul_workspace_size(100, 5000, 60, 1, 0, 0, 0) == 16 * 100 * 64 * 4
     # 16 x 1280 x 1000 (16,000 outputs, 20 k steps) takes the register-only kernel: none
