@@ -25,6 +25,7 @@
 namespace {
 
 typedef short v8s __attribute__((ext_vector_type(8)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
 
 constexpr int kThreads = 256;
 constexpr int kNonTemporal = 2;   // buffer access cache policy: nt
@@ -78,9 +79,45 @@ __device__ __forceinline__ int32_t valid_taps(int32_t base, int32_t k, int32_t d
 __device__ __forceinline__ uint32_t wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // ---------------------------------------------------------------- global --
-constexpr int kBatch = 8;   // 16-byte loads in flight per lane
-
+// One wavefront per plane, NB 16-byte loads per lane in flight (NB fitted to the
+// plane on the host: 1, 2, 4, or 8 repeated).  Each 16-byte vector (8 values, 4
+// packed pairs) is reduced on the raw values: sums of x (AVG) and x^2 (LP p=2)
+// by v_dot2 on the pairs, maxima by the packed 16-bit max, |x| (LP p=1) value by
+// value; the int32 sums wrap, and (sum of x) << 8 equals the sum of x << 8
+// modulo 2^32, so shifting once at the end gives the reference accumulator.
 template <int KIND>
+struct RawAcc {
+    typedef short v2s __attribute__((ext_vector_type(2)));
+    uint32_t s = KIND == K_MAX ? 0x80008000u : 0u;   // MAX: two packed int16 maxima
+    __device__ __forceinline__ void add_pair(uint32_t w) {
+        if constexpr (KIND == K_MAX) {
+            s = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(v2s, s),
+                                                                       __builtin_bit_cast(v2s, w)));
+        } else if constexpr (KIND == K_AVG) {
+            s = (uint32_t)__builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, w), v2s{1, 1}, (int32_t)s, false);
+        } else if constexpr (KIND == K_LP1) {
+            s += (uint32_t)__builtin_abs((int32_t)(int16_t)(w & 0xFFFFu)) + (uint32_t)__builtin_abs((int32_t)w >> 16);
+        } else {
+            const v2s p = __builtin_bit_cast(v2s, w);
+            s = (uint32_t)__builtin_amdgcn_sdot2(p, p, (int32_t)s, false);
+        }
+    }
+    __device__ __forceinline__ void add_one(int32_t x) { add_pair(KIND == K_MAX ? ((uint32_t)x & 0xFFFFu) | 0x80000000u
+                                                                                 : (uint32_t)x & 0xFFFFu); }
+    // the reference accumulator (Acc<KIND>::v) of this lane's values
+    __device__ __forceinline__ uint32_t acc() const {
+        if constexpr (KIND == K_MAX) {
+            const int32_t lo = (int32_t)(int16_t)(s & 0xFFFFu), hi = (int32_t)s >> 16;
+            return (uint32_t)__builtin_elementwise_max(lo, hi) << 8;
+        } else if constexpr (KIND == K_LP2) {
+            return s;
+        } else {
+            return s << 8;
+        }
+    }
+};
+
+template <int KIND, int NB>
 __global__ __launch_bounds__(kThreads) void pool_global(const int16_t* __restrict__ x,
                                                         int16_t* __restrict__ y, uint64_t planes,
                                                         uint32_t hw, float inv, uint32_t vec_ok) {
@@ -88,34 +125,32 @@ __global__ __launch_bounds__(kThreads) void pool_global(const int16_t* __restric
     const uint64_t plane = (uint64_t)blockIdx.x * (kThreads / 64) + wave_id();
     if (plane >= planes) return;
     const int16_t* xp = x + plane * hw;
-    Acc<KIND> a;
+    RawAcc<KIND> r;
     uint32_t done = 0;
     if (vec_ok) {
         // range-checked buffer loads: past the plane they read 0 and touch no
-        // memory, so none needs a branch and all kBatch are in flight together
+        // memory, so none needs a branch and all NB are in flight together
         // (a guarded load became a branch with a wait for every earlier load);
-        // 0 adds nothing to a sum, and MAX masks those elements to -32768
+        // 0 adds nothing to a sum, and MAX replaces those vectors by -32768
         const uint32_t nv = hw / 8;
         const __amdgpu_buffer_rsrc_t rs = make_rsrc(xp, nv * 16u);
-        for (uint32_t base = 0; base < nv; base += 64 * kBatch) {
-            v8s t[kBatch];
+        for (uint32_t base = 0; base < nv; base += 64 * NB) {
+            v4u t[NB];
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u)
-                t[u] = __builtin_bit_cast(v8s, __builtin_amdgcn_raw_buffer_load_b128(
-                                                   rs, (base + u * 64 + lane) * 16u, 0, kNonTemporal));
+            for (int u = 0; u < NB; ++u)
+                t[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, (base + u * 64 + lane) * 16u, 0, kNonTemporal);
 #pragma unroll
-            for (int u = 0; u < kBatch; ++u) {
-                const int32_t m = -(int32_t)(base + u * 64 + lane < nv);
+            for (int u = 0; u < NB; ++u) {
+                const bool in = base + u * 64 + lane < nv;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int32_t x = t[u][j];
-                    a.add(KIND == K_MAX ? (x & m) | (-32768 & ~m) : x);
-                }
+                for (int j = 0; j < 4; ++j) r.add_pair(KIND == K_MAX && !in ? 0x80008000u : t[u][j]);
             }
         }
         done = nv * 8;
     }
-    for (uint32_t i = done + lane; i < hw; i += 64) a.add(xp[i]);
+    for (uint32_t i = done + lane; i < hw; i += 64) r.add_one(xp[i]);
+    Acc<KIND> a;
+    a.v = r.acc();
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) a.merge((uint32_t)__shfl_xor((int)a.v, off, 64));
     if (lane == 0) y[plane] = a.finish(inv);
@@ -533,7 +568,6 @@ __global__ __launch_bounds__(kThreads) void pool_strip(const int16_t* __restrict
         const __amdgpu_buffer_rsrc_t rs = make_rsrc(base, bytes);
 #pragma unroll
         for (int u = 0; u < PRE; ++u) {
-            typedef uint32_t v4u __attribute__((ext_vector_type(4)));
             const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rs, (u * kThreads + threadIdx.x) * 16u, 0, kNonTemporal);
             pre[u] = __builtin_bit_cast(v8s, v);
         }
@@ -944,9 +978,18 @@ int pool_launch(const int16_t* x, int16_t* y, uint64_t planes, const PoolGeom& g
         const uint32_t vec_ok = (hw % 8 == 0) && (((uintptr_t)x & 15u) == 0);
         const uint64_t blocks = (planes + 3) / 4;
         if (blocks > 0x7FFFFFFFull) return cm_set_error(CM_ERR_RANGE, "pool: too many planes");
-        // no padding: the valid count equals the window size for either cip
-        hipLaunchKernelGGL(pool_global<KIND>, dim3((uint32_t)blocks), dim3(kThreads), 0, s, x, y,
-                           planes, (uint32_t)hw, host_inv_denom(hw), vec_ok);
+        // no padding: the valid count equals the window size for either cip; the
+        // loads per lane in flight fitted to the plane's 16-byte vectors
+        const uint64_t per_lane = (hw / 8 + 63) / 64;
+        const float inv_hw = host_inv_denom(hw);
+#define CM_POOL_GLOBAL(NB)                                                                       \
+    hipLaunchKernelGGL((pool_global<KIND, NB>), dim3((uint32_t)blocks), dim3(kThreads), 0, s, x, y, \
+                       planes, (uint32_t)hw, inv_hw, vec_ok)
+        if (per_lane <= 1) CM_POOL_GLOBAL(1);
+        else if (per_lane <= 2) CM_POOL_GLOBAL(2);
+        else if (per_lane <= 4) CM_POOL_GLOBAL(4);
+        else CM_POOL_GLOBAL(8);
+#undef CM_POOL_GLOBAL
         return cm_check_launch("pool_global");
     }
     // The band kernel indexes with 32-bit arithmetic: only shapes well inside

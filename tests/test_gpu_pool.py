@@ -152,3 +152,23 @@ def test_out_of_range_type_and_order_codes(ptype, lp, geom):
     x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
     got, want = pool_both(x, N, C, H, W, OH, OW, ph, pw, sh, sw, pt, pl, dh, dw, ptype, lp, 0)
     np.testing.assert_array_equal(got, want)
+
+
+GLOBAL_PLANES = [(8, 64), (8, 65), (28, 28), (10, 160), (60, 80), (56, 56), (7, 9), (1, 3)]
+
+
+@pytest.mark.parametrize("ptype,lp", [(0, 0), (1, 0), (2, 1), (2, 2)])
+@pytest.mark.parametrize("hw", GLOBAL_PLANES, ids=[f"{h}x{w}" for h, w in GLOBAL_PLANES])
+def test_global_pool_load_counts(ptype, lp, hw):
+    """Global pools on planes whose 16-byte vectors take 1, 2, 4 or 8 loads per lane
+    (one and two passes of the 8-load loop), and on planes that are no whole number
+    of vectors (the element path), every reduction kind, full-range values (sums
+    that wrap, negative maxima against the zero reads past a plane)."""
+    H, W = hw
+    N, C = 3, 5
+    say(f"global pool {H}x{W} type={ptype} lp={lp}")
+    g = wl.rng(813, ptype, lp, H, W)
+    x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
+    x[: H * W] = -(np.arange(H * W) % 7000) - 100          # an all-negative plane
+    got, want = pool_both(x, N, C, H, W, 1, 1, H, W, 1, 1, 0, 0, 1, 1, ptype, lp, 1)
+    np.testing.assert_array_equal(got, want)
