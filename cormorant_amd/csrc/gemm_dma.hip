@@ -171,14 +171,27 @@ __device__ __forceinline__ v4u sdesc(const void* base, uint32_t bytes) {
                (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xFFFFu),
                (uint32_t)__builtin_amdgcn_readfirstlane(bytes), (uint32_t)kBufferWord3};
 }
-// 16 bytes per lane from the buffer at byte offset voff into LDS at m0 + lane * 16.
-// Issued as inline asm: the compiler then neither waits for these loads before
-// every LDS read (it cannot tell the stages apart) nor counts them; the kernel
-// waits for them itself (wait_vm before the barrier that publishes a stage).
-__device__ __forceinline__ void dma16(const v4u& desc, uint32_t voff, uint32_t lds_addr) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :: "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voff), "s"(desc)
-                 : "memory", "m0");
+// One stage of loads: 16 bytes per lane from buffer da at byte offsets a0, a1
+// into LDS at la0 / la1 + lane * 16, then the same from buffer db at b0, b1 into
+// lb0 / lb1 (each LDS address goes through M0). Issued as inline asm: the
+// compiler then neither waits for these loads before every LDS read (it cannot
+// tell the stages apart) nor counts them; the kernel waits for them itself
+// (wait_vm before the barrier that publishes a stage). M0 is saved first and
+// restored last, so the asm leaves it as it found it.
+__device__ __forceinline__ void dma_stage(const v4u& da, uint32_t a0, uint32_t a1, uint32_t la0, uint32_t la1,
+                                          const v4u& db, uint32_t b0, uint32_t b1, uint32_t lb0, uint32_t lb1) {
+    uint32_t saved;
+    asm volatile("s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %1\n\ts_nop 0\n\tbuffer_load_dwordx4 %5, %9, 0 offen lds\n\t"
+                 "s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %6, %9, 0 offen lds\n\t"
+                 "s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %7, %10, 0 offen lds\n\t"
+                 "s_mov_b32 m0, %4\n\ts_nop 0\n\tbuffer_load_dwordx4 %8, %10, 0 offen lds\n\t"
+                 "s_nop 0\n\ts_mov_b32 m0, %0"
+                 : "=&s"(saved)
+                 : "s"(__builtin_amdgcn_readfirstlane(la0)), "s"(__builtin_amdgcn_readfirstlane(la1)),
+                   "s"(__builtin_amdgcn_readfirstlane(lb0)), "s"(__builtin_amdgcn_readfirstlane(lb1)),
+                   "v"(a0), "v"(a1), "v"(b0), "v"(b1), "s"(da), "s"(db)
+                 : "memory");
 }
 
 template <uint32_t N>
@@ -227,20 +240,16 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dma(DmaArgs g) {
         a_off[q] = (row * g.k + c * 8u) * 2u;
     }
     auto issue = [&](uint32_t s) {
-        const uint32_t st = lds0 + (s % kStages) * kStage;
+        const uint32_t st = lds0 + (s % kStages) * kStage + wave * 64u * 16u;
         const uint32_t k0 = s * BK;
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            // chunks at or past K (and every chunk of a step past the last) read 0
-            const uint32_t off = k0 + a_kc[q] < g.k ? a_off[q] + k0 * 2u : kOob;
-            dma16(ars, off, st + (q * kThreads + wave * 64u) * 16u);
-        }
+        // A chunks at or past K (and every chunk of a step past the last) read 0
+        const uint32_t a0 = k0 + a_kc[0] < g.k ? a_off[0] + k0 * 2u : kOob;
+        const uint32_t a1 = k0 + a_kc[1] < g.k ? a_off[1] + k0 * 2u : kOob;
         const uint32_t bbase = s < g.nk ? (s * g.nct8 + bx * 8u) * 2048u : kOob;
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const uint32_t u = q * kThreads + tid;
-            dma16(brs, bbase == kOob ? kOob : bbase + u * 16u, st + kStageA + (q * kThreads + wave * 64u) * 16u);
-        }
+        const uint32_t b0 = bbase == kOob ? kOob : bbase + tid * 16u;
+        const uint32_t b1 = bbase == kOob ? kOob : bbase + (kThreads + tid) * 16u;
+        dma_stage(ars, a0, a1, st, st + kThreads * 16u,
+                  brs, b0, b1, st + kStageA, st + kStageA + kThreads * 16u);
     };
 
     v4i hh[2][4], mid[2][4], ll[2][4];
