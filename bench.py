@@ -85,6 +85,9 @@ def summarize(results: dict, cases: list, cpu_res: dict) -> dict:
     for name, e in results.items():
         if name.startswith("gemm_"):
             s[name] = dict(gops=e["gops"], mfma_frac=e["mfma_frac"])
+            lib = e.get("library_int8", {})
+            if "mfma_frac" in lib:
+                s[name]["library_int8_mfma_frac"] = lib["mfma_frac"]
         elif name.startswith("conv_"):
             s[name] = dict(gops=e["gops"], mfma_frac_issued=e["mfma_frac"],
                            frac_4product=e["frac_of_4product_roofline"])
@@ -212,8 +215,31 @@ def bench_gemm(steps: int, warmup: int):
             workspace_bytes=need,
             kernel="gemm_bpack + gemm_dma (B packed per call, A streamed into LDS)" if need
             else "q88_gemm (dense)")
+        out[case.name]["library_int8"] = library_int8_gemm(case, steps)
         out[case.name]["_dev"] = (da, db, dc, a, b)
     return out
+
+
+def library_int8_gemm(case, steps: int):
+    """The platform's own int8 GEMM rate at the case's shape: torch._int_mm
+    (hipBLASLt) on random int8 operands, B column-major (its faster layout), one
+    call per batch.  It computes ONE int8 product per MAC where the exact Q8.8
+    kernel issues four, so its MFMA fraction is the practical ceiling for an
+    MFMA fraction at this shape."""
+    import torch
+    try:
+        g = torch.Generator(device="cuda").manual_seed(7)
+        a8 = torch.randint(-128, 128, (case.n, case.k), dtype=torch.int8, device="cuda", generator=g)
+        b8 = torch.randint(-128, 128, (case.m, case.k), dtype=torch.int8, device="cuda", generator=g).t()
+        fn = lambda: torch._int_mm(a8, b8)
+        for _ in range(3):
+            fn()
+        ms = time_launches([fn], steps * case.batch) * case.batch
+    except (RuntimeError, AttributeError) as ex:   # no int8 GEMM in this torch build
+        return dict(kernel="torch._int_mm", error=str(ex)[:200])
+    tops = 2.0 * case.macs / (ms * 1e-3) / 1e12
+    return dict(kernel="torch._int_mm (hipBLASLt), int8 x int8 -> int32, B column-major",
+                ms=round(ms, 5), int8_tops=round(tops, 1), mfma_frac=round(tops / INT8_PEAK_TOPS, 4))
 
 
 # ------------------------------------------------------- conv + pool block --

@@ -206,7 +206,8 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dma(DmaArgs g) {
     __shared__ uint32_t row_sum[BM];
     __shared__ uint32_t col_sum[BN];
     touch_lines(g);
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = tid >> 6;
     // XCD-aware order: workgroups are dealt to the 8 XCDs round robin; XCD x
     // takes the x-th contiguous share of the (batch, row tile, column tile)
     // order, so that blocks sharing A rows and B columns meet in one L2
@@ -257,14 +258,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dma(DmaArgs g) {
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) hh[i][j] = mid[i][j] = ll[i][j] = v4i{0, 0, 0, 0};
-    int32_t rsum[2] = {0, 0};
+    // A row sums: the two waves of a wave row read the same 32 A rows, so each
+    // sums 16 of them: wave column wc holds row tile wc as its fragment set 0
+    // (set i is row tile i ^ wc) and sums set 0's words
+    int32_t rsum = 0;
 
     // fragment addresses: A row r = 32 wr + 16 i + (lane % 16), logical chunks 2q, 2q + 1
     const uint32_t q4 = lane >> 4;
     uint32_t a_rd[2][2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const uint32_t r = wr * 32u + i * 16u + (lane & 15u), f = (r >> 1) & 7u;
+        const uint32_t r = wr * 32u + (i ^ wc) * 16u + (lane & 15u), f = (r >> 1) & 7u;
         a_rd[i][0] = r * 128u + (((2u * q4) ^ f) << 4);
         a_rd[i][1] = r * 128u + (((2u * q4 + 1u) ^ f) << 4);
     }
@@ -289,7 +293,17 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dma(DmaArgs g) {
             f.r1[i] = *reinterpret_cast<const v4u*>(st + a_rd[i][1]);
         }
     };
+    auto row_words = [&](const v4u& r0, const v4u& r1) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            // (a vector element copied out first: bit_cast of r0[e] itself reads r0[0])
+            const uint32_t w0 = r0[e], w1 = r1[e];
+            rsum = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, w0), v2s{1, 1}, rsum, false);
+            rsum = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, w1), v2s{1, 1}, rsum, false);
+        }
+    };
     auto compute = [&](const Frags& f) {
+        row_words(f.r0[0], f.r1[0]);
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const v4u r0 = f.r0[i], r1 = f.r1[i];
@@ -297,13 +311,6 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dma(DmaArgs g) {
                                (int)hi4(r1[0], r1[1]), (int)hi4(r1[2], r1[3])};
             const v4i al = v4i{(int)lo4(r0[0], r0[1]), (int)lo4(r0[2], r0[3]),
                                (int)lo4(r1[0], r1[1]), (int)lo4(r1[2], r1[3])};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                // (a vector element copied out first: bit_cast of r0[e] itself reads r0[0])
-                const uint32_t w0 = r0[e], w1 = r1[e];
-                rsum[i] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, w0), v2s{1, 1}, rsum[i], false);
-                rsum[i] = __builtin_amdgcn_sdot2(__builtin_bit_cast(v2s, w1), v2s{1, 1}, rsum[i], false);
-            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 hh[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah, f.bh[j], hh[i][j], 0, 0, 0);
@@ -341,12 +348,11 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dma(DmaArgs g) {
     __syncthreads();     // every wave is done with the stages: the tile may reuse them
 
     // row sums (lanes l, l+16, l+32, l+48 hold one row's four k groups) and column sums
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        int32_t v = rsum[i];
+    {
+        int32_t v = rsum;
         v += __shfl_xor(v, 16, 64);
         v += __shfl_xor(v, 32, 64);
-        if (wc == 0u && lane < 16u) row_sum[wr * 32u + i * 16u + lane] = (uint32_t)v;
+        if (lane < 16u) row_sum[wr * 32u + wc * 16u + lane] = (uint32_t)v;
     }
     if (tid < BN) {
         const uint32_t c = col0 + tid;
@@ -364,7 +370,7 @@ __global__ __launch_bounds__(kThreads, 1) void gemm_dma(DmaArgs g) {
             for (int e = 0; e < 4; ++e) {
                 const uint32_t v = ((uint32_t)hh[i][j][e] << 16) + ((uint32_t)mid[i][j][e] << 8) +
                                    (uint32_t)ll[i][j][e];
-                tile[(wr * 32u + i * 16u + q4 * 4u + e) * kTilePitch + wc * 64u + j * 16u + (lane & 15u)] = v;
+                tile[(wr * 32u + (i ^ wc) * 16u + q4 * 4u + e) * kTilePitch + wc * 64u + j * 16u + (lane & 15u)] = v;
             }
     __syncthreads();
 
