@@ -55,6 +55,12 @@ SHAPES = [
     ("broadcast_b", 6, 1024, 320, 768, True, 0),
     ("gapped_c", 4, 1024, 256, 1024, False, 8),       # batch outputs with 8-element gaps
     ("long_k", 1, 2048, 8192, 2048, False, 0),
+    # the kernel is persistent (one block per CU walking its tiles, the next tile's
+    # first steps loaded during the current one's last): several tiles per block,
+    # shares of unequal length, odd step counts, ragged edges on every side
+    ("many_tiles_ragged", 1, 3000, 264, 2600, False, 0),   # 24 x 21 = 504 tiles, 5 steps
+    ("batched_odd_steps", 5, 1000, 320, 1000, False, 0),   # 320 tiles, 5 steps
+    ("broadcast_many", 9, 640, 256, 904, True, 16),        # 9 x 5 x 8 = 360 tiles, 4 steps, gaps
 ]
 
 
