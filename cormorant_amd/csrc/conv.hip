@@ -392,7 +392,7 @@ __device__ __forceinline__ uint32_t dot2(uint32_t x, uint32_t w, uint32_t acc) {
 }
 
 template <int MT, int KC, bool HAS_BIAS>
-__global__ __launch_bounds__(kDirThreads) void conv_direct(DirArgs g) {
+__global__ __launch_bounds__(kDirThreads) __attribute__((amdgpu_waves_per_eu(1, 4))) void conv_direct(DirArgs g) {
     touch_lines(g);
     extern __shared__ __align__(16) uint32_t dsm[];
     uint32_t* wt = dsm;                                                  // [KC / 2][MT]
@@ -466,15 +466,19 @@ __global__ __launch_bounds__(kDirThreads) void conv_direct(DirArgs g) {
     uint32_t acc[MT];
 #pragma unroll
     for (int mm = 0; mm < MT; ++mm) acc[mm] = 0u;
+    // per k pair: all MT weight words read first (MT / 4 broadcast LDS reads in
+    // flight together), then the MT dot products -- one LDS round trip per pair
 #pragma unroll
     for (uint32_t q = 0; q < (uint32_t)KC / 2; ++q) {
         const uint32_t xp = xv[2 * q] | xv[2 * q + 1] << 16;
         const uint32_t* wr = wt + q * MT;
+        v4u wv[MT / 4];
 #pragma unroll
-        for (int mm = 0; mm < MT; mm += 4) {
-            const v4u wv = *reinterpret_cast<const v4u*>(wr + mm);
+        for (int g4 = 0; g4 < MT / 4; ++g4) wv[g4] = *reinterpret_cast<const v4u*>(wr + 4 * g4);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) acc[mm + e] = dot2(xp, wv[e], acc[mm + e]);
+        for (int g4 = 0; g4 < MT / 4; ++g4) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) acc[4 * g4 + e] = dot2(xp, wv[g4][e], acc[4 * g4 + e]);
         }
     }
     // the products are done here: without the empty asm the compiler sinks them
