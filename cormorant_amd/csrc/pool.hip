@@ -896,6 +896,180 @@ PlaneGeom plane_geom(const PoolGeom& g, uint32_t kw) {
     return p;
 }
 
+// --------------------------------------------------------------- colpair --
+// Planes of at most 1024 elements with an even row length of at most 32 under a
+// K x K window (K = 2 or 3) at stride 2 in both directions, dilation 1 and equal
+// top and left padding P (0 or 1), at most 16 x 16 outputs: sixteen lanes per
+// group, S groups per plane (each taking 16 / S consecutive output rows), 4 / S
+// planes per wave, no per-output addressing.  The wave copies its planes into
+// LDS by 16-byte loads (per-row dword loads from memory were slower: four times
+// the load instructions, each touching four partial lines), then lane j of a
+// group reads input columns 2j and 2j + 1 of each row its outputs need as one
+// dword.  Output (oh, ow) sits on lane ow of the group holding row oh: its
+// window covers input rows 2oh - P .. 2oh - P + K - 1 and input columns
+// 2ow - P .. 2ow - P + K - 1, i.e. the lane's own pairs and at most one element
+// of a neighbouring lane, fetched with a DPP row shift (the 16-lane DPP row is
+// the group, so no shift crosses groups).  Positions outside the plane take the
+// pad value of the reduction before any arithmetic (-32768 for MAX, 0 for the
+// sums), which is the reference's treatment of a padded tap
+// (PoolingKernel.cpp:151-173, 197-212).  One plane per wave (S = 4) keeps many
+// small waves in flight, so early waves reduce and store while later waves'
+// loads still stream; S = 2 and 1 serve planes whose size keeps a single
+// plane's start off 16-byte alignment.
+constexpr uint32_t kCpMaxOut = 16;   // output rows / columns per plane
+constexpr uint32_t kCpMaxHW = 1024;  // elements per plane (32 x 32)
+constexpr int kCpSlotWords = 4 * kCpMaxHW / 2;   // LDS dwords per wave: four planes at most
+// row reads reach one row (at most 16 dwords) before a wave's planes and, past
+// the last one, up to row 32 of the last plane's slot: front and back slack
+constexpr int kCpFront = 16;
+constexpr int kCpBack = 32 * 16 + 16;
+constexpr int kDppRowShl1 = 0x101;   // lane i reads lane i + 1 of its 16-lane row
+constexpr int kDppRowShr1 = 0x111;   // lane i reads lane i - 1
+
+// The value lane i + 1 (SHL) or i - 1 holds; `pad` at the row's edge lane.
+template <bool SHL>
+__device__ __forceinline__ int32_t dpp_neighbour(int32_t v, int32_t pad) {
+    return __builtin_amdgcn_update_dpp(pad, v, SHL ? kDppRowShl1 : kDppRowShr1, 0xF, 0xF, false);
+}
+
+// Taps t < K with 0 <= first + t < n.
+template <int K>
+__device__ __forceinline__ uint32_t taps_inside(int32_t first, uint32_t n) {
+    const int32_t c = __builtin_elementwise_min(first + K, (int32_t)n) - __builtin_elementwise_max(first, 0);
+    return (uint32_t)__builtin_elementwise_max(c, 0);
+}
+
+template <int KIND, int K, int P, int S>
+__global__ __launch_bounds__(kThreads) void pool_colpair(const int16_t* __restrict__ x,
+                                                         int16_t* __restrict__ y, PoolGeom g,
+                                                         uint64_t planes, float inv_full) {
+    typedef short v2s __attribute__((ext_vector_type(2)));
+    constexpr uint32_t PPW = 4 / S;                  // planes per wave
+    constexpr uint32_t RO = kCpMaxOut / S;           // output rows per lane group
+    constexpr int RR = 2 * ((int)RO - 1) + K;        // input rows per lane
+    touch_lines(g);
+    const uint32_t lane = threadIdx.x & 63, grp = lane >> 4, j = lane & 15;
+    const uint32_t pl = grp / S, part = grp % S;      // plane in the wave, row part
+    const uint64_t plane0 = ((uint64_t)blockIdx.x * (kThreads / 64) + wave_id()) * PPW;
+    if (plane0 >= planes) return;   // the whole wave leaves
+    const uint32_t np = (uint32_t)(planes - plane0 < PPW ? planes - plane0 : PPW);
+    const uint32_t hw = g.in_h * g.in_w, ohw = g.out_h * g.out_w;
+    // the wave's planes (contiguous, 16-byte aligned) are copied into its LDS slot
+    // by 16-byte range-checked loads (past the planes they read 0); every store is
+    // range-checked against the wave's planes
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + plane0 * hw, np * hw * 2u);
+    const __amdgpu_buffer_rsrc_t ry = make_rsrc(y + plane0 * ohw, np * ohw * 2u);
+    constexpr int SLOT = kCpSlotWords / S;
+    __shared__ __align__(16) uint32_t tile[kCpFront + kThreads / 64 * SLOT + kCpBack];
+    uint32_t* t = tile + kCpFront + wave_id() * SLOT;
+    {
+        constexpr int NV = SLOT / 4 / 64;   // 16-byte vectors per lane
+        v4u v[NV];
+#pragma unroll
+        for (int u = 0; u < NV; ++u)
+            v[u] = __builtin_amdgcn_raw_buffer_load_b128(rx, (u * 64 + lane) * 16u, 0, kNonTemporal);
+#pragma unroll
+        for (int u = 0; u < NV; ++u) *reinterpret_cast<v4u*>(t + (u * 64 + lane) * 4) = v[u];
+    }
+    wave_sync();
+    // register row i holds input row r0 + i; rows outside the plane read what
+    // lies there (inside the slots or their slack) and are masked to the pad
+    // value through a bit mask, not a select: a select let the compiler sink a
+    // read into a branch, after which the first row waited for every read
+    const int32_t r0 = (int32_t)(2 * RO * part) - P;
+    const uint32_t pitch = g.in_w / 2;
+    const uint32_t* tl = t + (int32_t)(pl * (hw / 2) + j) + r0 * (int32_t)pitch;
+    constexpr uint32_t kPadPair = KIND == K_MAX ? 0x80008000u : 0u;
+    const uint32_t col_m = 2u * j < g.in_w ? ~0u : 0u;
+    uint32_t d[RR];
+#pragma unroll
+    for (int i = 0; i < RR; ++i) {
+        const uint32_t m = (uint32_t)(r0 + i) < g.in_h ? col_m : 0u;
+        d[i] = (tl[(uint32_t)i * pitch] & m) | (kPadPair & ~m);
+    }
+    // output offsets: the lane's first row and column (past the range when the
+    // column is outside the plane), then one row step per output
+    const uint32_t oh0 = RO * part;
+    const uint32_t yb = j < g.out_w ? (pl * ohw + oh0 * g.out_w + j) * 2u : kOob;
+    // the outputs; CIP: AVG with count_include_pad (one denominator), a uniform
+    // choice made once
+    auto emit = [&](auto cip_tag) {
+        constexpr bool CIP = decltype(cip_tag)::value;
+        // AVG without count_include_pad: inv * 2^-8 (avg_finalize8) for each count
+        // of window rows inside the plane (0..K) times this lane's columns inside
+        // it, computed once (no division per output)
+        float inv8[K + 1];
+        if constexpr (KIND == K_AVG && !CIP) {
+            const uint32_t vcols = taps_inside<K>(2 * (int32_t)j - P, g.in_w);
+#pragma unroll
+            for (int vr = 0; vr <= K; ++vr)
+                inv8[vr] = q88::mul_rn(q88::inv_denom((uint32_t)vr * vcols), 1.0f / 256.0f);
+        }
+        const float inv8_full = q88::mul_rn(inv_full, 1.0f / 256.0f);
+#pragma unroll
+        for (uint32_t o = 0; o < RO; ++o) {
+            const uint32_t* r = d + 2 * o;
+            int32_t out;
+            if constexpr (KIND == K_MAX) {
+                // rows by the packed 16-bit max, then the columns of the low halves
+                v2s m = __builtin_elementwise_max(__builtin_bit_cast(v2s, r[0]), __builtin_bit_cast(v2s, r[1]));
+                if constexpr (K == 3) m = __builtin_elementwise_max(m, __builtin_bit_cast(v2s, r[2]));
+                const int32_t e0 = m[0], e1 = m[1];
+                int32_t v = __builtin_elementwise_max(e0, e1);
+                if constexpr (P == 0 && K == 3) v = __builtin_elementwise_max(v, dpp_neighbour<true>(e0, -32768));
+                if constexpr (P == 1 && K == 2) v = e0;
+                if constexpr (P == 1) v = __builtin_elementwise_max(v, dpp_neighbour<false>(e1, -32768));
+                out = v;
+            } else {
+                uint32_t s;
+                if constexpr (P == 0 && K == 2 && KIND != K_LP1) {
+                    // the window is the lane's own pairs of two rows: sums of x or
+                    // x^2 by v_dot2 (the int32 sum wraps like the reference accumulator)
+                    const v2s r0v = __builtin_bit_cast(v2s, r[0]), r1v = __builtin_bit_cast(v2s, r[1]);
+                    const v2s w0 = KIND == K_LP2 ? r0v : v2s{1, 1}, w1 = KIND == K_LP2 ? r1v : v2s{1, 1};
+                    s = (uint32_t)__builtin_amdgcn_sdot2(r1v, w1, __builtin_amdgcn_sdot2(r0v, w0, 0, false), false);
+                } else {
+                    // each column's rows summed (x, |x| or x^2, as wrapping uint32)
+                    auto term = [](int32_t e) -> uint32_t {
+                        if constexpr (KIND == K_LP1) return (uint32_t)__builtin_abs(e);
+                        else if constexpr (KIND == K_LP2) return (uint32_t)(e * e);
+                        else return (uint32_t)e;
+                    };
+                    uint32_t c0 = 0, c1 = 0;
+#pragma unroll
+                    for (int tp = 0; tp < K; ++tp) {
+                        c0 += term((int32_t)(int16_t)(r[tp] & 0xFFFFu));
+                        c1 += term((int32_t)r[tp] >> 16);
+                    }
+                    if constexpr (P == 0 && K == 3) s = c0 + c1 + (uint32_t)dpp_neighbour<true>((int32_t)c0, 0);
+                    else if constexpr (P == 0) s = c0 + c1;
+                    else if constexpr (K == 3) s = c0 + c1 + (uint32_t)dpp_neighbour<false>((int32_t)c1, 0);
+                    else s = c0 + (uint32_t)dpp_neighbour<false>((int32_t)c1, 0);
+                }
+                if constexpr (KIND == K_AVG) {
+                    float inv = inv8_full;
+                    if constexpr (!CIP) {
+                        const uint32_t vr = taps_inside<K>(r0 + 2 * (int32_t)o, g.in_h);
+                        inv = inv8[0];
+#pragma unroll
+                        for (int tp = 1; tp <= K; ++tp) inv = vr == (uint32_t)tp ? inv8[tp] : inv;
+                    }
+                    out = q88::avg_finalize8(s << 8, inv);
+                } else if constexpr (KIND == K_LP2) {
+                    out = q88::lp2_finalize(s);
+                } else {
+                    out = q88::acc_to_data(s << 8);
+                }
+            }
+            // (kOob plus a row offset stays below 2^32: still past the range)
+            const uint32_t yo = oh0 + o < g.out_h ? yb + o * g.out_w * 2u : kOob;
+            __builtin_amdgcn_raw_buffer_store_b16((int16_t)out, ry, yo, 0, 0);
+        }
+    };
+    if (KIND == K_AVG && !g.cip) emit(std::false_type{});
+    else emit(std::true_type{});
+}
+
 // ---------------------------------------------------------------- direct --
 template <int KIND>
 __global__ __launch_bounds__(kThreads) void pool_direct(const int16_t* __restrict__ x,
@@ -1001,6 +1175,31 @@ int pool_launch(const int16_t* x, int16_t* y, uint64_t planes, const PoolGeom& g
                        g.pw < (1u << 10) && (uint64_t)g.out_w * g.sw < (1u << 30) &&
                        (uint64_t)g.out_h * g.sh < (1u << 30) &&
                        (uint64_t)g.in_h * g.in_w < (1u << 30);
+    // planes of at most 1024 elements, rows of at most 32, under a 2x2 / 3x3
+    // window at stride 2: sixteen lanes per plane, rows in registers (pool_colpair)
+    const uint32_t kcp = g.ph == g.pw && (g.ph == 2 || g.ph == 3) ? g.ph : 0;
+    if (kcp && g.sh == 2 && g.sw == 2 && g.dh == 1 && g.dw == 1 && g.pt == g.pl && g.pt <= 1 &&
+        g.in_w % 2 == 0 && g.in_w <= 32 && (uint64_t)g.in_h * g.in_w <= kCpMaxHW &&
+        g.out_h <= kCpMaxOut && g.out_w <= kCpMaxOut && ((uintptr_t)x & 15u) == 0 &&
+        (planes + 15) / 16 <= 0x7FFFFFFFull) {
+        // one plane per wave when a plane's start stays 16-byte aligned, else two or four
+        const uint64_t hw = (uint64_t)g.in_h * g.in_w;
+        const uint32_t S = hw % 8 == 0 ? 4 : (hw % 4 == 0 ? 2 : 1);
+        const uint64_t per_block = 4 * (4 / S);
+        const dim3 grid((uint32_t)((planes + per_block - 1) / per_block)), block(kThreads);
+#define CM_COLPAIR(K_, P_, S_) \
+    hipLaunchKernelGGL((pool_colpair<KIND, K_, P_, S_>), grid, block, 0, s, x, y, g, planes, inv_full)
+#define CM_COLPAIR_S(K_, P_) \
+    do { if (S == 4) CM_COLPAIR(K_, P_, 4); else if (S == 2) CM_COLPAIR(K_, P_, 2); else CM_COLPAIR(K_, P_, 1); } while (0)
+        if (kcp == 3) {
+            if (g.pt) CM_COLPAIR_S(3, 1); else CM_COLPAIR_S(3, 0);
+        } else {
+            if (g.pt) CM_COLPAIR_S(2, 1); else CM_COLPAIR_S(2, 0);
+        }
+#undef CM_COLPAIR_S
+#undef CM_COLPAIR
+        return cm_check_launch("pool_colpair");
+    }
     // small planes: one wave per plane, the plane in LDS
     if (small && (uint64_t)g.in_h * g.in_w <= kPlaneMax && (uint64_t)g.out_h * g.out_w <= (1u << 24)) {
         const uint64_t blocks = (planes + 3) / 4;

@@ -92,23 +92,47 @@ __device__ __forceinline__ float acc_to_float(uint32_t acc) {
 // saturate_cast<Data_t>(AccData_t(f)) for |f| < 32768: AccData_t floors f to a
 // multiple of 2^-16 and the output keeps floor(f * 256), saturated (the scale is
 // exact).  Both pool finalisers stay in that range (see below).
-__device__ __forceinline__ int16_t float_to_data(float f) {
-    const float s = __builtin_amdgcn_fmed3f(__builtin_floorf(mul_rn(f, 256.0f)), -8388608.0f, 8388607.0f);
+__device__ __forceinline__ int16_t floor_to_data(float f256) {   // f256 = f * 256
+    const float s = __builtin_amdgcn_fmed3f(__builtin_floorf(f256), -8388608.0f, 8388607.0f);
     return (int16_t)sat16((int32_t)s);
 }
+__device__ __forceinline__ int16_t float_to_data(float f) { return floor_to_data(mul_rn(f, 256.0f)); }
 
 // PoolingKernel.cpp:137, 259, 265: AccData_t((float)acc * (1.0f / denom)).
 // |acc * 2^-16| <= 32768, times 1/d <= 1/2 for d >= 2; for d = 1 the sum is one
 // value << 8, so |f| <= 128; d = 0 gives 0: the result is always in range.
+// The reference's floor(fl32(fl32(raw) * 2^-16 * inv) * 256) is computed as
+// floor(fl32(fl32(raw) * inv8)) with inv8 = inv * 2^-8: power-of-two scalings
+// commute with rounding away from the subnormal range (|fl32(raw) * inv| is 0
+// or at least 2^-32 here), so both give the same float for every accumulator.
+__device__ __forceinline__ int16_t avg_finalize8(uint32_t acc, float inv8) {
+    return floor_to_data(mul_rn((float)(int32_t)acc, inv8));
+}
 __device__ __forceinline__ int16_t avg_finalize(uint32_t acc, float inv_denom) {
-    return float_to_data(mul_rn(acc_to_float(acc), inv_denom));
+    return avg_finalize8(acc, mul_rn(inv_denom, 1.0f / 256.0f));
+}
+
+// Correctly rounded square root of x = 0 or a normal x (the LP accumulator's
+// float: 0 or at least 2^-16): the hardware estimate, within one ulp, moved to
+// the nearest float by the signs of the residuals x - n * s of its neighbours n
+// (the same correction LLVM's IEEE square root applies, without its rescaling
+// of subnormal inputs).  Negative x gives NaN.
+__device__ __forceinline__ float sqrt_acc(float x) {
+    const float s = __builtin_amdgcn_sqrtf(x);
+    const float dn = __builtin_bit_cast(float, __builtin_bit_cast(int32_t, s) - 1);
+    const float up = __builtin_bit_cast(float, __builtin_bit_cast(int32_t, s) + 1);
+    float r = __builtin_fmaf(-dn, s, x) <= 0.0f ? dn : s;
+    r = __builtin_fmaf(-up, s, x) > 0.0f ? up : r;
+    return r;
 }
 
 // PoolingKernel.cpp:263, 265: AccData_t(sqrtf((float)acc)).  A non-negative
-// acc is below 2^31, so the root is at most 2^7.5.
+// acc is below 2^31, so the root is at most 2^7.5; a negative (wrapped) sum's
+// root is NaN, which the reference's conversion takes to 0 (selected, not
+// branched: the pool kernels keep every load in flight past it).
 __device__ __forceinline__ int16_t lp2_finalize(uint32_t acc) {
-    if ((int32_t)acc < 0) return 0;   // sqrt of a negative (wrapped) sum: NaN -> 0
-    return float_to_data(sqrt_rn(acc_to_float(acc)));
+    const int16_t r = float_to_data(sqrt_acc(acc_to_float(acc)));
+    return (int32_t)acc < 0 ? (int16_t)0 : r;
 }
 
 }  // namespace q88

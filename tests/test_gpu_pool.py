@@ -172,3 +172,42 @@ def test_global_pool_load_counts(ptype, lp, hw):
     x[: H * W] = -(np.arange(H * W) % 7000) - 100          # an all-negative plane
     got, want = pool_both(x, N, C, H, W, 1, 1, H, W, 1, 1, 0, 0, 1, 1, ptype, lp, 1)
     np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("seed", range(32))
+def test_colpair_path_random(seed):
+    """Random shapes on the sixteen-lanes-per-plane path (2x2 / 3x3 window, stride 2
+    both ways, top / left padding 0 or 1, even rows of at most 32 elements, at most
+    16 x 16 outputs): plane counts that are not a multiple of 16, some output
+    sizes past the natural ones (windows wholly in the bottom / right padding),
+    every pool type and count_include_pad, full-range values."""
+    g = wl.rng(813, seed)
+    k = int(g.choice([2, 3]))
+    p = int(g.integers(0, 2))
+    W = 2 * int(g.integers(1, 17))
+    H = int(g.integers(1, 36))
+    OH = min((H + 2 * p - k) // 2 + 1 if H + 2 * p >= k else 1, 16)
+    OW = min((W + 2 * p - k) // 2 + 1 if W + 2 * p >= k else 1, 16)
+    if g.integers(0, 3) == 0:   # outputs past the natural size: windows in the padding
+        OH, OW = min(OH + int(g.integers(0, 3)), 16), min(OW + int(g.integers(0, 3)), 16)
+    OH, OW = max(OH, 1), max(OW, 1)
+    N, C = int(g.integers(1, 5)), int(g.integers(1, 40))
+    ptype, lp = [(0, 0), (1, 0), (2, 1), (2, 2), (3, 0), (2, 0)][int(g.integers(0, 6))]
+    cip = int(g.integers(0, 2)) if ptype == 1 else 0
+    say(f"pool colpair random seed {seed}: {(N, C, H, W, OH, OW, k, p, ptype, lp, cip)}")
+    x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
+    got, want = pool_both(x, N, C, H, W, OH, OW, k, k, 2, 2, p, p, 1, 1, ptype, lp, cip)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("ptype,lp,cip", [(0, 0, 0), (1, 0, 1), (1, 0, 0), (2, 2, 0), (2, 1, 0)])
+@pytest.mark.parametrize("k,p", [(3, 0), (3, 1), (2, 0), (2, 1)])
+def test_colpair_path_conv_b_size(ptype, lp, cip, k, p):
+    """The conv + pool block's 28x28 pools at full size ([32, 128, 28, 28], 4096
+    planes) on the sixteen-lanes-per-plane path, full-range values."""
+    N, C, H = 32, 128, 28
+    OH = (H + 2 * p - k) // 2 + 1
+    say(f"pool colpair 28x28 k={k} p={p} type={ptype} lp={lp} cip={cip}")
+    x = wl.rng(814, k, p, ptype, lp, cip).integers(-32768, 32768, N * C * H * H, dtype=np.int16)
+    got, want = pool_both(x, N, C, H, H, OH, OH, k, k, 2, 2, p, p, 1, 1, ptype, lp, cip)
+    np.testing.assert_array_equal(got, want)
