@@ -939,7 +939,11 @@ __device__ __forceinline__ uint32_t taps_inside(int32_t first, uint32_t n) {
     return (uint32_t)__builtin_elementwise_max(c, 0);
 }
 
-template <int KIND, int K, int P, int S>
+// MASK false: every window of an output inside [0, out_h) x [0, out_w) ends
+// inside the plane (host-checked), so only the top padding row needs the pad
+// value -- a left padding column is the DPP shift's edge value -- and rows or
+// columns past the plane feed only outputs that are not stored.
+template <int KIND, int K, int P, int S, bool MASK>
 __global__ __launch_bounds__(kThreads) void pool_colpair(const int16_t* __restrict__ x,
                                                          int16_t* __restrict__ y, PoolGeom g,
                                                          uint64_t planes, float inv_full) {
@@ -982,10 +986,14 @@ __global__ __launch_bounds__(kThreads) void pool_colpair(const int16_t* __restri
     constexpr uint32_t kPadPair = KIND == K_MAX ? 0x80008000u : 0u;
     const uint32_t col_m = 2u * j < g.in_w ? ~0u : 0u;
     uint32_t d[RR];
+    typedef __attribute__((address_space(3))) const uint32_t lds_u32;
+    lds_u32* lp = (lds_u32*)tl;   // 32-bit LDS address: one add per row
 #pragma unroll
-    for (int i = 0; i < RR; ++i) {
-        const uint32_t m = (uint32_t)(r0 + i) < g.in_h ? col_m : 0u;
-        d[i] = (tl[(uint32_t)i * pitch] & m) | (kPadPair & ~m);
+    for (int i = 0; i < RR; ++i, lp += pitch) {
+        uint32_t m;
+        if constexpr (MASK) m = (uint32_t)(r0 + i) < g.in_h ? col_m : 0u;
+        else m = i < P && part == 0 ? 0u : ~0u;   // only the top padding row
+        d[i] = (*lp & m) | (kPadPair & ~m);
     }
     // output offsets: the lane's first row and column (past the range when the
     // column is outside the plane), then one row step per output
@@ -1187,17 +1195,21 @@ int pool_launch(const int16_t* x, int16_t* y, uint64_t planes, const PoolGeom& g
         const uint32_t S = hw % 8 == 0 ? 4 : (hw % 4 == 0 ? 2 : 1);
         const uint64_t per_block = 4 * (4 / S);
         const dim3 grid((uint32_t)((planes + per_block - 1) / per_block)), block(kThreads);
-#define CM_COLPAIR(K_, P_, S_) \
-    hipLaunchKernelGGL((pool_colpair<KIND, K_, P_, S_>), grid, block, 0, s, x, y, g, planes, inv_full)
+        // windows of the last output row / column end inside the plane: no masks
+        const bool inside = 2ull * (g.out_h - 1) + kcp - 1 < (uint64_t)g.in_h + g.pt &&
+                            2ull * (g.out_w - 1) + kcp - 1 < (uint64_t)g.in_w + g.pl;
+#define CM_COLPAIR_M(K_, P_, S_) \
+    do { if (inside) hipLaunchKernelGGL((pool_colpair<KIND, K_, P_, S_, false>), grid, block, 0, s, x, y, g, planes, inv_full); \
+         else hipLaunchKernelGGL((pool_colpair<KIND, K_, P_, S_, true>), grid, block, 0, s, x, y, g, planes, inv_full); } while (0)
 #define CM_COLPAIR_S(K_, P_) \
-    do { if (S == 4) CM_COLPAIR(K_, P_, 4); else if (S == 2) CM_COLPAIR(K_, P_, 2); else CM_COLPAIR(K_, P_, 1); } while (0)
+    do { if (S == 4) CM_COLPAIR_M(K_, P_, 4); else if (S == 2) CM_COLPAIR_M(K_, P_, 2); else CM_COLPAIR_M(K_, P_, 1); } while (0)
         if (kcp == 3) {
             if (g.pt) CM_COLPAIR_S(3, 1); else CM_COLPAIR_S(3, 0);
         } else {
             if (g.pt) CM_COLPAIR_S(2, 1); else CM_COLPAIR_S(2, 0);
         }
 #undef CM_COLPAIR_S
-#undef CM_COLPAIR
+#undef CM_COLPAIR_M
         return cm_check_launch("pool_colpair");
     }
     // small planes: one wave per plane, the plane in LDS

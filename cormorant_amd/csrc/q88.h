@@ -113,7 +113,7 @@ __device__ __forceinline__ int16_t avg_finalize(uint32_t acc, float inv_denom) {
 }
 
 // Correctly rounded square root of x = 0 or a normal x (the LP accumulator's
-// float: 0 or at least 2^-16): the hardware estimate, within one ulp, moved to
+// raw value as a float: 0 or at least 1): the hardware estimate, within one ulp, moved to
 // the nearest float by the signs of the residuals x - n * s of its neighbours n
 // (the same correction LLVM's IEEE square root applies, without its rescaling
 // of subnormal inputs).  Negative x gives NaN.
@@ -126,13 +126,15 @@ __device__ __forceinline__ float sqrt_acc(float x) {
     return r;
 }
 
-// PoolingKernel.cpp:263, 265: AccData_t(sqrtf((float)acc)).  A non-negative
-// acc is below 2^31, so the root is at most 2^7.5; a negative (wrapped) sum's
-// root is NaN, which the reference's conversion takes to 0 (selected, not
-// branched: the pool kernels keep every load in flight past it).
+// PoolingKernel.cpp:263, 265: AccData_t(sqrtf((float)acc)), kept as floor(root *
+// 256) saturated.  With a = fl32(raw), sqrtf(a * 2^-16) * 256 = RN(sqrt(a)) exactly
+// (power-of-two scalings commute with the rounding), and a non-negative root is
+// floored by truncation; it reaches at most 46341, so only the top clamp applies.
+// A negative (wrapped) sum's root is NaN, which the reference's conversion takes
+// to 0 (selected, not branched: the pool kernels keep every load in flight past it).
 __device__ __forceinline__ int16_t lp2_finalize(uint32_t acc) {
-    const int16_t r = float_to_data(sqrt_acc(acc_to_float(acc)));
-    return (int32_t)acc < 0 ? (int16_t)0 : r;
+    const int32_t r = (int32_t)sqrt_acc((float)(int32_t)acc);   // NaN only when acc < 0
+    return (int32_t)acc < 0 ? (int16_t)0 : (int16_t)__builtin_elementwise_min(r, 32767);
 }
 
 }  // namespace q88
