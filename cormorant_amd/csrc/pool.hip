@@ -897,39 +897,48 @@ PlaneGeom plane_geom(const PoolGeom& g, uint32_t kw) {
 }
 
 // --------------------------------------------------------------- colpair --
-// Planes of at most 1024 elements with an even row length of at most 32 under a
-// K x K window (K = 2 or 3) at stride 2 in both directions, dilation 1 and equal
-// top and left padding P (0 or 1), at most 16 x 16 outputs: sixteen lanes per
-// group, S groups per plane (each taking 16 / S consecutive output rows), 4 / S
-// planes per wave, no per-output addressing.  The wave copies its planes into
-// LDS by 16-byte loads (per-row dword loads from memory were slower: four times
-// the load instructions, each touching four partial lines), then lane j of a
-// group reads input columns 2j and 2j + 1 of each row its outputs need as one
-// dword.  Output (oh, ow) sits on lane ow of the group holding row oh: its
-// window covers input rows 2oh - P .. 2oh - P + K - 1 and input columns
-// 2ow - P .. 2ow - P + K - 1, i.e. the lane's own pairs and at most one element
-// of a neighbouring lane, fetched with a DPP row shift (the 16-lane DPP row is
-// the group, so no shift crosses groups).  Positions outside the plane take the
-// pad value of the reduction before any arithmetic (-32768 for MAX, 0 for the
-// sums), which is the reference's treatment of a padded tap
-// (PoolingKernel.cpp:151-173, 197-212).  One plane per wave (S = 4) keeps many
-// small waves in flight, so early waves reduce and store while later waves'
-// loads still stream; S = 2 and 1 serve planes whose size keeps a single
+// Planes with an even row length under a K x K window (K = 2 or 3) at stride 2
+// in both directions, dilation 1 and equal top and left padding P (0 or 1):
+// GW lanes per group (16 for rows of at most 32 elements, 32 for at most 64), S
+// groups per plane (each taking RO consecutive output rows), 64 / GW / S planes
+// per wave, no per-output addressing.  The wave copies its planes into LDS by
+// 16-byte loads (per-row dword loads from memory were slower: four times the
+// load instructions, each touching four partial lines), then lane j of a group
+// reads input columns 2j and 2j + 1 of each row its outputs need as one dword.
+// Output (oh, ow) sits on lane ow of the group holding row oh: its window covers
+// input rows 2oh - P .. 2oh - P + K - 1 and input columns 2ow - P .. 2ow - P +
+// K - 1, i.e. the lane's own pairs and at most one element of a neighbouring
+// lane, fetched with a DPP shift (16 lanes: a row shift, whose 16-lane row is
+// the group; 32 lanes: a wave shift, its value replaced at the group's edge
+// lanes).  Positions outside the plane take the pad value of the reduction
+// before any arithmetic (-32768 for MAX, 0 for the sums), which is the
+// reference's treatment of a padded tap (PoolingKernel.cpp:151-173, 197-212).
+// One plane per wave (16 lanes: S = 4; 32 lanes: S = 2) keeps many small waves
+// in flight, so early waves reduce and store while later waves' loads still
+// stream; with 16 lanes, S = 2 and 1 serve planes whose size keeps a single
 // plane's start off 16-byte alignment.
-constexpr uint32_t kCpMaxOut = 16;   // output rows / columns per plane
-constexpr uint32_t kCpMaxHW = 1024;  // elements per plane (32 x 32)
-constexpr int kCpSlotWords = 4 * kCpMaxHW / 2;   // LDS dwords per wave: four planes at most
-// row reads reach one row (at most 16 dwords) before a wave's planes and, past
-// the last one, up to row 32 of the last plane's slot: front and back slack
-constexpr int kCpFront = 16;
-constexpr int kCpBack = 32 * 16 + 16;
-constexpr int kDppRowShl1 = 0x101;   // lane i reads lane i + 1 of its 16-lane row
-constexpr int kDppRowShr1 = 0x111;   // lane i reads lane i - 1
+template <int GW>
+struct CpShape {
+    static constexpr uint32_t kMaxHW = GW == 16 ? 1024u : 4096u;     // elements per plane
+    static constexpr uint32_t kMaxOutH = GW == 16 ? 16u : 28u;       // output rows per plane
+    static constexpr uint32_t kMaxIn = 2u * GW;                      // elements per input row
+    static constexpr int kFront = GW;   // LDS dwords before the slots: row -1 (at most GW dwords)
+};
+constexpr int kDppRowShl1 = 0x101;    // lane i reads lane i + 1 of its 16-lane row
+constexpr int kDppRowShr1 = 0x111;    // lane i reads lane i - 1
+constexpr int kDppWaveShl1 = 0x130;   // lane i reads lane i + 1 of the wave
+constexpr int kDppWaveShr1 = 0x138;   // lane i reads lane i - 1
 
-// The value lane i + 1 (SHL) or i - 1 holds; `pad` at the row's edge lane.
-template <bool SHL>
-__device__ __forceinline__ int32_t dpp_neighbour(int32_t v, int32_t pad) {
-    return __builtin_amdgcn_update_dpp(pad, v, SHL ? kDppRowShl1 : kDppRowShr1, 0xF, 0xF, false);
+// The value lane i + 1 (SHL) or i - 1 of the lane's GW-lane group holds; `pad`
+// at the group's edge lane (j: the lane's index in its group).
+template <int GW, bool SHL>
+__device__ __forceinline__ int32_t dpp_neighbour(int32_t v, int32_t pad, uint32_t j) {
+    if constexpr (GW == 16) {
+        return __builtin_amdgcn_update_dpp(pad, v, SHL ? kDppRowShl1 : kDppRowShr1, 0xF, 0xF, false);
+    } else {
+        const int32_t n = __builtin_amdgcn_update_dpp(pad, v, SHL ? kDppWaveShl1 : kDppWaveShr1, 0xF, 0xF, false);
+        return j == (SHL ? (uint32_t)GW - 1u : 0u) ? pad : n;
+    }
 }
 
 // Taps t < K with 0 <= first + t < n.
@@ -943,16 +952,17 @@ __device__ __forceinline__ uint32_t taps_inside(int32_t first, uint32_t n) {
 // inside the plane (host-checked), so only the top padding row needs the pad
 // value -- a left padding column is the DPP shift's edge value -- and rows or
 // columns past the plane feed only outputs that are not stored.
-template <int KIND, int K, int P, int S, bool MASK>
+template <int KIND, int K, int P, int GW, int S, bool MASK>
 __global__ __launch_bounds__(kThreads) void pool_colpair(const int16_t* __restrict__ x,
                                                          int16_t* __restrict__ y, PoolGeom g,
                                                          uint64_t planes, float inv_full) {
     typedef short v2s __attribute__((ext_vector_type(2)));
-    constexpr uint32_t PPW = 4 / S;                  // planes per wave
-    constexpr uint32_t RO = kCpMaxOut / S;           // output rows per lane group
+    using Sh = CpShape<GW>;
+    constexpr uint32_t PPW = 64u / GW / S;           // planes per wave
+    constexpr uint32_t RO = (Sh::kMaxOutH + S - 1) / S;   // output rows per lane group
     constexpr int RR = 2 * ((int)RO - 1) + K;        // input rows per lane
     touch_lines(g);
-    const uint32_t lane = threadIdx.x & 63, grp = lane >> 4, j = lane & 15;
+    const uint32_t lane = threadIdx.x & 63, grp = lane / GW, j = lane % GW;
     const uint32_t pl = grp / S, part = grp % S;      // plane in the wave, row part
     const uint64_t plane0 = ((uint64_t)blockIdx.x * (kThreads / 64) + wave_id()) * PPW;
     if (plane0 >= planes) return;   // the whole wave leaves
@@ -963,9 +973,13 @@ __global__ __launch_bounds__(kThreads) void pool_colpair(const int16_t* __restri
     // range-checked against the wave's planes
     const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + plane0 * hw, np * hw * 2u);
     const __amdgpu_buffer_rsrc_t ry = make_rsrc(y + plane0 * ohw, np * ohw * 2u);
-    constexpr int SLOT = kCpSlotWords / S;
-    __shared__ __align__(16) uint32_t tile[kCpFront + kThreads / 64 * SLOT + kCpBack];
-    uint32_t* t = tile + kCpFront + wave_id() * SLOT;
+    constexpr int SLOT = PPW * Sh::kMaxHW / 2;      // LDS dwords per wave
+    // row reads reach, from a slot's start, the last plane's row 2 RO S + K - 3
+    // (at most GW dwords each) and its column pair: past the last slot, slack
+    constexpr int REACH = ((int)PPW - 1) * (int)Sh::kMaxHW / 2 + (2 * (int)(RO * S) + K - 3) * GW + GW;
+    constexpr int BACK = REACH > SLOT ? REACH - SLOT : 0;
+    __shared__ __align__(16) uint32_t tile[Sh::kFront + kThreads / 64 * SLOT + BACK];
+    uint32_t* t = tile + Sh::kFront + wave_id() * SLOT;
     {
         constexpr int NV = SLOT / 4 / 64;   // 16-byte vectors per lane
         v4u v[NV];
@@ -1024,9 +1038,9 @@ __global__ __launch_bounds__(kThreads) void pool_colpair(const int16_t* __restri
                 if constexpr (K == 3) m = __builtin_elementwise_max(m, __builtin_bit_cast(v2s, r[2]));
                 const int32_t e0 = m[0], e1 = m[1];
                 int32_t v = __builtin_elementwise_max(e0, e1);
-                if constexpr (P == 0 && K == 3) v = __builtin_elementwise_max(v, dpp_neighbour<true>(e0, -32768));
+                if constexpr (P == 0 && K == 3) v = __builtin_elementwise_max(v, dpp_neighbour<GW, true>(e0, -32768, j));
                 if constexpr (P == 1 && K == 2) v = e0;
-                if constexpr (P == 1) v = __builtin_elementwise_max(v, dpp_neighbour<false>(e1, -32768));
+                if constexpr (P == 1) v = __builtin_elementwise_max(v, dpp_neighbour<GW, false>(e1, -32768, j));
                 out = v;
             } else {
                 uint32_t s;
@@ -1049,10 +1063,10 @@ __global__ __launch_bounds__(kThreads) void pool_colpair(const int16_t* __restri
                         c0 += term((int32_t)(int16_t)(r[tp] & 0xFFFFu));
                         c1 += term((int32_t)r[tp] >> 16);
                     }
-                    if constexpr (P == 0 && K == 3) s = c0 + c1 + (uint32_t)dpp_neighbour<true>((int32_t)c0, 0);
+                    if constexpr (P == 0 && K == 3) s = c0 + c1 + (uint32_t)dpp_neighbour<GW, true>((int32_t)c0, 0, j);
                     else if constexpr (P == 0) s = c0 + c1;
-                    else if constexpr (K == 3) s = c0 + c1 + (uint32_t)dpp_neighbour<false>((int32_t)c1, 0);
-                    else s = c0 + (uint32_t)dpp_neighbour<false>((int32_t)c1, 0);
+                    else if constexpr (K == 3) s = c0 + c1 + (uint32_t)dpp_neighbour<GW, false>((int32_t)c1, 0, j);
+                    else s = c0 + (uint32_t)dpp_neighbour<GW, false>((int32_t)c1, 0, j);
                 }
                 if constexpr (KIND == K_AVG) {
                     float inv = inv8_full;
@@ -1183,26 +1197,33 @@ int pool_launch(const int16_t* x, int16_t* y, uint64_t planes, const PoolGeom& g
                        g.pw < (1u << 10) && (uint64_t)g.out_w * g.sw < (1u << 30) &&
                        (uint64_t)g.out_h * g.sh < (1u << 30) &&
                        (uint64_t)g.in_h * g.in_w < (1u << 30);
-    // planes of at most 1024 elements, rows of at most 32, under a 2x2 / 3x3
-    // window at stride 2: sixteen lanes per plane, rows in registers (pool_colpair)
+    // planes under a 2x2 / 3x3 window at stride 2 with even rows of at most 32
+    // elements (16-lane groups) or 64 (32-lane groups, one plane per wave): rows
+    // in registers (pool_colpair)
     const uint32_t kcp = g.ph == g.pw && (g.ph == 2 || g.ph == 3) ? g.ph : 0;
-    if (kcp && g.sh == 2 && g.sw == 2 && g.dh == 1 && g.dw == 1 && g.pt == g.pl && g.pt <= 1 &&
-        g.in_w % 2 == 0 && g.in_w <= 32 && (uint64_t)g.in_h * g.in_w <= kCpMaxHW &&
-        g.out_h <= kCpMaxOut && g.out_w <= kCpMaxOut && ((uintptr_t)x & 15u) == 0 &&
-        (planes + 15) / 16 <= 0x7FFFFFFFull) {
-        // one plane per wave when a plane's start stays 16-byte aligned, else two or four
-        const uint64_t hw = (uint64_t)g.in_h * g.in_w;
-        const uint32_t S = hw % 8 == 0 ? 4 : (hw % 4 == 0 ? 2 : 1);
-        const uint64_t per_block = 4 * (4 / S);
+    const uint64_t hw = (uint64_t)g.in_h * g.in_w;
+    const bool cp_geom = kcp && g.sh == 2 && g.sw == 2 && g.dh == 1 && g.dw == 1 && g.pt == g.pl &&
+                         g.pt <= 1 && g.in_w % 2 == 0 && ((uintptr_t)x & 15u) == 0;
+    const bool cp16 = cp_geom && g.in_w <= CpShape<16>::kMaxIn && hw <= CpShape<16>::kMaxHW &&
+                      g.out_h <= CpShape<16>::kMaxOutH && g.out_w <= 16u;
+    const bool cp32 = !cp16 && cp_geom && hw % 8 == 0 && g.in_w <= CpShape<32>::kMaxIn &&
+                      hw <= CpShape<32>::kMaxHW && g.out_h <= CpShape<32>::kMaxOutH && g.out_w <= 32u;
+    if ((cp16 || cp32) && (planes + 3) / 4 <= 0x7FFFFFFFull) {
+        // 16 lanes: one plane per wave when a plane's start stays 16-byte aligned,
+        // else two or four
+        const uint32_t S = cp32 ? 2u : hw % 8 == 0 ? 4u : (hw % 4 == 0 ? 2u : 1u);
+        const uint64_t per_block = 4 * (64 / (cp32 ? 32 : 16) / S);
         const dim3 grid((uint32_t)((planes + per_block - 1) / per_block)), block(kThreads);
         // windows of the last output row / column end inside the plane: no masks
         const bool inside = 2ull * (g.out_h - 1) + kcp - 1 < (uint64_t)g.in_h + g.pt &&
                             2ull * (g.out_w - 1) + kcp - 1 < (uint64_t)g.in_w + g.pl;
-#define CM_COLPAIR_M(K_, P_, S_) \
-    do { if (inside) hipLaunchKernelGGL((pool_colpair<KIND, K_, P_, S_, false>), grid, block, 0, s, x, y, g, planes, inv_full); \
-         else hipLaunchKernelGGL((pool_colpair<KIND, K_, P_, S_, true>), grid, block, 0, s, x, y, g, planes, inv_full); } while (0)
+#define CM_COLPAIR_M(K_, P_, GW_, S_) \
+    do { if (inside) hipLaunchKernelGGL((pool_colpair<KIND, K_, P_, GW_, S_, false>), grid, block, 0, s, x, y, g, planes, inv_full); \
+         else hipLaunchKernelGGL((pool_colpair<KIND, K_, P_, GW_, S_, true>), grid, block, 0, s, x, y, g, planes, inv_full); } while (0)
 #define CM_COLPAIR_S(K_, P_) \
-    do { if (S == 4) CM_COLPAIR_M(K_, P_, 4); else if (S == 2) CM_COLPAIR_M(K_, P_, 2); else CM_COLPAIR_M(K_, P_, 1); } while (0)
+    do { if (cp32) CM_COLPAIR_M(K_, P_, 32, 2); \
+         else if (S == 4) CM_COLPAIR_M(K_, P_, 16, 4); else if (S == 2) CM_COLPAIR_M(K_, P_, 16, 2); \
+         else CM_COLPAIR_M(K_, P_, 16, 1); } while (0)
         if (kcp == 3) {
             if (g.pt) CM_COLPAIR_S(3, 1); else CM_COLPAIR_S(3, 0);
         } else {

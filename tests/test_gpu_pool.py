@@ -211,3 +211,46 @@ def test_colpair_path_conv_b_size(ptype, lp, cip, k, p):
     x = wl.rng(814, k, p, ptype, lp, cip).integers(-32768, 32768, N * C * H * H, dtype=np.int16)
     got, want = pool_both(x, N, C, H, H, OH, OH, k, k, 2, 2, p, p, 1, 1, ptype, lp, cip)
     np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_colpair32_path_random(seed):
+    """Random shapes on the 32-lanes-per-row-group path (rows of 34-64 elements,
+    planes of at most 4096 elements a multiple of 8, at most 28 output rows and 32
+    columns): 2x2 / 3x3 windows at stride 2, padding 0 or 1, some output sizes past
+    the natural ones, plane counts not a multiple of 4, every pool type, full-range
+    values.  Shapes outside the path (a plane size not a multiple of 8) check the
+    path they take instead."""
+    g = wl.rng(815, seed)
+    k = int(g.choice([2, 3]))
+    p = int(g.integers(0, 2))
+    W = 2 * int(g.integers(17, 33))
+    H = int(g.integers(1, min(57, 4096 // W + 1)))
+    if g.integers(0, 4):
+        H -= H % 4   # plane size a multiple of 8 (W even)
+        H = max(H, 4)
+    OH = min((H + 2 * p - k) // 2 + 1 if H + 2 * p >= k else 1, 28)
+    OW = min((W + 2 * p - k) // 2 + 1, 32)
+    if g.integers(0, 3) == 0:
+        OH, OW = min(OH + int(g.integers(0, 3)), 28), min(OW + int(g.integers(0, 3)), 32)
+    OH, OW = max(OH, 1), max(OW, 1)
+    N, C = int(g.integers(1, 4)), int(g.integers(1, 20))
+    ptype, lp = [(0, 0), (1, 0), (2, 1), (2, 2), (3, 0), (2, 0)][int(g.integers(0, 6))]
+    cip = int(g.integers(0, 2)) if ptype == 1 else 0
+    say(f"pool colpair32 random seed {seed}: {(N, C, H, W, OH, OW, k, p, ptype, lp, cip)}")
+    x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
+    got, want = pool_both(x, N, C, H, W, OH, OW, k, k, 2, 2, p, p, 1, 1, ptype, lp, cip)
+    np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("ptype,lp,cip", [(0, 0, 0), (1, 0, 1), (1, 0, 0), (2, 2, 0), (2, 1, 0)])
+@pytest.mark.parametrize("k,p", [(3, 0), (3, 1), (2, 0), (2, 1)])
+def test_colpair32_path_conv_a_size(ptype, lp, cip, k, p):
+    """The conv + pool block's 56x56 pools at full size ([32, 128, 56, 56], 4096
+    planes) on the 32-lanes-per-row-group path, full-range values."""
+    N, C, H = 32, 128, 56
+    OH = (H + 2 * p - k) // 2 + 1
+    say(f"pool colpair32 56x56 k={k} p={p} type={ptype} lp={lp} cip={cip}")
+    x = wl.rng(816, k, p, ptype, lp, cip).integers(-32768, 32768, N * C * H * H, dtype=np.int16)
+    got, want = pool_both(x, N, C, H, H, OH, OH, k, k, 2, 2, p, p, 1, 1, ptype, lp, cip)
+    np.testing.assert_array_equal(got, want)
