@@ -46,22 +46,28 @@ __device__ __forceinline__ int32_t sub(int32_t a, int32_t b) { return sat16(a - 
 __device__ __forceinline__ int32_t mul(int32_t a, int32_t b) { return sat16((a * b) >> 8); }
 
 // VectorOP.cpp:22-25: b == 0 -> 0, else sat16(trunc((a * 256) / b)).
-// The quotient estimate comes from v_rcp_f32 (relative error ~2^-23) and is
-// clamped to +-40000 (saturation is decided well outside that band); inside
-// the band the estimate is within 0.01 of the exact quotient, so one integer
-// remainder check moves it onto trunc(A/b) exactly.  Verified exhaustively
-// over all 2^32 (a, b) pairs against integer division.
+// Branch-free in float: A = 256 a and b are exact floats; the estimate
+// A * rcp(b) (v_rcp_f32, relative error ~2^-23) is clamped to +-40000
+// (saturation is decided well outside that band) and truncated to q0, which is
+// then within one of trunc(A / b).  The remainder r = A - q0 b comes from one
+// FMA, exact when |q0| < 40000 (|r| < 2 |b|, an integer); q0 moves one step
+// toward zero when r has the sign opposite to A (it overshot) and one step
+// away from zero, in the quotient's direction, when |r| >= |b| (it fell
+// short) -- the two cannot both hold.  Clamped estimates only need the result
+// to stay beyond the saturation bound, which they do.  Verified exhaustively
+// over all 2^32 (a, b) pairs against exact integer division.
 __device__ __forceinline__ int32_t div(int32_t a, int32_t b) {
-    if (b == 0) return 0;
-    const int32_t A = a * 256;
-    float qf = (float)A * __builtin_amdgcn_rcpf((float)b);
-    qf = __builtin_fminf(__builtin_fmaxf(qf, -40000.0f), 40000.0f);
-    int32_t q = (int32_t)qf;                      // truncation toward zero
-    const int32_t r = A - q * b;                  // |q * b| < 2^31
-    const int32_t s = ((A ^ b) < 0) ? -1 : 1;     // sign of the true quotient
-    if (r != 0 && ((r ^ A) < 0)) q -= s;          // overshot past trunc(A/b)
-    else if (__builtin_abs(r) >= __builtin_abs(b)) q += s;   // undershot
-    return sat16(q);
+    const float fa = (float)a * 256.0f, fb = (float)b;
+    const float t = __builtin_amdgcn_fmed3f(fa * __builtin_amdgcn_rcpf(fb), -40000.0f, 40000.0f);
+    const float q0 = __builtin_truncf(t);
+    const float r = __builtin_fmaf(-q0, fb, fa);
+    const float s = __builtin_copysignf(1.0f, fa * fb);   // the quotient's sign (A != 0)
+    const float over = r * fa < 0.0f ? s : 0.0f;
+    const float under = __builtin_fabsf(r) >= __builtin_fabsf(fb) ? s : 0.0f;
+    const int32_t q = (int32_t)(q0 + (under - over));
+    // b == 0 gives 0 through a mask, not a select (which became a branch around
+    // the whole computation)
+    return sat16(q) & -(int32_t)(b != 0);
 }
 
 // VectorOP.cpp:27-35
