@@ -1055,7 +1055,7 @@ int launch_gemm(GemmArgs& g0, uint32_t zdim, const LaunchCtx& lc, const char* na
 }  // namespace
 
 int cm_matmul_rk_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k, uint32_t m,
-                        const cm_epilogue_t* epi, const LaunchCtx& lc);
+                        uint32_t lda, uint32_t ldc, const cm_epilogue_t* epi, const LaunchCtx& lc);
 int cm_gemm_dma_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k,
                        uint32_t m, uint32_t batch, uint32_t a_bs, uint32_t b_bs, uint32_t c_bs,
                        const cm_epilogue_t* epi, const LaunchCtx& lc);
@@ -1083,7 +1083,15 @@ int cm_matmul_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n,
     // one small product: the register-only kernel, the reduction split over a
     // block's waves (matmul_rk.hip)
     if (batch == 1) {
-        const int rc = cm_matmul_rk_launch(g.a, g.b, g.c, n, k, m, epi, lc);
+        const int rc = cm_matmul_rk_launch(g.a, g.b, g.c, n, k, m, k, m, epi, lc);
+        if (rc != 1) return rc;
+    }
+    // a batch of single-row products sharing one B (the scheduler's row-strided
+    // form of a product whose output rows are padded, nodes.py:785-801) is one
+    // product of `batch` rows, A rows a_bs apart and C rows c_bs apart, when no
+    // two batches' outputs overlap
+    if (batch > 1 && n == 1 && b_bs == 0 && a_bs >= k && c_bs >= m) {
+        const int rc = cm_matmul_rk_launch(a, b, c, batch, k, m, a_bs, c_bs, epi, lc);
         if (rc != 1) return rc;
     }
     // large products with a workspace for the packed B: operands streamed into

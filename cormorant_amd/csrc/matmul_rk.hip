@@ -47,6 +47,7 @@ struct MrArgs {
     int16_t* c;
     EpiArgs epi;
     uint32_t n, k, m;
+    uint32_t lda, ldc;          // elements between rows of A and of C (and of a same-shaped Add)
     uint32_t rt, nk;            // row tiles of 32, k steps of 64
     uint32_t a_bytes, b_bytes, c_bytes;
 };
@@ -108,7 +109,7 @@ __global__ __launch_bounds__(64 * NW) void matmul_rk(MrArgs g) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
         const uint32_t r = rt * 32u + i * 16u + r16;
-        arow[i] = r < g.n ? r * g.k * 2u : kOob;
+        arow[i] = r < g.n ? r * g.lda * 2u : kOob;
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -127,7 +128,7 @@ __global__ __launch_bounds__(64 * NW) void matmul_rk(MrArgs g) {
             const uint32_t v = U * wave + u, i = v >> 3, e = (v >> 1) & 3u, j = v & 1u;
             const uint32_t r = rt * 32u + i * 16u + kg * 4u + e;
             const bool ok = r < g.n && col[j] < g.m;
-            const uint32_t el = g.epi.add_mode == 1u ? r * g.m + col[j] : col[j];
+            const uint32_t el = g.epi.add_mode == 1u ? r * g.ldc + col[j] : col[j];
             fadd[u] = __builtin_amdgcn_raw_buffer_load_b16(xr, ok ? el * 2u : kOob, 0, 0);
         }
     }
@@ -222,30 +223,35 @@ __global__ __launch_bounds__(64 * NW) void matmul_rk(MrArgs g) {
         if (r >= g.n || col[j] >= g.m) continue;
         int32_t o = q88::acc_to_data(acc);
         if (g.epi.add_mode != 0u) o = q88::add(o, (int16_t)fadd[u]);
-        g.c[r * g.m + col[j]] = (int16_t)q88::clamp(o, lo, hi);
+        g.c[r * g.ldc + col[j]] = (int16_t)q88::clamp(o, lo, hi);
     }
 }
 
 }  // namespace
 
 // Returns 1 when the shape is not for this path (the caller takes the block GEMM).
+// Rows of A lie lda elements apart and rows of C (and of a same-shaped Add) ldc
+// apart: a batch of single-row products whose B is shared is one product here.
 int cm_matmul_rk_launch(const int16_t* a, const int16_t* b, int16_t* c, uint32_t n, uint32_t k, uint32_t m,
-                        const cm_epilogue_t* epi, const LaunchCtx& lc) {
+                        uint32_t lda, uint32_t ldc, const cm_epilogue_t* epi, const LaunchCtx& lc) {
     const uint64_t out = (uint64_t)n * m;
     if (n == 0 || m == 0 || k == 0 || out > kMrMaxOut || (k + 63u) / 64u > kMrMaxSteps) return 1;
-    if (2ull * n * k >= 0x80000000ull || 2ull * k * m >= 0x80000000ull) return 1;
+    if (lda < k || ldc < m) return 1;
+    const uint64_t a_span = 2ull * ((uint64_t)(n - 1) * lda + k), c_span = 2ull * ((uint64_t)(n - 1) * ldc + m);
+    if (a_span >= 0x80000000ull || 2ull * k * m >= 0x80000000ull || c_span >= 0x80000000ull) return 1;
     if (lc.need) return CM_OK;   // no workspace
     MrArgs g{};
     g.a = a; g.b = b; g.c = c; g.epi = cm_epi_args(epi);
     g.n = n; g.k = k; g.m = m;
+    g.lda = lda; g.ldc = ldc;
     g.rt = (n + 31) / 32;
     g.nk = (k + 63) / 64;
-    g.a_bytes = (uint32_t)(2ull * n * k);
+    g.a_bytes = (uint32_t)a_span;
     g.b_bytes = (uint32_t)(2ull * k * m);
-    g.c_bytes = (uint32_t)(2ull * out);
+    g.c_bytes = (uint32_t)c_span;
     const dim3 grid((uint32_t)((uint64_t)g.rt * ((m + 31) / 32)));
     // eight waves when there are eight or more k steps: each walks half as many
-    const bool av = k % 8 == 0 && ((uintptr_t)a & 15u) == 0;
+    const bool av = k % 8 == 0 && lda % 8 == 0 && ((uintptr_t)a & 15u) == 0;
     if (g.nk >= 8) {
         if (av) hipLaunchKernelGGL((matmul_rk<true, 8>), grid, dim3(512), 0, lc.s, g);
         else hipLaunchKernelGGL((matmul_rk<false, 8>), grid, dim3(512), 0, lc.s, g);

@@ -138,3 +138,43 @@ def test_conv_epilogue_in_place_add():
     buf = dev(res)
     K.ConvKernel(dev(x), dev(w), dev(bias), buf, *args, add=buf, act=K.ACT_RELU6)
     np.testing.assert_array_equal(host(buf), apply_epilogue(y, res, False, K.ACT_RELU6, 0, 0))
+
+
+ROWS_CASES = [
+    # batch, k, m, a_bs, c_bs, add mode, act: single-row products sharing B (one
+    # product on the register-only kernel, A rows a_bs apart, C rows c_bs apart)
+    (64, 256, 10, 256, 16, "column", K.ACT_NONE),
+    (100, 784, 33, 792, 40, "same", K.ACT_RELU),
+    (7, 72, 1, 72, 3, None, K.ACT_RELU6),
+    (300, 128, 64, 136, 64, "column", K.ACT_RELU6),
+    (33, 20, 17, 24, 17, "same", K.ACT_NONE),
+    (5, 1000, 200, 1000, 256, None, K.ACT_NONE),
+]
+
+
+@pytest.mark.parametrize("case", ROWS_CASES, ids=[str(c[:5]) for c in ROWS_CASES])
+def test_matmul_single_row_batches(case):
+    """Batches of single-row products with a shared B and padded output rows, with
+    and without the fused Add / activation, full-range operands (sums wrap):
+    each written row equals the oracle's MatMul followed by the unfused VectorOP
+    calls, and the padding between rows keeps its contents."""
+    batch, k, m, a_bs, c_bs, mode, act = case
+    say(f"matmul single-row batches {case}")
+    g = wl.rng(904, *case[:5])
+    a = full_range(g, (batch - 1) * a_bs + k)
+    b = full_range(g, k * m)
+    c_len = (batch - 1) * c_bs + m
+    add = None if mode is None else full_range(g, m if mode == "column" else c_len)
+    fill = np.full(c_len, 0x5A5A, np.int16)
+    c = dev(fill)
+    K.MatmulKernel(dev(a), dev(b), c, 1, k, m, batch, a_bs, 0, c_bs,
+                   add=None if add is None else dev(add), add_column=mode == "column", act=act)
+    y = fill.copy()
+    oracle.set_threads(oracle_threads())
+    oracle.matmul(a, b, y, 1, k, m, batch, a_bs, 0, c_bs, threads=True)
+    want = y.copy()
+    for r in range(batch):
+        row = y[r * c_bs: r * c_bs + m].copy()
+        radd = None if add is None else (add if mode == "column" else add[r * c_bs: r * c_bs + m])
+        want[r * c_bs: r * c_bs + m] = apply_epilogue(row, radd, False, act, 1, m)
+    np.testing.assert_array_equal(host(c), want)
