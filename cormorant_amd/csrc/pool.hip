@@ -78,6 +78,35 @@ __device__ __forceinline__ int32_t valid_taps(int32_t base, int32_t k, int32_t d
 // registers, and every buffer load through it becomes a read-first-lane loop.
 __device__ __forceinline__ uint32_t wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
+// Merges of Acc values across lanes by DPP: row16_reduce leaves each 16-lane
+// row's merge in the row's last lane (row shifts by 1, 2, 4 and 8, the row's
+// first lanes taking the merge's identity); wave_reduce merges the four row
+// results read out with readlane (scalar, no LDS round trips).
+template <int KIND>
+__device__ __forceinline__ uint32_t acc_merge(uint32_t a, uint32_t b) {
+    Acc<KIND> t;
+    t.v = a;
+    t.merge(b);
+    return t.v;
+}
+template <int KIND>
+__device__ __forceinline__ uint32_t row16_reduce(uint32_t v) {
+    constexpr int kId = KIND == K_MAX ? (int)0x80000000u : 0;
+    v = acc_merge<KIND>(v, (uint32_t)__builtin_amdgcn_update_dpp(kId, (int)v, 0x111, 0xF, 0xF, false));
+    v = acc_merge<KIND>(v, (uint32_t)__builtin_amdgcn_update_dpp(kId, (int)v, 0x112, 0xF, 0xF, false));
+    v = acc_merge<KIND>(v, (uint32_t)__builtin_amdgcn_update_dpp(kId, (int)v, 0x114, 0xF, 0xF, false));
+    v = acc_merge<KIND>(v, (uint32_t)__builtin_amdgcn_update_dpp(kId, (int)v, 0x118, 0xF, 0xF, false));
+    return v;
+}
+template <int KIND>
+__device__ __forceinline__ uint32_t wave_reduce(uint32_t v) {
+    v = row16_reduce<KIND>(v);
+    uint32_t t = (uint32_t)__builtin_amdgcn_readlane((int)v, 15);
+    t = acc_merge<KIND>(t, (uint32_t)__builtin_amdgcn_readlane((int)v, 31));
+    t = acc_merge<KIND>(t, (uint32_t)__builtin_amdgcn_readlane((int)v, 47));
+    return acc_merge<KIND>(t, (uint32_t)__builtin_amdgcn_readlane((int)v, 63));
+}
+
 // ---------------------------------------------------------------- global --
 // One wavefront per plane, NB 16-byte loads per lane in flight (NB fitted to the
 // plane on the host: 1, 2, 4, or 8 repeated).  Each 16-byte vector (8 values, 4
@@ -150,10 +179,38 @@ __global__ __launch_bounds__(kThreads) void pool_global(const int16_t* __restric
     }
     for (uint32_t i = done + lane; i < hw; i += 64) r.add_one(xp[i]);
     Acc<KIND> a;
-    a.v = r.acc();
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) a.merge((uint32_t)__shfl_xor((int)a.v, off, 64));
+    a.v = wave_reduce<KIND>(r.acc());
     if (lane == 0) y[plane] = a.finish(inv);
+}
+
+// Small planes (at most 16 * NL elements, e.g. a 7x7 GlobalAveragePool): sixteen
+// lanes per plane, four planes per wave, NL two-byte loads per lane (all issued
+// before any is used; positions past the plane take the pad value), the sixteen
+// lanes' accumulators merged by DPP row shifts, and the group's last lane
+// finishes its plane.
+template <int KIND, int NL>
+__global__ __launch_bounds__(kThreads) void pool_gsmall(const int16_t* __restrict__ x,
+                                                        int16_t* __restrict__ y, uint64_t planes,
+                                                        uint32_t hw, float inv) {
+    const uint32_t lane = threadIdx.x & 63, grp = lane >> 4, j = lane & 15;
+    const uint64_t plane0 = ((uint64_t)blockIdx.x * (kThreads / 64) + wave_id()) * 4;
+    if (plane0 >= planes) return;
+    const uint32_t np = (uint32_t)(planes - plane0 < 4 ? planes - plane0 : 4);
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + plane0 * hw, np * hw * 2u);
+    uint32_t v[NL];
+#pragma unroll
+    for (int u = 0; u < NL; ++u) {
+        const uint32_t e = j + 16u * u;
+        v[u] = __builtin_amdgcn_raw_buffer_load_b16(rx, e < hw ? (grp * hw + e) * 2u : kOob, 0, kNonTemporal);
+    }
+    Acc<KIND> a;
+#pragma unroll
+    for (int u = 0; u < NL; ++u) {
+        const uint32_t e = j + 16u * u;
+        a.add(e < hw ? (int32_t)(int16_t)v[u] : Acc<KIND>::kPad);
+    }
+    a.v = row16_reduce<KIND>(a.v);
+    if (j == 15u && grp < np) y[plane0 + grp] = a.finish(inv);
 }
 
 // ------------------------------------------------------------------ band --
@@ -1178,6 +1235,15 @@ int pool_launch(const int16_t* x, int16_t* y, uint64_t planes, const PoolGeom& g
         // loads per lane in flight fitted to the plane's 16-byte vectors
         const uint64_t per_lane = (hw / 8 + 63) / 64;
         const float inv_hw = host_inv_denom(hw);
+        if (hw <= 128) {   // small planes: sixteen lanes each
+            const dim3 grid((uint32_t)((planes + 15) / 16)), block(kThreads);
+            if ((planes + 15) / 16 > 0x7FFFFFFFull) return cm_set_error(CM_ERR_RANGE, "pool: too many planes");
+            if (hw <= 16) hipLaunchKernelGGL((pool_gsmall<KIND, 1>), grid, block, 0, s, x, y, planes, (uint32_t)hw, inv_hw);
+            else if (hw <= 32) hipLaunchKernelGGL((pool_gsmall<KIND, 2>), grid, block, 0, s, x, y, planes, (uint32_t)hw, inv_hw);
+            else if (hw <= 64) hipLaunchKernelGGL((pool_gsmall<KIND, 4>), grid, block, 0, s, x, y, planes, (uint32_t)hw, inv_hw);
+            else hipLaunchKernelGGL((pool_gsmall<KIND, 8>), grid, block, 0, s, x, y, planes, (uint32_t)hw, inv_hw);
+            return cm_check_launch("pool_gsmall");
+        }
 #define CM_POOL_GLOBAL(NB)                                                                       \
     hipLaunchKernelGGL((pool_global<KIND, NB>), dim3((uint32_t)blocks), dim3(kThreads), 0, s, x, y, \
                        planes, (uint32_t)hw, inv_hw, vec_ok)

@@ -254,3 +254,21 @@ def test_colpair32_path_conv_a_size(ptype, lp, cip, k, p):
     x = wl.rng(816, k, p, ptype, lp, cip).integers(-32768, 32768, N * C * H * H, dtype=np.int16)
     got, want = pool_both(x, N, C, H, H, OH, OH, k, k, 2, 2, p, p, 1, 1, ptype, lp, cip)
     np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_global_pool_random(seed):
+    """Global pools (window = plane) over random plane sizes: the sixteen-lanes-per-
+    plane kernel (at most 128 elements) and the wave-per-plane kernel (planes that
+    are and are not multiples of 8), plane counts not a multiple of 16, every pool
+    type, full-range values."""
+    g = wl.rng(817, seed)
+    H = int(g.integers(1, 12 if seed < 12 else 40))
+    W = int(g.integers(1, 12 if seed < 12 else 40))
+    N, C = int(g.integers(1, 5)), int(g.integers(1, 70))
+    ptype, lp = [(0, 0), (1, 0), (2, 1), (2, 2), (3, 0), (2, 0)][int(g.integers(0, 6))]
+    cip = int(g.integers(0, 2)) if ptype == 1 else 0
+    say(f"global pool random seed {seed}: {(N, C, H, W, ptype, lp, cip)}")
+    x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
+    got, want = pool_both(x, N, C, H, W, 1, 1, H, W, 1, 1, 0, 0, 1, 1, ptype, lp, cip)
+    np.testing.assert_array_equal(got, want)
