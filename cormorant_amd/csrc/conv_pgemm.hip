@@ -602,44 +602,50 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
     a_load8(0, fa_h[0]);
     if constexpr (NS == 3) a_load8(ks_plus(0, 1), fa_h[1]);
 
+    // The first chunk's patch (without MULTI: every chunk, staged once for every
+    // sub-tile), before the accumulators of a sub-tile are live.  Without MULTI
+    // this runs once ahead of the sub-tile loop: the staging loop's addresses then
+    // die before the k loop instead of living (and being spilled) across it, and
+    // their reloads cannot make the staging loads wait for the A fragments'.
+    auto stage_first = [&](uint32_t sub) {
+        if (sub) __syncthreads();   // every wave is done with the previous patch and q table
+        stage_patch(0u, MULTI ? 4u : g.cpt_all);
+        build_qtab(MULTI ? 4u : g.cpt_last, MULTI ? g.div_cpt4 : g.div_cpt_last, MULTI ? 0u : g.nfull);
+        if (sub == 0) {
+            // the prologue's loads are used from here on: the empty asm keeps
+            // the compiler from computing with them (and so waiting for them)
+            // ahead of the patch loads
+            uint32_t wsum = ld_wsum, bias = ld_bias, fit = ld_fit;
+            uint32_t wsum2 = ld_wsum2, bias2 = ld_bias2, fit2 = ld_fit2;
+            asm volatile("" : "+v"(wsum), "+v"(bias), "+v"(fit), "+v"(wsum2), "+v"(bias2), "+v"(fit2));
+            const bool real = row0 + tid < g.M;
+            if (tid < TB) rowterm_s[tid] = real ? 128u * wsum + (uint32_t)(int32_t)(int16_t)bias * 256u : 0u;
+            if constexpr (PAIR) {
+                if (tid < ((g.M2 + 31u) & ~31u))
+                    reinterpret_cast<uint32_t*>(lds + g.rt2_off)[tid] =
+                        tid < g.M2 ? 128u * wsum2 + (uint32_t)(int32_t)(int16_t)bias2 * 256u : 0u;
+                fast2 = __syncthreads_and(tid >= g.M2 || fit2 != 0u) != 0;
+            }
+            fast = __syncthreads_and(tid >= TB || !real || fit != 0u) != 0;
+            if (!fast) {
+                a_load(0, fa_h[0], fa_l[0]);
+                if constexpr (NS == 3) a_load(ks_plus(0, 1), fa_h[1], fa_l[1]);
+            }
+        } else {
+            __syncthreads();
+        }
+        if (!fast) {   // the column term's position sums
+            pos_sums(MULTI ? 4u : g.cpt_all);
+            __syncthreads();
+        }
+    };
+    if constexpr (!MULTI) stage_first(0u);
+
     for (uint32_t sub = 0; sub < nsub; ++sub) {
         const uint32_t p0 = pb + sub * SPX + wc * 64u;      // this wave's first pixel of the sub-tile
         const uint32_t pn = p0 < pe ? min(64u, pe - p0) : 0u;   // the wave's pixels of this sub-tile
         const uint32_t nj = (pn + 15u) / 16u;              // 16-pixel column tiles in use (0 - 4)
-        // the first chunk's patch (without MULTI: every chunk, staged once for
-        // every sub-tile), before the accumulators of this sub-tile are live
-        if (sub == 0 || MULTI) {
-            if (sub) __syncthreads();   // every wave is done with the previous patch and q table
-            stage_patch(0u, MULTI ? 4u : g.cpt_all);
-            build_qtab(MULTI ? 4u : g.cpt_last, MULTI ? g.div_cpt4 : g.div_cpt_last, MULTI ? 0u : g.nfull);
-            if (sub == 0) {
-                // the prologue's loads are used from here on: the empty asm keeps
-                // the compiler from computing with them (and so waiting for them)
-                // ahead of the patch loads
-                uint32_t wsum = ld_wsum, bias = ld_bias, fit = ld_fit;
-                uint32_t wsum2 = ld_wsum2, bias2 = ld_bias2, fit2 = ld_fit2;
-                asm volatile("" : "+v"(wsum), "+v"(bias), "+v"(fit), "+v"(wsum2), "+v"(bias2), "+v"(fit2));
-                const bool real = row0 + tid < g.M;
-                if (tid < TB) rowterm_s[tid] = real ? 128u * wsum + (uint32_t)(int32_t)(int16_t)bias * 256u : 0u;
-                if constexpr (PAIR) {
-                    if (tid < ((g.M2 + 31u) & ~31u))
-                        reinterpret_cast<uint32_t*>(lds + g.rt2_off)[tid] =
-                            tid < g.M2 ? 128u * wsum2 + (uint32_t)(int32_t)(int16_t)bias2 * 256u : 0u;
-                    fast2 = __syncthreads_and(tid >= g.M2 || fit2 != 0u) != 0;
-                }
-                fast = __syncthreads_and(tid >= TB || !real || fit != 0u) != 0;
-                if (!fast) {
-                    a_load(0, fa_h[0], fa_l[0]);
-                    if constexpr (NS == 3) a_load(ks_plus(0, 1), fa_h[1], fa_l[1]);
-                }
-            } else {
-                __syncthreads();
-            }
-            if (!fast) {   // the column term's position sums
-                pos_sums(MULTI ? 4u : g.cpt_all);
-                __syncthreads();
-            }
-        }
+        if constexpr (MULTI) stage_first(sub);
         // patch position of the window origin of this lane's pixel in each column
         // tile (row (oh - oh_a) * S', column ow * S') and its byte offset
         uint32_t ppos[4], pbase[4];
