@@ -76,6 +76,7 @@ struct PgArgs {
     uint32_t L, rpi, rpi_n;      // output pixels per block; ranges per image; ranges per row tile
     FastDiv div_npr, div_nbm, div_rpi, div_ow, div_npos, div_pw, div_nv, div_prows, div_nh, div_kw, div_cpt4, div_cpt_last, div_t4;
     uint32_t vw;                 // output / Add access width in elements (8 or 1)
+    uint32_t add_w4;             // Add runs 4-byte aligned (P even, operand 4-byte aligned)
     uint32_t x_img_bytes, pk_bytes;   // pk_bytes: both packed layouts (limb planes, then int8)
     uint32_t pk8_off;            // byte offset of the int8 plane
     uint64_t x_img, y_img;
@@ -254,7 +255,8 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
             touch ^= reinterpret_cast<const uint32_t*>(&g)[i * 16];
         asm volatile("" ::"s"(touch));
     }
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t tid = threadIdx.x, wave = tid >> 6;
+    uint32_t lane = tid & 63;   // made opaque after each k loop (see there)
     int16_t* et = reinterpret_cast<int16_t*>(lds + g.epi_off + wave * kEpiBytes);
     // Workgroups are dealt to the 8 XCDs round robin; block b of XCD x takes the
     // x-th contiguous share of the (row tile, image, range) order, so ranges
@@ -506,13 +508,67 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
     const uint32_t kp_term = 16384u * 64u * g.steps;
     const int32_t lo = q88::act_lo(g.epi.act), hi = q88::act_hi(g.epi.act);
     const bool plain = g.epi.add_mode == 0u && g.epi.act == 0u;   // no Add, no activation
+    // The fused Add's operands of a 32-row tile (output rows m_base.., rows from
+    // m_end on read 0; pixels p0w.. of the range, pnw of them valid), laid out as
+    // finish_tile reads them (half i, run t: row (lane / 8) + 8t of the half,
+    // pixels 8 * (lane % 8)..+8, as 8 packed int16), loaded ahead of the finish
+    // in one go: 16-byte loads when the runs are 16-byte aligned, 4-byte loads
+    // when they are 4-byte aligned, else 2-byte loads.  Values past a run's valid
+    // pixels are never stored (they lie in the operand's image, or past it,
+    // where the buffer reads 0); empty runs and rows past m_end read 0 through
+    // bit 31 of their offset, never through a branch.  Every load is issued
+    // before any is used.
+    const __amdgpu_buffer_rsrc_t ars = make_rsrc(g.epi.add_mode == 1u ? g.epi.add + (uint64_t)n * g.y_img : g.x,
+                                                 g.epi.add_mode == 1u ? (uint32_t)(g.y_img * 2u) : 0u);
+    auto add_load = [&](uint32_t m_base, uint32_t m_end, uint32_t p0w, uint32_t pnw, v4u (&av)[2][2]) {
+        const uint32_t c8 = (lane & 7) * 8;
+        uint32_t off[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const uint32_t m = m_base + i * 16 + (lane >> 3) + 8 * t;
+                const uint32_t bad = (uint32_t)(m >= m_end || c8 >= pnw);
+                off[i][t] = ((m * g.P + p0w + c8) * 2u) | (bad << 31);
+            }
+        if (g.vw == 8u) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int t = 0; t < 2; ++t) av[i][t] = __builtin_amdgcn_raw_buffer_load_b128(ars, off[i][t], 0, 0);
+        } else if (g.add_w4) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        av[i][t][q] = __builtin_amdgcn_raw_buffer_load_b32(ars, off[i][t] + 4u * q, 0, 0);
+        } else {
+            uint32_t h[2][2][8];
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int q = 0; q < 8; ++q)
+                        h[i][t][q] = __builtin_amdgcn_raw_buffer_load_b16(ars, off[i][t] + 2u * q, 0, 0);
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+                    av[i][t] = v4u{pack2(h[i][t][0], h[i][t][1]), pack2(h[i][t][2], h[i][t][3]),
+                                   pack2(h[i][t][4], h[i][t][5]), pack2(h[i][t][6], h[i][t][7])};
+        }
+    };
     // Epilogue, per wave, of a 32-row x 64-pixel accumulator tile (output rows
     // m_base.., rows from m_end on skipped; pixels p0w.. of the range, pnw of them
     // valid, njw 16-pixel column tiles in use): each 16-row half is finished into
     // the wave's LDS tile (row 4*(lane/16)+e, pixel column of the lane), then read
     // back as 8-pixel runs: lane -> (row lane/8 + 8t, pixels 8*(lane%8)..)
     auto finish_tile = [&](const v4i (&th)[2][4], const v4i (&tm)[2][4], const v4i (&tl)[2][4],
-                           uint32_t m_base, uint32_t m_end, uint32_t p0w, uint32_t pnw, uint32_t njw) {
+                           uint32_t m_base, uint32_t m_end, uint32_t p0w, uint32_t pnw, uint32_t njw,
+                           const v4u (&av)[2][2]) {
         const uint32_t c8 = (lane & 7) * 8;
         const uint32_t ncol = c8 < pnw ? min(8u, pnw - c8) : 0u;
 #pragma unroll
@@ -548,22 +604,12 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
                         yv[2 * q] = (int32_t)(int16_t)(tv[q] & 0xFFFFu);
                         yv[2 * q + 1] = (int32_t)tv[q] >> 16;
                     }
-                    if (g.epi.add_mode == 1u) {
-                        const int16_t* ap = g.epi.add + o;
-                        int32_t add[8];
-                        if (vec8) {
-                            const v4u a = *reinterpret_cast<const v4u*>(ap);
+                    if (g.epi.add_mode == 1u) {   // the operands add_load brought in
 #pragma unroll
-                            for (int q = 0; q < 4; ++q) {
-                                add[2 * q] = (int32_t)(int16_t)(a[q] & 0xFFFFu);
-                                add[2 * q + 1] = (int32_t)a[q] >> 16;
-                            }
-                        } else {
-#pragma unroll
-                            for (int q = 0; q < 8; ++q) add[q] = (uint32_t)q < ncol ? ap[q] : 0;
+                        for (int q = 0; q < 4; ++q) {
+                            yv[2 * q] = q88::add(yv[2 * q], (int32_t)(int16_t)(av[i][t][q] & 0xFFFFu));
+                            yv[2 * q + 1] = q88::add(yv[2 * q + 1], (int32_t)av[i][t][q] >> 16);
                         }
-#pragma unroll
-                        for (int q = 0; q < 8; ++q) yv[q] = q88::add(yv[q], add[q]);
                     }
 #pragma unroll
                     for (int q = 0; q < 8; ++q) yv[q] = q88::clamp(yv[q], lo, hi);
@@ -801,10 +847,55 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
             if (nj == 4u) k_loop(std::true_type{}, std::false_type{});
             else k_loop(std::false_type{}, std::false_type{});
         }
+        // Everything below recomputes its lane-dependent addresses: hoisted ahead
+        // of the k loop they would hold registers across it (and be spilled, and
+        // their reloads would wait for the loads issued after the k loop).
+        asm volatile("" : "+v"(lane));
 
         if constexpr (!PAIR) {
-            finish_tile(hh, mid, ll, wrow, g.M, p0, pn, nj);
+            v4u av[2][2] = {};
+            if (g.epi.add_mode == 1u) add_load(wrow, g.M, p0, pn, av);
+            finish_tile(hh, mid, ll, wrow, g.M, p0, pn, nj, av);
         } else {
+            // The 1x1: 32 x 64 tiles (row tile rt of its outputs, wave column cw's
+            // pixels) dealt over the waves.  A tile's A fragments (both k steps;
+            // with one step the second reads data that is never used) and its
+            // fused-Add operands load ahead: the wave's first tile's here, before
+            // the middle tile is written, the next tile's after a tile is finished.
+            // ah2 comes from the int8 plane when every weight fits int8 (fast2,
+            // chosen by a mask: no branch), else from the high limb plane; al2
+            // always from the low limb plane (unused with fast2: copying ah2 into
+            // it would wait for the load).
+            const uint32_t nrt2 = (g.M2 + 31u) / 32u;
+            const uint32_t arow = (lane & 15) * 64u + (lane >> 4) * 16u;
+            v4i ah2[2][2], al2[2][2];
+            v4u av2[2][2] = {};
+            auto tile2 = [&](uint32_t t, uint32_t& rt, uint32_t& p0w, uint32_t& pnw) {
+                rt = t / WC;
+                const uint32_t cw = t - rt * WC;
+                p0w = pb + sub * SPX + cw * 64u;
+                pnw = p0w < pe ? min(64u, pe - p0w) : 0u;
+            };
+            const uint32_t f2mask = fast2 ? ~0u : 0u;
+            auto load2 = [&](uint32_t t) {
+                uint32_t rt, p0w, pnw;
+                tile2(t, rt, p0w, pnw);
+#pragma unroll
+                for (int s2 = 0; s2 < 2; ++s2) {
+                    const uint32_t ro = rt * g.steps2 + (uint32_t)s2;
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        const uint32_t oh = ro * 4096u + i * 1024u + arow;
+                        const uint32_t o8 = g.pk2_8off + ro * 2048u + i * 1024u + arow;
+                        ah2[s2][i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                 wrs2, oh ^ ((oh ^ o8) & f2mask), 0, 0));
+                        al2[s2][i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
+                                                                 wrs2, oh + 2048u, 0, 0));
+                    }
+                }
+                if (g.epi.add_mode == 1u) add_load(rt * 32u, g.M2, p0w, pnw, av2);
+            };
+            if (wave < nrt2 * WC) load2(wave);
             // the middle tensor of this sub-tile, act1(sat16(acc >> 8)), as limb
             // planes: pixel px of the sub-tile at px * HP, channel c at byte c
             // (rows past the middle channels hold 0: their weights are 0)
@@ -843,70 +934,55 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
                 }
                 __syncthreads();
             }
-            // the 1x1: 32 x 64 tiles (row tile rt of its outputs, wave column cw's
-            // pixels) dealt over the waves
             const uint32_t* rt2 = reinterpret_cast<const uint32_t*>(lds + g.rt2_off);
-            const uint32_t nrt2 = (g.M2 + 31u) / 32u;
             const uint32_t kp2 = fast2 ? 0u : 16384u * 64u * g.steps2;
-            const uint32_t arow = (lane & 15) * 64u + (lane >> 4) * 16u;
             for (uint32_t t = wave; t < nrt2 * WC; t += 4u) {
-                const uint32_t rt = t / WC, cw = t - rt * WC;
-                const uint32_t p0w = pb + sub * SPX + cw * 64u;
-                const uint32_t pnw = p0w < pe ? min(64u, pe - p0w) : 0u;
-                if (pnw == 0u) continue;
-                const uint32_t njw = (pnw + 15u) / 16u;
-                v4i h2[2][4], m2[2][4], l2[2][4];
+                uint32_t rt, p0w, pnw;
+                tile2(t, rt, p0w, pnw);
+                if (pnw != 0u) {
+                    const uint32_t cw = t - rt * WC;
+                    const uint32_t njw = (pnw + 15u) / 16u;
+                    v4i h2[2][4], m2[2][4], l2[2][4];
 #pragma unroll
-                for (int i = 0; i < 2; ++i)
+                    for (int i = 0; i < 2; ++i)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        h2[i][j] = v4i{0, 0, 0, 0};
-                        m2[i][j] = v4i{0, 0, 0, 0};
-                        const uint32_t colt = fast2 ? 0u : 128u * cs[cw * 64u + j * 16u + (lane & 15)];
+                        for (int j = 0; j < 4; ++j) {
+                            h2[i][j] = v4i{0, 0, 0, 0};
+                            m2[i][j] = v4i{0, 0, 0, 0};
+                            const uint32_t colt = fast2 ? 0u : 128u * cs[cw * 64u + j * 16u + (lane & 15)];
 #pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            l2[i][j][e] = (int32_t)(rt2[rt * 32u + i * 16u + (lane >> 4) * 4u + e] - kp2 + colt);
-                    }
-                for (uint32_t s2 = 0; s2 < g.steps2; ++s2) {
-                    const uint32_t ro = rt * g.steps2 + s2;
-                    v4i ah[2], al[2];
-#pragma unroll
-                    for (int i = 0; i < 2; ++i) {
-                        if (fast2) {
-                            ah[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
-                                                                wrs2, g.pk2_8off + ro * 2048u + i * 1024u + arow, 0, 0));
-                            al[i] = ah[i];
-                        } else {
-                            ah[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
-                                                                wrs2, ro * 4096u + i * 1024u + arow, 0, 0));
-                            al[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(
-                                                                wrs2, ro * 4096u + 2048u + i * 1024u + arow, 0, 0));
+                            for (int e = 0; e < 4; ++e)
+                                l2[i][j][e] = (int32_t)(rt2[rt * 32u + i * 16u + (lane >> 4) * 4u + e] - kp2 + colt);
                         }
-                    }
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        if ((uint32_t)j >= njw) continue;
-                        const uint32_t b = (cw * 64u + j * 16u + (lane & 15)) * g.HP + s2 * 64u + (lane >> 4) * 16u;
-                        const v4i bh = *reinterpret_cast<const v4i*>(h_hi + b);
-                        const v4i bl = *reinterpret_cast<const v4i*>(h_lo + b);
-                        if (fast2) {   // sum w*x = 256 * sum w*x_hi + sum w*x_lo + 128 * sum w
+                    for (int s2 = 0; s2 < 2; ++s2) {
+                        if ((uint32_t)s2 >= g.steps2) continue;
 #pragma unroll
-                            for (int i = 0; i < 2; ++i) {
-                                m2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bh, m2[i][j], 0, 0, 0);
-                                l2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bl, l2[i][j], 0, 0, 0);
-                            }
-                        } else {
+                        for (int j = 0; j < 4; ++j) {
+                            if ((uint32_t)j >= njw) continue;
+                            const uint32_t b = (cw * 64u + j * 16u + (lane & 15)) * g.HP + s2 * 64u + (lane >> 4) * 16u;
+                            const v4i bh = *reinterpret_cast<const v4i*>(h_hi + b);
+                            const v4i bl = *reinterpret_cast<const v4i*>(h_lo + b);
+                            if (fast2) {   // sum w*x = 256 * sum w*x_hi + sum w*x_lo + 128 * sum w
 #pragma unroll
-                            for (int i = 0; i < 2; ++i) {
-                                h2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bh, h2[i][j], 0, 0, 0);
-                                m2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah[i], bl, m2[i][j], 0, 0, 0);
-                                l2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], bl, l2[i][j], 0, 0, 0);
-                                m2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al[i], bh, m2[i][j], 0, 0, 0);
+                                for (int i = 0; i < 2; ++i) {
+                                    m2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah2[s2][i], bh, m2[i][j], 0, 0, 0);
+                                    l2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah2[s2][i], bl, l2[i][j], 0, 0, 0);
+                                }
+                            } else {
+#pragma unroll
+                                for (int i = 0; i < 2; ++i) {
+                                    h2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah2[s2][i], bh, h2[i][j], 0, 0, 0);
+                                    m2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(ah2[s2][i], bl, m2[i][j], 0, 0, 0);
+                                    l2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al2[s2][i], bl, l2[i][j], 0, 0, 0);
+                                    m2[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(al2[s2][i], bh, m2[i][j], 0, 0, 0);
+                                }
                             }
                         }
                     }
+                    finish_tile(h2, m2, l2, rt * 32u, g.M2, p0w, pnw, njw, av2);
                 }
-                finish_tile(h2, m2, l2, rt * 32u, g.M2, p0w, pnw, njw);
+                if (t + 4u < nrt2 * WC) load2(t + 4u);
             }
             if (sub + 1 < nsub) __syncthreads();   // the next sub-tile's middle tile overwrites this one
         }
@@ -1199,6 +1275,7 @@ int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* 
     // 16-byte output accesses: every run of 8 pixels starts 16-byte aligned
     // (ranges start at multiples of L, sub-tiles at multiples of 64 pixels)
     g.vw = P % 8 == 0 && aligned(y, 16) && (ea.add_mode != 1u || aligned(ea.add, 16)) ? 8u : 1u;
+    g.add_w4 = P % 2 == 0 && ea.add_mode == 1u && aligned(ea.add, 4) ? 1u : 0u;
     const void* k = nullptr;
 #define CM_PG_PICK(M, NS, W, PR) (vec == 1 ? (const void*)conv_pgemm<1, M, NS, W, PR> \
                                   : vec == 2 ? (const void*)conv_pgemm<2, M, NS, W, PR> \
