@@ -241,6 +241,7 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
     __shared__ int32_t qtab[kMaxQ + 4];  // per sub-chunk q: patch byte offset of its tap and group
     __shared__ uint32_t tpos[kMaxTaps];  // per tap: patch position offset from a window origin
     __shared__ uint32_t rowterm_s[kMaxTB];   // per output channel of the row tile: the row term
+    __shared__ uint32_t flags_s[4];          // per wave: its rows' int8 votes
     uint8_t* p_hi = lds;
     uint8_t* p_lo = lds + g.p_plane;
     uint32_t* spos = reinterpret_cast<uint32_t*>(lds + g.spos_off);   // per position: channel sum
@@ -255,7 +256,10 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
             touch ^= reinterpret_cast<const uint32_t*>(&g)[i * 16];
         asm volatile("" ::"s"(touch));
     }
-    const uint32_t tid = threadIdx.x, wave = tid >> 6;
+    const uint32_t tid = threadIdx.x;
+    // the wave index in a scalar register: what derives from it (wave row and
+    // column, tile coordinates, weight-row offsets) stays scalar too
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     uint32_t lane = tid & 63;   // made opaque after each k loop (see there)
     int16_t* et = reinterpret_cast<int16_t*>(lds + g.epi_off + wave * kEpiBytes);
     // Workgroups are dealt to the 8 XCDs round robin; block b of XCD x takes the
@@ -670,9 +674,18 @@ __global__ __launch_bounds__(kPgThreads, 2) void conv_pgemm(PgArgs g) {
                 if (tid < ((g.M2 + 31u) & ~31u))
                     reinterpret_cast<uint32_t*>(lds + g.rt2_off)[tid] =
                         tid < g.M2 ? 128u * wsum2 + (uint32_t)(int32_t)(int16_t)bias2 * 256u : 0u;
-                fast2 = __syncthreads_and(tid >= g.M2 || fit2 != 0u) != 0;
             }
-            fast = __syncthreads_and(tid >= TB || !real || fit != 0u) != 0;
+            // the int8 flags: a wave vote each, met in LDS behind the one barrier
+            // the patch needs anyway (bit 0: a row of the tile past int8, bit 1:
+            // a 1x1 row past int8)
+            const bool wide1 = tid < TB && real && fit == 0u;
+            const bool wide2 = PAIR && tid < g.M2 && fit2 == 0u;
+            const uint32_t vote = (__ballot(wide1) != 0ull ? 1u : 0u) | (__ballot(wide2) != 0ull ? 2u : 0u);
+            if (lane == 0) flags_s[wave] = vote;
+            __syncthreads();
+            const uint32_t wide = __builtin_amdgcn_readfirstlane(flags_s[0] | flags_s[1] | flags_s[2] | flags_s[3]);
+            fast = (wide & 1u) == 0u;
+            fast2 = (wide & 2u) == 0u;
             if (!fast) {
                 a_load(0, fa_h[0], fa_l[0]);
                 if constexpr (NS == 3) a_load(ks_plus(0, 1), fa_h[1], fa_l[1]);
