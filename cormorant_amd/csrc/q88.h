@@ -46,28 +46,33 @@ __device__ __forceinline__ int32_t sub(int32_t a, int32_t b) { return sat16(a - 
 __device__ __forceinline__ int32_t mul(int32_t a, int32_t b) { return sat16((a * b) >> 8); }
 
 // VectorOP.cpp:22-25: b == 0 -> 0, else sat16(trunc((a * 256) / b)).
-// Branch-free in float: A = 256 a and b are exact floats; the estimate
-// A * rcp(b) (v_rcp_f32, relative error ~2^-23) is clamped to +-40000
-// (saturation is decided well outside that band) and truncated to q0, which is
-// then within one of trunc(A / b).  The remainder r = A - q0 b comes from one
-// FMA, exact when |q0| < 40000 (|r| < 2 |b|, an integer); q0 moves one step
-// toward zero when r has the sign opposite to A (it overshot) and one step
-// away from zero, in the quotient's direction, when |r| >= |b| (it fell
-// short) -- the two cannot both hold.  Clamped estimates only need the result
-// to stay beyond the saturation bound, which they do.  Verified exhaustively
-// over all 2^32 (a, b) pairs against exact integer division.
-__device__ __forceinline__ int32_t div(int32_t a, int32_t b) {
-    const float fa = (float)a * 256.0f, fb = (float)b;
-    const float t = __builtin_amdgcn_fmed3f(fa * __builtin_amdgcn_rcpf(fb), -40000.0f, 40000.0f);
-    const float q0 = __builtin_truncf(t);
-    const float r = __builtin_fmaf(-q0, fb, fa);
-    const float s = __builtin_copysignf(1.0f, fa * fb);   // the quotient's sign (A != 0)
-    const float over = r * fa < 0.0f ? s : 0.0f;
-    const float under = __builtin_fabsf(r) >= __builtin_fabsf(fb) ? s : 0.0f;
-    const int32_t q = (int32_t)(q0 + (under - over));
-    // b == 0 gives 0 through a mask, not a select (which became a branch around
-    // the whole computation)
-    return sat16(q) & -(int32_t)(b != 0);
+// Branch-free in float, on magnitudes: X = 256 |a| and B = |b| are exact
+// floats (X < 2^23; B = 1 stands in for b == 0, masked at the end).  The
+// estimate q0 = floor(X * rcp(B)) (v_rcp_f32, within one ulp) is within two of
+// floor(X / B); the remainder r = X - q0 B comes from one FMA and is exact (an
+// integer, |r| < 3B), and floor(r * rcp(B) + 2^-18) is exactly the number of
+// steps q0 is off: r / B lies at least 1/B >= 2^-15 below any integer it does
+// not reach, far more than the product's rounding error (< 2^-20) plus the
+// 2^-18 nudge, and the nudge lifts a product that rounds just under an integer
+// r / B equals.  The sign of a ^ b then goes onto the magnitude.  Verified
+// exhaustively over all 2^32 (a, b) pairs against exact division, on the GPU
+// and on the CPU with the reciprocal moved up to three ulps either way.
+// div_q is the unsaturated quotient (|q| <= 2^23, 0 for b == 0).
+__device__ __forceinline__ int32_t div_q(int32_t a, int32_t b) {
+    const float B = __builtin_fmaxf(__builtin_fabsf((float)b), 1.0f);
+    const float X = __builtin_fabsf((float)a) * 256.0f;
+    const float rb = __builtin_amdgcn_rcpf(B);
+    const float q0 = __builtin_floorf(X * rb);
+    const float r = __builtin_fmaf(-q0, B, X);
+    const float q = q0 + __builtin_floorf(__builtin_fmaf(r, rb, 0x1p-18f));
+    const uint32_t qs = __builtin_bit_cast(uint32_t, q) | ((uint32_t)(a ^ b) & 0x80000000u);
+    return (int32_t)__builtin_bit_cast(float, qs) & -(int32_t)(b != 0);
+}
+__device__ __forceinline__ int32_t div(int32_t a, int32_t b) { return sat16(div_q(a, b)); }
+// Two quotients saturated and packed by one v_cvt_pk_i16_i32: (a0 / b0) in the
+// low half, (a1 / b1) in the high half.
+__device__ __forceinline__ uint32_t div2(int32_t a0, int32_t b0, int32_t a1, int32_t b1) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pk_i16(div_q(a0, b0), div_q(a1, b1)));
 }
 
 // VectorOP.cpp:27-35

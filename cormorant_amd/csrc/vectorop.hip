@@ -33,10 +33,22 @@ __device__ __forceinline__ int32_t apply(int32_t a, int32_t b) {
 
 template <int OP>
 __device__ __forceinline__ v8s apply8(v8s a, v8s b) {
-    v8s r;
+    if constexpr (OP == CM_OP_DIV) {
+        // unsaturated quotients, saturated and packed two at a time
+        typedef unsigned int v4u8 __attribute__((ext_vector_type(4)));
+        v4u8 r;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) r[j] = (short)apply<OP>(a[j], b[j]);
-    return r;
+        for (int j = 0; j < 4; ++j) {
+            const short a0 = a[2 * j], a1 = a[2 * j + 1], b0 = b[2 * j], b1 = b[2 * j + 1];
+            r[j] = q88::div2(a0, b0, a1, b1);
+        }
+        return __builtin_bit_cast(v8s, r);
+    } else {
+        v8s r;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[j] = (short)apply<OP>(a[j], b[j]);
+        return r;
+    }
 }
 
 constexpr bool is_binary(int op) { return op < CM_OP_RELU; }
@@ -199,7 +211,12 @@ __global__ __launch_bounds__(kThreads) void vecop_div_sweep(uint32_t b_lo, uint3
         const double q = __builtin_trunc((double)(av * 256) / (double)bv);
         want = (int32_t)(q > 32767.0 ? 32767.0 : (q < -32768.0 ? -32768.0 : q));
     }
-    const int32_t got = q88::div(av, bv);
+    // the packed pair form the streaming kernel runs: (av, bv) in the low half,
+    // and the scalar form beside it
+    const uint32_t pair = q88::div2(av, bv, av, bv);
+    const int32_t got_lo = (int16_t)(pair & 0xFFFFu), got_hi = (int32_t)pair >> 16;
+    const int32_t got_s = q88::div(av, bv);
+    const int32_t got = got_lo != want ? got_lo : (got_hi != want ? got_hi : got_s);
     const unsigned long long bad = __ballot(got != want);
     if ((threadIdx.x & 63) == 0 && bad != 0) atomicAdd(out, (unsigned long long)__popcll(bad));
     if (got != want) {
