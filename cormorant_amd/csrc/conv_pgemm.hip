@@ -1106,7 +1106,7 @@ int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* 
     const uint32_t khspan = (kh - 1) * Dg + 1;
     const uint32_t last_cpt = (in_ch - (nchunks - 1) * 64 + 15) / 16;
     const uint32_t cpt_all = (in_ch + 15) / 16;
-    const uint32_t steps = (nchunks - 1) * taps + (taps * last_cpt + 3) / 4;
+    uint32_t steps = (nchunks - 1) * taps + (taps * last_cpt + 3) / 4;
     auto a16 = [](uint64_t v) { return (v + 15) & ~15ull; };
     // LDS bytes per patch position and plane: an odd multiple of 16 (the 16
     // pixels of a fragment read then fall on distinct bank groups)
@@ -1182,6 +1182,16 @@ int pg_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* 
         L = pick_l(true, ppitch, prows);
     }
     if (L == 0) return 1;
+    // With one patch of every chunk, a step count padded to a multiple of 3
+    // (k steps of zero weights, which the pack writes as the limbs of 0 and the
+    // q table sends to the zero slot: both sides of the limb identity gain
+    // 16384 per position, or nothing on the int8 path) runs the three-set
+    // pipeline, two steps of A fragments in flight instead of one; worth it
+    // when the added steps are at most an eighth of the real ones.
+    if (!multi) {
+        const uint32_t pad = (3u - steps % 3u) % 3u;
+        if (pad && 8u * pad <= steps && (steps + pad) * 4u <= (uint32_t)kMaxQ) steps += pad;
+    }
     uint64_t spos_off = 0, epi_off = 0;
     const uint64_t lds = layout(prows, ppitch, spos_off, epi_off);
     const uint32_t rpi = (uint32_t)((P + L - 1) / L);

@@ -142,14 +142,21 @@ def test_config4_full_size(case, ws):
 
 
 def pgemm_need(C, M, kh, kw):
-    """Workspace of the patch-GEMM path: packed weights (row tiles of TB = 32, 64 or
-    128 output channels: TB x 64 k as two limb planes and one int8 plane per row tile
-    and k step), and one uint32 row sum and one int8 flag per padded row."""
+    """Workspace sizes of the patch-GEMM path: packed weights (row tiles of TB = 32, 64
+    or 128 output channels: TB x 64 k as two limb planes and one int8 plane per row
+    tile and k step), and one uint32 row sum and one int8 flag per padded row.  With
+    one patch of every channel chunk the step count is padded to a multiple of 3 when
+    that adds at most an eighth more steps (zero-weight steps for the three-set
+    pipeline); with restaged chunks it is not, so both sizes are possible."""
     taps, nch = kh * kw, -(-C // 64)
     tb = 128 if nch > 1 or M > 64 else 64 if M > 32 else 32
     mt = -(-M // tb)
     steps = (nch - 1) * taps + (taps * -(-(C - (nch - 1) * 64) // 16) + 3) // 4
-    return mt * steps * 3 * tb * 64 + 8 * tb * mt
+    pad = (3 - steps % 3) % 3
+    sizes = {mt * steps * 3 * tb * 64 + 8 * tb * mt}
+    if pad and 8 * pad <= steps and (steps + pad) * 4 <= 256:
+        sizes.add(mt * (steps + pad) * 3 * tb * 64 + 8 * tb * mt)
+    return sizes
 
 
 PGEMM = [
@@ -174,7 +181,7 @@ def test_patch_gemm_full_range(geom):
     N, C, H, W, M, kh, kw, s, d, p = geom
     OH, OW = (H + 2 * p - d * (kh - 1) - 1) // s + 1, (W + 2 * p - d * (kw - 1) - 1) // s + 1
     args = (N, C, H, W, M, OH, OW, kh, kw, s, s, d, d, p, p, 1, 0)
-    assert K.conv_workspace_size(*args) == pgemm_need(C, M, kh, kw), "expected the patch-GEMM path"
+    assert K.conv_workspace_size(*args) in pgemm_need(C, M, kh, kw), "expected the patch-GEMM path"
     say(f"conv patch gemm {geom}")
     g = wl.rng(833, *geom)
     x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
@@ -206,7 +213,7 @@ def test_patch_gemm_int8_weights(geom, mix):
     N, C, H, W, M, kh, kw, s, d, p = geom
     OH, OW = (H + 2 * p - d * (kh - 1) - 1) // s + 1, (W + 2 * p - d * (kw - 1) - 1) // s + 1
     args = (N, C, H, W, M, OH, OW, kh, kw, s, s, d, d, p, p, 1, 0)
-    assert K.conv_workspace_size(*args) == pgemm_need(C, M, kh, kw), "expected the patch-GEMM path"
+    assert K.conv_workspace_size(*args) in pgemm_need(C, M, kh, kw), "expected the patch-GEMM path"
     say(f"conv patch gemm int8 weights {geom} {mix}")
     g = wl.rng(834, *geom, len(mix))
     x = g.integers(-32768, 32768, N * C * H * W, dtype=np.int16)
@@ -280,7 +287,7 @@ def test_conv_packed_weights(geom):
     OH, OW = (H + 2 * p - d * (kh - 1) - 1) // s + 1, (W + 2 * p - d * (kw - 1) - 1) // s + 1
     args = (N, C, H, W, M, OH, OW, kh, kw, s, s, d, d, p, p, 1, 0)
     size = K.conv_packed_size(*args)
-    assert size == pgemm_need(C, M, kh, kw)
+    assert size in pgemm_need(C, M, kh, kw)
     say(f"conv packed weights {geom}")
     g = wl.rng(835, *geom)
     for lo, hi in ((-128, 128), (-32768, 32768)):
