@@ -60,6 +60,7 @@ METRIC = "Q8.8 GOP/s (conv/GEMM), GB/s (vecop/pool); images/s MobileNet-like b16
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, 8 TB/s
 INT8_PEAK_TOPS = 5000.0        # MI355X dense int8 MFMA, 5.0 POP/s
 LIMB_PRODUCTS = 4              # int8 MFMA products per exact Q8.8 product
+SETTLE_MS = 30.0               # untimed back-to-back runs ahead of each measurement
 
 
 HEADLINE_MAX = 4000            # bytes of the last stdout line
@@ -110,12 +111,34 @@ def summarize(results: dict, cases: list, cpu_res: dict) -> dict:
     return s
 
 
+def settle(run_once, min_ms: float = SETTLE_MS, max_runs: int = 100000) -> None:
+    """Run `run_once` back to back, untimed, for at least `min_ms` of wall time
+    (synchronising every few runs, so that the time is the GPU's): the engine clock
+    climbs for a few milliseconds after an idle stretch (host-side checks between
+    the measurements), and a measurement taken on the ramp reads 5-10 % slow."""
+    import torch
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    runs = 0
+    while (time.perf_counter() - t0) * 1e3 < min_ms and runs < max_runs:
+        run_once()
+        runs += 1
+        if runs % 4 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
+
+
 def time_launches(calls, steps: int) -> float:
     """Mean duration (ms) of one launch: HIP events on the launch stream (torch's
     current stream, which the C-ABI wrappers use) bracket `steps` back-to-back
-    launches, cycling through `calls`."""
+    launches, cycling through `calls`, after the clock has settled under the same
+    launches."""
     import torch
-    torch.cuda.synchronize()
+
+    def once():
+        for c in calls:
+            c()
+    settle(once)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
@@ -129,7 +152,7 @@ def time_launches(calls, steps: int) -> float:
 def time_graph(calls, steps: int) -> float:
     """Mean duration (ms) of one launch with host overhead removed: `steps`
     launches (cycling through `calls`) are captured into one HIP graph, which is
-    replayed once untimed and then once between HIP events.  The calls run once
+    replayed untimed until the clock has settled and then once between HIP events.  The calls run once
     eagerly on the capture stream first."""
     import torch
     side = torch.cuda.Stream()
@@ -143,8 +166,7 @@ def time_graph(calls, steps: int) -> float:
     with torch.cuda.graph(graph, stream=side):
         for i in range(steps):
             calls[i % len(calls)]()
-    graph.replay()
-    torch.cuda.synchronize()
+    settle(graph.replay)
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
     e0.record()
@@ -672,7 +694,7 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--quick", action="store_true", help="headline workload only, no CPU baseline")
     ap.add_argument("--workloads", default="vecop,gemm,conv,pool,graphs,cases",
                     help="comma list of vecop (always run: the headline), gemm, conv, pool "
