@@ -171,6 +171,8 @@ PGEMM = [
     (48, 8, 26, 22, 96, 3, 1, 1, 3, 1),        # 3x1 window, dilation 3
     (32, 130, 12, 100, 72, 3, 3, 1, 1, 1),     # three chunks too wide for one patch: restaged in turn
     (112, 150, 20, 24, 40, 5, 5, 1, 1, 2),     # 5x5, three chunks in one patch: 63 k steps
+    (32, 96, 28, 28, 96, 3, 3, 1, 1, 1),       # 14 k steps padded to 15 (one zero-weight step)
+    (96, 160, 14, 14, 160, 3, 3, 1, 1, 1),     # 23 k steps padded to 24, two row tiles
 ]
 
 
