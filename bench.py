@@ -424,7 +424,7 @@ def graph_lower_bound_s(plan) -> float:
 def launch_members(item):
     """The kernel calls one launch of the session runs, in order."""
     from cormorant_amd.scheduler import fuse
-    if isinstance(item, (fuse.FusedCall, fuse.PairCall)):
+    if isinstance(item, (fuse.FusedCall, fuse.PairCall, fuse.GapCall)):
         return (item.call,) + tuple(item.absorbed)
     return (item,)
 
@@ -434,13 +434,13 @@ def launch_lower_bound_s(launch_list) -> float:
     bytes the launch must move, MFMA time of its MACs).  A launch's bytes are the
     tensors its member calls read that no member writes, plus the tensor it leaves in
     memory; intermediates kept on chip (fused epilogues, a convolution pair's middle
-    tensor) count for nothing."""
+    tensor, the output a fused GlobalAveragePool reduces) count for nothing."""
     from cormorant_amd.scheduler import fuse
     total = 0.0
     for item in launch_list:
         members = launch_members(item)
         written = {fuse._writes(c) for c in members}
-        out = item.out if isinstance(item, (fuse.FusedCall, fuse.PairCall)) else fuse._writes(item)
+        out = item.out if isinstance(item, (fuse.FusedCall, fuse.PairCall, fuse.GapCall)) else fuse._writes(item)
         need = {}
         for c in members:
             ext = c.extents()

@@ -23,6 +23,7 @@ EXPORTS = (
     "cm_matmul_workspace_size", "cm_conv_workspace_size", "cm_set_workspace",
     "cm_matmul_noalloc", "cm_conv_packed_size", "cm_conv_pack", "cm_conv_packed_ex",
     "cm_conv_pair_packed_size", "cm_conv_pair_pack", "cm_conv_pair_packed_ex",
+    "cm_conv_gap_supported", "cm_conv_gap",
 )
 
 CM_OK = 0
@@ -117,6 +118,8 @@ _SIGS = {
     "cm_conv_pair_pack": (_i, [_vp, _vp] + [_u32] * 14 + [_vp, ctypes.c_size_t, _vp]),
     "cm_conv_pair_packed_ex": (_i, [_vp, _vp, _vp, _vp, _vp] + [_u32] * 15 +
                                [ctypes.POINTER(CmEpilogue), _vp]),
+    "cm_conv_gap_supported": (_i, [_u32] * 4),
+    "cm_conv_gap": (_i, [_vp, _vp, _vp, _vp] + [_u32] * 5 + [_vp]),
 }
 
 _lib = None

@@ -278,6 +278,22 @@ int cm_conv_pair_packed_ex(const int16_t* x, const void* packed, const int16_t* 
                                    pick(stream));
 }
 
+int cm_conv_gap_supported(uint32_t batch, uint32_t in_ch, uint32_t hw, uint32_t out_ch) {
+    return cm_conv_gap_fits(batch, in_ch, hw, out_ch) ? 1 : 0;
+}
+
+int cm_conv_gap(const int16_t* x, const int16_t* weight, const int16_t* bias, int16_t* y,
+                uint32_t batch, uint32_t in_ch, uint32_t hw, uint32_t out_ch, uint32_t act,
+                hipStream_t stream) {
+    if ((uint64_t)batch * out_ch == 0) return CM_OK;
+    if (!x || !weight || !y) return cm_set_error(CM_ERR_INVALID, "conv gap: null x, weight or y");
+    if (act > 2u) return cm_set_error(CM_ERR_INVALID, "conv gap: act %u (0 none, 1 Relu, 2 Clip(0,6))", act);
+    if (!cm_conv_gap_fits(batch, in_ch, hw, out_ch))
+        return cm_set_error(CM_ERR_INVALID, "conv gap: %u channels of %u pixels are outside the fused kernel's "
+                            "range (in_ch 1-512, hw 1-64)", in_ch, hw);
+    return cm_conv_gap_launch(x, weight, bias, y, batch, in_ch, hw, out_ch, act, pick(stream));
+}
+
 int cm_pool(const int16_t* x, int16_t* y, uint32_t batch, uint32_t channels, uint32_t in_h,
             uint32_t in_w, uint32_t out_h, uint32_t out_w, uint32_t pool_h, uint32_t pool_w,
             uint32_t stride_h, uint32_t stride_w, uint32_t pad_top, uint32_t pad_left,

@@ -41,6 +41,10 @@ inline EpiArgs cm_epi_args(const cm_epilogue_t* e) {
     return e ? EpiArgs{e->add, e->add_mode, e->act} : EpiArgs{nullptr, 0u, 0u};
 }
 int cm_check_launch(const char* what);
+bool cm_conv_gap_fits(uint32_t batch, uint32_t in_ch, uint32_t hw, uint32_t out_ch);
+int cm_conv_gap_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
+                       uint32_t batch, uint32_t in_ch, uint32_t hw, uint32_t out_ch, uint32_t act,
+                       hipStream_t s);
 uint32_t cm_cu_count();   // compute units of the current device (cached per device)
 
 // Division of any n < 2^31 by a fixed d >= 1 as a multiply and shift

@@ -46,6 +46,9 @@ struct PwArgs {
     uint32_t rt, nk;        // row tiles of 32; k steps of 64
     uint32_t x_bytes, w_bytes, y_bytes;
     FastDiv div_p, div_rt;
+    // GAP form: row-tile pairs per image, and 1 / P for the average's finaliser
+    uint32_t rtp;
+    float inv_p;
 };
 
 using limbs::hi4;
@@ -99,12 +102,30 @@ __device__ __forceinline__ void pw_load(const PwArgs& g, __amdgpu_buffer_rsrc_t 
         }
 }
 
-template <bool HAS_BIAS, bool AV>
+// GAP: the convolution followed by GlobalAveragePool of every output plane
+// (P <= 64), y = [image][channel].  A block is one image and two 32-channel row
+// tiles; its waves 2t and 2t + 1 take row tile t's pixels 0-31 and 32-63 (the
+// columns past P read 0 and are left out of the sums), each sums its finished
+// outputs (sat16, activation: the values the unfused convolution would store)
+// over its pixels as the pool's accumulator does (value << 8, mod 2^32), the
+// two halves meet in LDS, and the even wave finishes the average
+// (PoolingKernel.cpp:253-266 through the pool kernels' own finaliser).
+template <bool HAS_BIAS, bool AV, bool GAP>
 __global__ __launch_bounds__(kThreads) void conv_pw(PwArgs g) {
     const uint32_t lane = threadIdx.x & 63;
-    const uint32_t wid = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
-    const uint32_t ct = fdiv(wid, g.div_rt), rt = wid - ct * g.rt;   // waves of a block share columns
-    if (ct * 32u >= g.NP) return;   // the whole wave
+    const uint32_t wave = threadIdx.x >> 6;
+    uint32_t ct, rt, gap_n = 0, half = 0;
+    if constexpr (GAP) {
+        gap_n = blockIdx.x / g.rtp;
+        rt = (blockIdx.x - gap_n * g.rtp) * 2u + (wave >> 1);
+        half = wave & 1u;
+        ct = 0;
+    } else {
+        const uint32_t wid = blockIdx.x * (kThreads / 64) + wave;
+        ct = fdiv(wid, g.div_rt);
+        rt = wid - ct * g.rt;   // waves of a block share columns
+        if (ct * 32u >= g.NP) return;   // the whole wave
+    }
     const uint32_t r16 = lane & 15, kg = lane >> 4;
     const __amdgpu_buffer_rsrc_t wr = make_rsrc(g.w, g.w_bytes), xr = make_rsrc(g.x, g.x_bytes);
     // this lane's fragment rows (output channels) and columns (image, pixel)
@@ -116,10 +137,16 @@ __global__ __launch_bounds__(kThreads) void conv_pw(PwArgs g) {
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const uint32_t col = ct * 32u + j * 16u + r16;
-        const uint32_t n = fdiv(col, g.div_p), p = col - n * g.P;
-        bcol[j] = col < g.NP ? (n * g.C * g.P + p) * 2u : kOob;
-        yoff[j] = col < g.NP ? n * g.M * g.P + p : 0xFFFFFFFFu;
+        if constexpr (GAP) {
+            const uint32_t p = half * 32u + j * 16u + r16;
+            bcol[j] = p < g.P ? (gap_n * g.C * g.P + p) * 2u : kOob;
+            yoff[j] = p < g.P ? 0u : 0xFFFFFFFFu;
+        } else {
+            const uint32_t col = ct * 32u + j * 16u + r16;
+            const uint32_t n = fdiv(col, g.div_p), p = col - n * g.P;
+            bcol[j] = col < g.NP ? (n * g.C * g.P + p) * 2u : kOob;
+            yoff[j] = col < g.NP ? n * g.M * g.P + p : 0xFFFFFFFFu;
+        }
     }
     // the bias and the fused Add's operand of every output this lane stores,
     // loaded now so that their latency hides behind the k loop (loaded in the
@@ -134,7 +161,7 @@ __global__ __launch_bounds__(kThreads) void conv_pw(PwArgs g) {
                 biasv[i][e] = q88::data_to_acc(g.bias[m < g.M ? m : 0u]);
             }
     }
-    if (g.epi.add_mode == 1u) {
+    if (!GAP && g.epi.add_mode == 1u) {
         const __amdgpu_buffer_rsrc_t ar = make_rsrc(g.epi.add, g.y_bytes);
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -214,6 +241,7 @@ __global__ __launch_bounds__(kThreads) void conv_pw(PwArgs g) {
     }
     // epilogue: lane holds rows 4 * kg + e (e = 0..3) of each 16-row tile, column r16
     const int32_t lo = q88::act_lo(g.epi.act), hi = q88::act_hi(g.epi.act);
+    uint32_t gsum[2][4] = {};   // GAP: this lane's columns' (value << 8) per row
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -228,12 +256,35 @@ __global__ __launch_bounds__(kThreads) void conv_pw(PwArgs g) {
                 if (yoff[j] == 0xFFFFFFFFu) continue;
                 const uint32_t acc = 65536u * (uint32_t)hh[i][j][e] + 256u * (uint32_t)mid[i][j][e] +
                                      (uint32_t)ll[i][j][e] + 128u * (rs + csum[j]) - 16384u * kp + b8;
-                const uint32_t yi = yoff[j] + m * g.P;
                 int32_t v = q88::acc_to_data(acc);
-                if (g.epi.add_mode == 1u) v = q88::add(v, (int16_t)addv[i][e][j]);
-                g.y[yi] = (int16_t)q88::clamp(v, lo, hi);
+                if constexpr (GAP) {
+                    gsum[i][e] += (uint32_t)q88::clamp(v, lo, hi) << 8;
+                } else {
+                    const uint32_t yi = yoff[j] + m * g.P;
+                    if (g.epi.add_mode == 1u) v = q88::add(v, (int16_t)addv[i][e][j]);
+                    g.y[yi] = (int16_t)q88::clamp(v, lo, hi);
+                }
             }
         }
+    if constexpr (GAP) {
+        // the sixteen columns of a row are the lanes of one 16-lane group
+        __shared__ uint32_t part[kThreads / 64][32];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                uint32_t v = gsum[i][e];
+#pragma unroll
+                for (int o = 1; o < 16; o <<= 1) v += (uint32_t)__shfl_xor((int)v, o, 64);
+                if (r16 == 0) part[wave][i * 16 + kg * 4 + e] = v;
+            }
+        __syncthreads();
+        if (half == 0 && lane < 32u) {
+            const uint32_t m = rt * 32u + lane;
+            if (m < g.M)
+                g.y[(uint64_t)gap_n * g.M + m] = q88::avg_finalize(part[wave][lane] + part[wave + 1][lane], g.inv_p);
+        }
+    }
 }
 
 }  // namespace
@@ -262,11 +313,49 @@ int cm_conv_pw_launch(const int16_t* x, const int16_t* w, const int16_t* bias, i
     const dim3 grid((uint32_t)((waves + 3) / 4));
     const bool av = in_ch % 8 == 0 && ((uintptr_t)w & 15u) == 0;
     if (bias) {
-        if (av) hipLaunchKernelGGL((conv_pw<true, true>), grid, dim3(kThreads), 0, lc.s, g);
-        else hipLaunchKernelGGL((conv_pw<true, false>), grid, dim3(kThreads), 0, lc.s, g);
+        if (av) hipLaunchKernelGGL((conv_pw<true, true, false>), grid, dim3(kThreads), 0, lc.s, g);
+        else hipLaunchKernelGGL((conv_pw<true, false, false>), grid, dim3(kThreads), 0, lc.s, g);
     } else {
-        if (av) hipLaunchKernelGGL((conv_pw<false, true>), grid, dim3(kThreads), 0, lc.s, g);
-        else hipLaunchKernelGGL((conv_pw<false, false>), grid, dim3(kThreads), 0, lc.s, g);
+        if (av) hipLaunchKernelGGL((conv_pw<false, true, false>), grid, dim3(kThreads), 0, lc.s, g);
+        else hipLaunchKernelGGL((conv_pw<false, false, false>), grid, dim3(kThreads), 0, lc.s, g);
     }
     return cm_check_launch("conv_pw");
+}
+
+// The 1x1 convolution + activation + GlobalAveragePool shapes cm_conv_gap runs:
+// planes of at most 64 pixels, the register-only kernel's channel limit, and
+// operands whose byte offsets fit the buffer ranges.
+bool cm_conv_gap_fits(uint32_t batch, uint32_t in_ch, uint32_t hw, uint32_t out_ch) {
+    if (batch == 0 || in_ch == 0 || in_ch > kPwMaxK || hw == 0 || hw > 64 || out_ch == 0) return false;
+    const uint64_t x_bytes = 2ull * in_ch * hw * batch, w_bytes = 2ull * out_ch * in_ch;
+    const uint64_t blocks = (uint64_t)batch * ((out_ch + 63) / 64);
+    return x_bytes < 0x80000000ull && w_bytes < 0x80000000ull && blocks < 0x80000000ull &&
+           (uint64_t)batch * out_ch < 0xFFFFFFFFull;
+}
+
+int cm_conv_gap_launch(const int16_t* x, const int16_t* w, const int16_t* bias, int16_t* y,
+                       uint32_t batch, uint32_t in_ch, uint32_t hw, uint32_t out_ch, uint32_t act,
+                       hipStream_t s) {
+    PwArgs g{};
+    g.x = x; g.w = w; g.bias = bias; g.y = y;
+    g.epi = EpiArgs{};
+    g.epi.act = act;
+    g.C = in_ch; g.M = out_ch; g.P = hw; g.NP = batch * hw;
+    g.rt = (out_ch + 31) / 32;
+    g.rtp = (g.rt + 1) / 2;
+    g.nk = (in_ch + 63) / 64;
+    g.x_bytes = 2u * in_ch * hw * batch; g.w_bytes = 2u * out_ch * in_ch; g.y_bytes = 2u * batch * out_ch;
+    g.div_p = make_fastdiv(hw);
+    g.div_rt = make_fastdiv(g.rt);
+    g.inv_p = 1.0f / (float)hw;
+    const dim3 grid(batch * g.rtp);
+    const bool av = in_ch % 8 == 0 && ((uintptr_t)w & 15u) == 0;
+    if (bias) {
+        if (av) hipLaunchKernelGGL((conv_pw<true, true, true>), grid, dim3(kThreads), 0, s, g);
+        else hipLaunchKernelGGL((conv_pw<true, false, true>), grid, dim3(kThreads), 0, s, g);
+    } else {
+        if (av) hipLaunchKernelGGL((conv_pw<false, true, true>), grid, dim3(kThreads), 0, s, g);
+        else hipLaunchKernelGGL((conv_pw<false, false, true>), grid, dim3(kThreads), 0, s, g);
+    }
+    return cm_check_launch("conv_gap");
 }

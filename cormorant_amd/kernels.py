@@ -198,6 +198,28 @@ def ConvPackedKernel(x, packed, bias, y, batch, in_ch, in_h, in_w, out_ch, out_h
                  ctypes.byref(epi) if epi is not None else None, _stream(stream))
 
 
+def conv_gap_supported(batch, in_ch, hw, out_ch) -> bool:
+    """Whether ConvGapKernel takes the shape (planes of at most 64 pixels, at most
+    512 input channels)."""
+    args = [_u32("conv gap arg", v) for v in (batch, in_ch, hw, out_ch)]
+    return bool(_native.load().cm_conv_gap_supported(*args))
+
+
+def ConvGapKernel(x, weight, bias, y, batch, in_ch, hw, out_ch, has_bias=1, act=ACT_NONE,
+                  stream=None) -> None:
+    """A 1x1 convolution (stride 1, no padding), its activation and a
+    GlobalAveragePool of every output plane as one launch: y [batch][out_ch] equals
+    ConvKernel(..., act) followed by PoolingKernel's global average, bit for bit."""
+    args = [_u32("conv gap arg", v) for v in (batch, in_ch, hw, out_ch, act)]
+    if batch * out_ch == 0:
+        return
+    px = _dev_ptr(x, batch * in_ch * hw, "x")
+    pw = _dev_ptr(weight, out_ch * in_ch, "weight")
+    pbias = _dev_ptr(bias, out_ch, "bias") if has_bias else None
+    py = _dev_ptr(y, batch * out_ch, "y")
+    _native.call("cm_conv_gap", px, pw, pbias, py, *args, _stream(stream))
+
+
 def conv_pair_packed_size(batch, in_ch, in_h, in_w, mid_ch, out_h, out_w, kh, kw, stride,
                           dilation, pad_top, pad_left, out_ch) -> int:
     """Bytes of packed weights for ConvPairKernel: a kh x kw convolution in_ch -> mid_ch

@@ -30,6 +30,15 @@ a 1x1 Conv (with its Add / activation) reads can run as one launch
 
 ``launch_list(plan, pair_ok)`` forms them where ``pair_ok`` (the backend's
 shape check) accepts the pair; the result is the same bit for bit.
+
+Pooled heads: a 1x1 Conv (with its Relu / Clip(0,6)) whose output nothing but a
+GlobalAveragePool reads runs as one launch (``cm_conv_gap``) that averages the
+activated outputs without storing them:
+
+    conv 1x1 [-> Relu | Clip(0,6)] -> GlobalAveragePool
+
+``launch_list(plan, pair_ok, gap_ok)`` forms them where ``gap_ok`` accepts the
+shape.
 """
 from __future__ import annotations
 
@@ -92,6 +101,34 @@ class PairCall:
 
     @property
     def act1(self) -> int:
+        return self.first.act if isinstance(self.first, FusedCall) else ACT_NONE
+
+    def __str__(self) -> str:
+        return " + ".join(str(c) for c in (self.call,) + self.absorbed)
+
+
+@dataclass(frozen=True)
+class GapCall:
+    """A 1x1 convolution group and the GlobalAveragePool that alone reads its
+    output, as one launch (``call`` / ``absorbed``: the convolution, its
+    activation, the pool)."""
+    first: object     # KernelCall or FusedCall: the 1x1 convolution (activation only)
+    pool: KernelCall  # the GlobalAveragePool
+
+    @property
+    def call(self) -> KernelCall:
+        return _call_of(self.first)
+
+    @property
+    def absorbed(self) -> Tuple[KernelCall, ...]:
+        return _absorbed(self.first) + (self.pool,)
+
+    @property
+    def out(self) -> str:
+        return _writes(self.pool)
+
+    @property
+    def act(self) -> int:
         return self.first.act if isinstance(self.first, FusedCall) else ACT_NONE
 
     def __str__(self) -> str:
@@ -279,6 +316,40 @@ def _pairs(plan, seq: List[Tuple[int, object]]) -> List[Tuple[int, PairCall]]:
     return out
 
 
+def _gap_match(g: _Graph, ka: int, a, kb: int, b) -> Optional[GapCall]:
+    """The pooled head of items a (plan index ka) and b (plan index kb), or None."""
+    if isinstance(b, (FusedCall, PairCall)) or isinstance(a, PairCall):
+        return None
+    ca = _call_of(a)
+    if ca.kernel != "conv" or b.kernel != "pool" or any(ca.offsets or ()) or any(b.offsets or ()):
+        return None
+    n, _c, h, w, m, oh, ow, kh, kw, sh, sw, dh, dw, pt, pl, _hb, dwise = ca.args
+    if dwise or (kh, kw, sh, sw, dh, dw, pt, pl) != (1, 1, 1, 1, 1, 1, 0, 0) or (oh, ow) != (h, w):
+        return None
+    if isinstance(a, FusedCall) and a.add is not None:
+        return None
+    pb, pc, ph, pw, poh, pow_, kph, kpw, _psh, _psw, ppt, ppl, pdh, pdw, ptype = b.args[:15]
+    if (pb, pc, ph, pw) != (n, m, oh, ow) or (poh, pow_, kph, kpw) != (1, 1, oh, ow):
+        return None
+    if (ppt, ppl, pdh, pdw, ptype) != (0, 0, 1, 1, 1):
+        return None
+    mid = _out_of(a)
+    if b.tensors[0] != mid or not g.private(mid, ka + len(_absorbed(a)), kb):
+        return None
+    return GapCall(a, b)
+
+
+def _gaps(plan, seq: List[Tuple[int, object]]) -> List[Tuple[int, GapCall]]:
+    """Every pooled head the call structure allows in seq (no storage or shape check)."""
+    g = _Graph(plan)
+    out: List[Tuple[int, GapCall]] = []
+    for i in range(len(seq) - 1):
+        gc = _gap_match(g, seq[i][0], seq[i][1], seq[i + 1][0], seq[i + 1][1])
+        if gc is not None:
+            out.append((i, gc))
+    return out
+
+
 def live_from(plan) -> Dict[str, int]:
     """{fused or paired output tensor: node index of its first MatMul / Conv} for
     the pool layout."""
@@ -288,6 +359,8 @@ def live_from(plan) -> Dict[str, int]:
     seq = _indexed(plan, dict(cands))
     for i, pc in _pairs(plan, seq):
         starts[pc.out] = node_of[seq[i][0]]
+    for i, gc in _gaps(plan, seq):
+        starts[gc.out] = node_of[seq[i][0]]
     return starts
 
 
@@ -338,18 +411,30 @@ def _pair_storage_ok(plan, pc: PairCall) -> bool:
     return True
 
 
-def launch_list(plan, pair_ok: Optional[Callable[[PairCall], bool]] = None) -> List[object]:
+def _gap_storage_ok(plan, gc: GapCall) -> bool:
+    """The pooled output overlaps nothing the convolution reads."""
+    out = _span(plan, gc.pool, gc.out)
+    return not any(_overlap(out, _span(plan, gc.call, n)) for n in _reads(gc.call))
+
+
+def launch_list(plan, pair_ok: Optional[Callable[[PairCall], bool]] = None,
+                gap_ok: Optional[Callable[[GapCall], bool]] = None) -> List[object]:
     """plan.calls with every fusable group replaced by its FusedCall and, when
-    ``pair_ok`` is given, every convolution pair it accepts by a PairCall."""
+    ``pair_ok`` is given, every convolution pair it accepts by a PairCall; when
+    ``gap_ok`` is given, every pooled head it accepts by a GapCall."""
     seq = _indexed(plan, dict(fusions(plan)))
-    if pair_ok is None:
-        return [item for _, item in seq]
-    pairs = {i: pc for i, pc in _pairs(plan, seq) if _pair_storage_ok(plan, pc) and pair_ok(pc)}
+    pairs = {} if pair_ok is None else {
+        i: pc for i, pc in _pairs(plan, seq) if _pair_storage_ok(plan, pc) and pair_ok(pc)}
+    gaps = {} if gap_ok is None else {
+        i: gc for i, gc in _gaps(plan, seq) if _gap_storage_ok(plan, gc) and gap_ok(gc)}
     out: List[object] = []
     i = 0
     while i < len(seq):
         if i in pairs:
             out.append(pairs[i])
+            i += 2
+        elif i in gaps:
+            out.append(gaps[i])
             i += 2
         else:
             out.append(seq[i][1])

@@ -19,7 +19,9 @@ directly by the producing kernel.  With ``fuse=True`` (default) an Add /
 Relu / Clip(0,6) call that is the sole reader of a MatMul / Conv output runs
 in that call's epilogue, and a convolution whose output only a 1x1
 convolution reads runs with it as one launch (``cm_conv_pair_packed_ex``,
-weights packed at init; ``fuse.py``); results are bit-identical either way.
+weights packed at init; ``fuse.py``), and a 1x1 convolution whose output only a
+GlobalAveragePool reads runs with it as one launch (``cm_conv_gap``); results
+are bit-identical either way.
 There is no CPU execution path: without the native library the constructor
 raises.
 """
@@ -52,7 +54,8 @@ class InferenceSession:
             starts = _fuse.live_from(self.plan)
             if starts:
                 self.plan = BufferPlan(self.graph, starts)
-            self.launch_list = _fuse.launch_list(self.plan, pair_ok=lambda pc: self._packed_size(pc) > 0)
+            self.launch_list = _fuse.launch_list(self.plan, pair_ok=lambda pc: self._packed_size(pc) > 0,
+                                                 gap_ok=self._gap_ok)
         else:
             self.launch_list = [c for _, c in self.plan.calls]
         self.stream = int(stream)
@@ -140,7 +143,11 @@ class InferenceSession:
 
     @staticmethod
     def _call_of(item) -> KernelCall:
-        return item.call if isinstance(item, (_fuse.FusedCall, _fuse.PairCall)) else item
+        return item.call if isinstance(item, (_fuse.FusedCall, _fuse.PairCall, _fuse.GapCall)) else item
+
+    def _gap_ok(self, gc) -> bool:
+        a = gc.call.args
+        return bool(self._lib.cm_conv_gap_supported(a[0], a[1], a[2] * a[3], a[4]))
 
     @classmethod
     def _pair_args(cls, pc) -> Tuple[int, ...]:
@@ -151,6 +158,8 @@ class InferenceSession:
                 cls._call_of(pc.second).args[4])
 
     def _packed_size(self, item) -> int:
+        if isinstance(item, _fuse.GapCall):
+            return 0
         if isinstance(item, _fuse.PairCall):
             return int(self._lib.cm_conv_pair_packed_size(*self._pair_args(item)))
         call = self._call_of(item)
@@ -159,7 +168,7 @@ class InferenceSession:
         return int(self._lib.cm_conv_packed_size(*call.args))
 
     def _workspace_need(self, item) -> int:
-        if isinstance(item, _fuse.PairCall):
+        if isinstance(item, (_fuse.PairCall, _fuse.GapCall)):
             return 0
         call = item.call if isinstance(item, _fuse.FusedCall) else item
         if call.kernel in ("matmul", "matmul_at"):
@@ -173,6 +182,14 @@ class InferenceSession:
         packed = self._packed.get(index)
         if packed is not None:   # packed weights in place of the weight tensor, no workspace
             ws = ()
+        if isinstance(item, _fuse.GapCall):
+            ca = item.call
+            a = ca.args
+            name = "cm_conv_gap"
+            args = (self.device_ptr(ca.tensors[0]), self.device_ptr(ca.tensors[1]),
+                    self.device_ptr(ca.tensors[2]) if a[15] else None, self.device_ptr(item.out),
+                    a[0], a[1], a[2] * a[3], a[4], item.act)
+            return getattr(self._lib, name), name, args, None
         if isinstance(item, _fuse.PairCall):
             ca, cb = item.call, self._call_of(item.second)
             epi = None

@@ -243,6 +243,21 @@ int cm_conv_pair_packed_ex(const int16_t *x, const void *packed, const int16_t *
                            uint32_t dilation, uint32_t pad_top, uint32_t pad_left, uint32_t out_ch,
                            uint32_t act1, const cm_epilogue_t *epi2, hipStream_t stream);
 
+/* A 1x1 convolution (stride 1, no padding, optional bias), its activation
+ * (act: 0 none, 1 Relu, 2 Clip(0,6)) and a GlobalAveragePool of every output
+ * plane as one launch: y [batch][out_ch] receives what cm_conv_ex (epilogue
+ * act) followed by cm_pool (global average) would write, bit for bit, and the
+ * convolution's output never reaches memory.  No counterpart in the
+ * reference: the scheduler's fusion of a network head (ConvKernel.cpp:171-249
+ * then PoolingKernel.cpp:253-266).  x [batch][in_ch][hw], weight
+ * [out_ch][in_ch].  cm_conv_gap_supported returns 1 for the shapes the fused
+ * kernel takes (hw at most 64, in_ch at most 512), else 0; cm_conv_gap
+ * returns CM_ERR_INVALID for the others. */
+int cm_conv_gap_supported(uint32_t batch, uint32_t in_ch, uint32_t hw, uint32_t out_ch);
+int cm_conv_gap(const int16_t *x, const int16_t *weight, const int16_t *bias, int16_t *y,
+                uint32_t batch, uint32_t in_ch, uint32_t hw, uint32_t out_ch, uint32_t act,
+                hipStream_t stream);
+
 /* cm_matmul_ex for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  No
  * counterpart in the reference.  Same arguments and result as cm_matmul_ex

@@ -674,6 +674,55 @@ def test_conv_pair_rejections():
     assert not pairs_of(g)
 
 
+def test_gap_heads():
+    """A 1x1 convolution (its Clip(0,6) fused) whose output only a GlobalAveragePool
+    reads becomes one GapCall: the MobileNetV2-like head (24 launches -> 23 with the
+    pairs of at most 128 middle channels); its pooled output is live from the
+    convolution (never in the convolution's input slot); the launch list run on the
+    oracle gives the graph's output.  No head when the pooled tensor has another
+    reader, when the convolution is not 1x1, or when the pool is not global."""
+    g = graph(wl.mobilenet_model(batch=2, hw=32))
+    plan = BufferPlan(g, fuse.live_from(BufferPlan(g)))
+    seq = fuse.launch_list(plan, pair_ok=lambda pc: pc.call.args[4] <= 128, gap_ok=lambda gc: True)
+    gaps = [x for x in seq if isinstance(x, fuse.GapCall)]
+    assert len(gaps) == 1 and len(seq) == 23
+    gc = gaps[0]
+    assert gc.act == fuse.ACT_RELU6 and gc.out == "gap" and gc.pool.kernel == "pool"
+    assert gc.call.args[7:9] == (1, 1)
+    assert not fuse._overlap(fuse._span(plan, gc.pool, gc.out), fuse._span(plan, gc.call, gc.call.tensors[0]))
+    assert fuse.launch_list(plan, pair_ok=lambda pc: pc.call.args[4] <= 128, gap_ok=lambda gc: False)[-2:] != seq[-2:]
+    x = wl.mobilenet_input(2, 32)
+    oracle.set_threads(min(os.cpu_count() or 1, 8))
+    got = gs.run_plan(plan, {"X": x}, launches=seq)["Y"]
+    np.testing.assert_array_equal(got, gs.run_plan(BufferPlan(g), {"X": x})["Y"])
+
+    N = ox.make_node
+
+    def model(nodes, out_shape):
+        inits = [ox.from_array(np.full((8, 4, 1, 1), 0.1, np.float32), "W1"),
+                 ox.from_array(np.full((8, 4, 3, 3), 0.1, np.float32), "W3")]
+        gr = ox.make_graph(nodes, "gaps", [ox.value_info("X", [2, 4, 6, 6])],
+                           [ox.value_info("Y", out_shape)], inits)
+        return graph(ox.make_model(gr))
+
+    def gaps_of(gr):
+        pl = BufferPlan(gr, fuse.live_from(BufferPlan(gr)))
+        return [x for x in fuse.launch_list(pl, gap_ok=lambda gc: True) if isinstance(x, fuse.GapCall)]
+
+    conv1 = N("Conv", ["X", "W1"], ["h"], kernel_shape=[1, 1])
+    assert len(gaps_of(model([conv1, N("GlobalAveragePool", ["h"], ["Y"])], [2, 8, 1, 1]))) == 1
+    # the convolution's output has a second reader
+    assert not gaps_of(model([conv1, N("GlobalAveragePool", ["h"], ["p"]),
+                              N("GlobalMaxPool", ["h"], ["q"]), N("Add", ["p", "q"], ["Y"])], [2, 8, 1, 1]))
+    # a 3x3 convolution
+    assert not gaps_of(model([N("Conv", ["X", "W3"], ["h"], kernel_shape=[3, 3], pads=[1, 1, 1, 1]),
+                              N("GlobalAveragePool", ["h"], ["Y"])], [2, 8, 1, 1]))
+    # a windowed average pool, and a global max pool
+    assert not gaps_of(model([conv1, N("AveragePool", ["h"], ["Y"], kernel_shape=[2, 2], strides=[2, 2])],
+                             [2, 8, 3, 3]))
+    assert not gaps_of(model([conv1, N("GlobalMaxPool", ["h"], ["Y"])], [2, 8, 1, 1]))
+
+
 def test_alias_reader_extends_source_lifetime():
     """A tensor read through a reshape alias after the reshape node stays live
     until that read: a tensor produced in between must not take its slot."""
